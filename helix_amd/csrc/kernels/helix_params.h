@@ -1,0 +1,105 @@
+/* helix_params.h -- the structs shared by the C++ runtime and the gfx950
+ * kernels. Plain C so both sides include it; passed by value as kernargs.
+ *
+ * Counterpart of the reference's HelixScanParams (src/kernels/helix_params.h:
+ * 45-110), re-laid for MI355X: strides are int64 (288 GB of HBM admits tensors
+ * past 2^31 elements; per-workgroup bases are formed once in scalar registers
+ * and lane offsets inside a chunk stay 32-bit), and the multipass fields
+ * describe the two-level segment scheme below instead of one scratch slot per
+ * chunk.
+ *
+ * Two-level decomposition of the chunk recurrence S_{c+1} = a_c S_c + dS_c
+ * (a_c = exp(sum of A*dt over chunk c), dS_c = B_c^T (decay . dt . x)_c):
+ *
+ *   Pass A  one workgroup per (seq, segment of seg_len chunks, head, P-slab)
+ *           walks its chunks in order with the partial state held in MFMA
+ *           accumulators. Before folding chunk c in, it stores the in-segment
+ *           prefix R_c (state entering chunk c from this segment's own tokens,
+ *           zero for the first chunk) to `s_local`. At the end it stores the
+ *           segment aggregate D_s to `s_seg` and the log-decays to `ld`/`segld`.
+ *   Pass B  per state element, scans the segments:
+ *           S_seg(s) = carry; carry = exp(segld_s) carry + D_s   (in place)
+ *           and writes the final carry to s1.
+ *   Pass C  per (seq, chunk, group, head block): the state entering chunk c is
+ *           S_init(c) = R_c + exp(ld_c) S_seg(s), assembled while staging;
+ *           y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C S_init).
+ *
+ * Scratch layouts (elements; every region 256-byte aligned):
+ *   s_local [seq][cg][head][P][N]    f32 (fp32 path) or bf16 (bf16 path)
+ *   s_seg   [seq][seg][head][P][N]   f32: D_s from Pass A, S_seg after Pass B
+ *   ld      [seq][cg][head]          f32: sum of chunk log-decays before c
+ *                                         within c's segment
+ *   segld   [seq][seg][head]         f32: whole-segment log-decay
+ * [P][N] is the caller's state layout, so Pass B and s0/s1 coalesce together.
+ */
+#ifndef HELIX_PARAMS_H
+#define HELIX_PARAMS_H
+
+/* Chunk length. 64 tokens = one wave64 lane per token for the decay scan. */
+#define HELIX_CS 64
+/* Head-dim slab width handled by one workgroup. */
+#define HELIX_HD 64
+/* Largest d_state served (padded up to 64 / 128 / 256 inside the kernels). */
+#define HELIX_N_MAX 256
+/* Threads per workgroup: four wave64s, one per SIMD of a CU. */
+#define HELIX_WG 256
+
+typedef struct HelixScanParams {
+    int n_tok;
+    int n_seq;
+    int n_head;
+    int head_dim;
+    int d_state;
+    int n_group;
+    int heads_per_group;
+    int n_pslab;          /* ceil(head_dim / HELIX_HD) */
+
+    /* Element strides, as in helix_scan_desc. */
+    long long s_x[3], seq_x;
+    long long s_b[3], seq_b;
+    long long s_c[3], seq_c;
+    long long s_dt[2], seq_dt;
+    long long s_s[3], seq_s;
+    long long s_y[3], seq_y;
+    long long s_a;
+
+    int   has_ids;
+    int   first_group;    /* 1 => Pass B carries in from s0 (through ids), else s1 */
+    float dt_min;
+    float dt_max;
+
+    /* Super-chunk group currently encoded. */
+    int chunk_base;       /* global index of the group's first chunk */
+    int n_cg;             /* chunks in this group */
+    int seg_len;          /* chunks per segment */
+    int n_seg;            /* segments in this group = ceil(n_cg / seg_len) */
+    int hblk;             /* heads per Pass C workgroup */
+    int n_hblk;           /* head blocks per B/C group */
+    int pad0, pad1;
+
+    /* Scratch strides in elements (see the layout comment above). */
+    long long sl_cg, sl_seq;     /* s_local: chunk stride (H*P*N), seq stride */
+    long long sg_seg, sg_seq;    /* s_seg: segment stride (H*P*N), seq stride */
+    long long ld_seq;            /* ld: seq stride (n_cg_max * H); chunk stride H */
+    long long sd_seq;            /* segld: seq stride (n_seg_max * H); seg stride H */
+} HelixScanParams;
+
+/* Device pointers for one encode. s_local is float* on the fp32 path and a
+ * bf16 array on the bf16 path. */
+typedef struct HelixScanBuffers {
+    const float* s0;
+    const float* x;
+    const float* dt;
+    const float* A;
+    const float* B;
+    const float* C;
+    const int*   ids;
+    float*       y;
+    float*       s1;
+    void*        s_local;
+    float*       s_seg;
+    float*       ld;
+    float*       segld;
+} HelixScanBuffers;
+
+#endif /* HELIX_PARAMS_H */

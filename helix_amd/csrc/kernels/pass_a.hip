@@ -1,0 +1,158 @@
+// pass_a.hip -- Pass A: chunk-state GEMM on fp32 MFMA, walked over a segment.
+//
+// Reference counterpart: helix_chunk_state_f32 (src/kernels/
+// helix_scan_multipass.metal:51-149), which computes one chunk's
+//     dS[n][c] = sum_j B[j][n] * exp(L_end - Lcum_j) * dt_j * x[j][c]
+// per threadgroup and leaves the chunk-to-chunk recurrence to Pass B.
+//
+// Here one workgroup owns (seq, segment, head, 64-wide P slab) and walks the
+// segment's chunks in order, keeping the running state in MFMA accumulators:
+//     store R_c            (state entering chunk c from this segment; c > first)
+//     R <- exp(L_end_c) R + B_c^T . (decay . dt . x)_c
+// so the per-chunk states reach HBM once (s_local) instead of three times,
+// and only the segment aggregates D_s go through Pass B.
+//
+// Tiling: the workgroup computes R^T[p][n] (64 x N) with v_mfma_f32_32x32x2_f32,
+// M = p, N = n, K = token. Wave w owns P tile (w & 1) and N tiles
+// (w >> 1) + 2i, so the A operand is loaded once per K step and reused across
+// its N tiles. Both operands come from LDS in their natural row-major staging
+// (dtXs[j][p], B[j][n]); R^T tiles store as 128-byte rows of the [P][N] layout.
+#include "helix_common.h"
+
+template <int NP, bool SBF>
+__device__ __forceinline__ void store_state_tiles(const f32x16* acc, void* dst_base, int pw, int N,
+                                                  int pt, int nt0, int lo, int hi) {
+    constexpr int NTW = NP / 64;
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) {
+        const int n = (nt0 + 2 * i) * 32 + lo;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int pr = pt * 32 + acc_row(r, hi);
+            if (pr < pw && n < N) {
+                const long long off = (long long)pr * N + n;
+                if (SBF)
+                    static_cast<__bf16*>(dst_base)[off] = to_bf16(acc[i][r]);
+                else
+                    static_cast<float*>(dst_base)[off] = acc[i][r];
+            }
+        }
+    }
+}
+
+template <int NP, bool SBF>
+__device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int NTW = NP / 64;      // N tiles per wave (NP/32 tiles over 2 waves)
+    constexpr int RSX = HELIX_HD;     // row stride of dtXs
+    constexpr int RSB = NP;           // row stride of B
+    __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * RSX];
+    __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+
+    const int seg  = blockIdx.x;
+    const int h    = blockIdx.y;
+    const int slab = blockIdx.z % p.n_pslab;
+    const int seq  = blockIdx.z / p.n_pslab;
+    const int p0   = slab * HELIX_HD;
+    const int pw   = min(HELIX_HD, p.head_dim - p0);
+    const int N    = p.d_state;
+    const int P    = p.head_dim;
+    const int g    = h / p.heads_per_group;
+
+    const int c_begin = seg * p.seg_len;
+    const int c_end   = min(c_begin + p.seg_len, p.n_cg);
+    if (c_begin >= c_end) return;
+
+    const float A_h = b.A[(long long)h * p.s_a];
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
+
+    const long long head_off = (long long)h * P * N + (long long)p0 * N;
+    char* sl_base = static_cast<char*>(b.s_local) +
+                    (seq * p.sl_seq + head_off) * (SBF ? 2 : 4);
+
+    const int pt  = wave & 1;
+    const int nt0 = wave >> 1;
+
+    f32x16 acc[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) acc[i] = zero16();
+    float lam = 0.0f;  // log-decay accumulated over this segment before chunk c
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int t0   = (p.chunk_base + c) * HELIX_CS;
+        const int tlen = min(HELIX_CS, p.n_tok - t0);
+
+        const ChunkDecay cd = chunk_decay(p, dt_h, t0, tlen, A_h);
+        const float sdec = (lane < tlen) ? exp_diff(cd.lend, cd.lcum) : 0.0f;
+        const float cf   = sdec * cd.dtv;
+
+        // dtXs[j][p] = exp(L_end - Lcum_j) dt_j x[j][p]; rows past tlen and
+        // columns past the slab are zero.
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+            const float cj = bcast(cf, j);
+            float v = 0.0f;
+            if (j < tlen && lane < pw) v = cj * x_h[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
+            sX[j * RSX + lane] = v;
+        }
+        // B chunk, zero-padded past tlen and past d_state.
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+            const float* brow = B_g + (long long)(t0 + j) * p.s_b[0];
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int n = lane + 64 * m;
+                float v = 0.0f;
+                if (j < tlen && n < N) v = brow[n];
+                sB[j * RSB + n] = v;
+            }
+        }
+
+        if (c > c_begin)
+            store_state_tiles<NP, SBF>(acc, sl_base + (long long)c * p.sl_cg * (SBF ? 2 : 4),
+                                       pw, N, pt, nt0, lo, hi);
+        if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
+        __syncthreads();
+
+        const float a_c = expf((float)cd.lend);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) acc[i] *= a_c;
+
+#pragma unroll 4
+        for (int s = 0; s < HELIX_CS / 2; ++s) {
+            const int j = 2 * s + hi;
+            const float av = sX[j * RSX + pt * 32 + lo];
+#pragma unroll
+            for (int i = 0; i < NTW; ++i) {
+                const float bv = sB[j * RSB + (nt0 + 2 * i) * 32 + lo];
+                acc[i] = mfma_f32(av, bv, acc[i]);
+            }
+        }
+        lam += (float)cd.lend;
+        __syncthreads();
+    }
+
+    float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + head_off;
+    store_state_tiles<NP, false>(acc, sg, pw, N, pt, nt0, lo, hi);
+    if (slab == 0 && tid == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
+}
+
+#define HELIX_PASS_A(NP)                                                                        \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_f32_n##NP(          \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_impl<NP, false>(p, b);                                                      \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_sbf_n##NP(          \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_impl<NP, true>(p, b);                                                       \
+    }
+
+HELIX_PASS_A(64)
+HELIX_PASS_A(128)
+HELIX_PASS_A(256)

@@ -1,0 +1,182 @@
+// pass_c_bf16.hip -- Pass C on bf16 MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// Reference counterpart: helix_chunk_out_mpp_impl<K> (src/kernels/mpp/
+// helix_scan_mpp.metal:54-232): same G1/G2/G3 algebra as the fp32 Pass C with
+// bf16 GEMM operands and fp32 accumulators; Lcum, exp, the carried state and
+// the output stay fp32.
+//
+// The reference needs a separate cast pass (helix_cast.metal:19-46) to give
+// MPP dense bf16 copies of B and C in device memory. Here B and C are read
+// once in fp32 and rounded to bf16 (round-to-nearest-even) while they are
+// staged into LDS, so the cast costs no extra HBM pass; rows past the end of
+// the sequence are staged as zeros, which is what the cast pass's padding did.
+//
+// Every operand is stored k-contiguous in LDS so each lane fetches its eight
+// bf16 K values with one 16-byte read:
+//   C[t][n], B[j][n]   (K = n for G1 and G3)
+//   M[t][j], dtX^T[p][j]  (K = j for G2)
+//   S^T[p][n]          (K = n for G3; s_local is already [P][N])
+#include "helix_common.h"
+
+template <int NP>
+__device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int RS  = NP + 8;          // bf16 row stride of C, B, S^T (16-byte aligned rows)
+    constexpr int RSJ = HELIX_CS + 8;    // bf16 row stride of M and dtX^T
+    constexpr int RSCB = HELIX_CS + 1;   // fp32 row stride of CB
+
+    __shared__ __attribute__((aligned(16))) __bf16 sC[HELIX_CS * RS];
+    __shared__ __attribute__((aligned(16))) __bf16 sBS[HELIX_CS * RS];   // B for G1, then S^T
+    __shared__ __attribute__((aligned(16))) __bf16 sM[HELIX_CS * RSJ];
+    __shared__ __attribute__((aligned(16))) __bf16 sXt[HELIX_HD * RSJ];
+    __shared__ __attribute__((aligned(16))) float sCB[HELIX_CS * RSCB];
+    __shared__ __attribute__((aligned(16))) float sE[HELIX_CS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+
+    const int cg  = blockIdx.x;
+    const int g   = blockIdx.y / p.n_hblk;
+    const int hb  = blockIdx.y % p.n_hblk;
+    const int seq = blockIdx.z;
+    const int t0   = (p.chunk_base + cg) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int N = p.d_state, P = p.head_dim;
+    const int seg = cg / p.seg_len;
+    const int cis = cg % p.seg_len;
+
+    const int h_begin = g * p.heads_per_group + hb * p.hblk;
+    const int h_end   = min(h_begin + p.hblk, (g + 1) * p.heads_per_group);
+    if (h_begin >= h_end) return;
+
+    // ---- stage C and B as bf16 ----------------------------------------------
+    {
+        const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
+        const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int n = lane + 64 * m;
+                float vc = 0.0f, vb = 0.0f;
+                if (j < tlen && n < N) {
+                    vc = C_g[(long long)j * p.s_c[0] + n];
+                    vb = B_g[(long long)j * p.s_b[0] + n];
+                }
+                sC[j * RS + n]  = to_bf16(vc);
+                sBS[j * RS + n] = to_bf16(vb);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- G1: CB tiles (0,0), (1,0), (1,1) on waves 0..2 ----------------------
+    if (wave < 3) {
+        const int tb = wave == 0 ? 0 : 1;
+        const int jb = wave == 2 ? 1 : 0;
+        f32x16 acc = zero16();
+#pragma unroll 4
+        for (int s = 0; s < NP / 16; ++s) {
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sC[(tb * 32 + lo) * RS + 16 * s + 8 * hi]);
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sBS[(jb * 32 + lo) * RS + 16 * s + 8 * hi]);
+            acc = mfma_bf16(av, bv, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = tb * 32 + acc_row(r, hi);
+            const int j = jb * 32 + lo;
+            sCB[t * RSCB + j] = (j <= t) ? acc[r] : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    const int tb = wave >> 1, pb = wave & 1;
+    const float* __restrict__ x_s  = b.x + seq * p.seq_x;
+    const float* __restrict__ dt_s = b.dt + seq * p.seq_dt;
+    const __bf16* __restrict__ sl_s = static_cast<const __bf16*>(b.s_local) + seq * p.sl_seq + (long long)cg * p.sl_cg;
+    const float* __restrict__ sg_s = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg;
+
+    for (int h = h_begin; h < h_end; ++h) {
+        const float A_h = b.A[(long long)h * p.s_a];
+        const ChunkDecay cd = chunk_decay(p, dt_s + h * p.s_dt[1], t0, tlen, A_h);
+        const float es = expf(b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h]);
+        const long long head_off = (long long)h * P * N;
+
+        for (int slab = 0; slab < p.n_pslab; ++slab) {
+            const int p0 = slab * HELIX_HD;
+            const int pw = min(HELIX_HD, P - p0);
+
+            // dtX^T[p][j] (bf16)
+            const float* xh = x_s + h * p.s_x[1] + p0 * p.s_x[2];
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int j = wave + 4 * i;
+                const float dj = bcast(cd.dtv, j);
+                float v = 0.0f;
+                if (j < tlen && lane < pw) v = dj * xh[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
+                sXt[lane * RSJ + j] = to_bf16(v);
+            }
+            // M[t][j] (bf16), zero above the diagonal.
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int t = wave + 4 * i;
+                const double lt = bcast(cd.lcum, t);
+                const float m = (lane <= t) ? sCB[t * RSCB + lane] * exp_diff(lt, cd.lcum) : 0.0f;
+                sM[t * RSJ + lane] = to_bf16(m);
+            }
+            if (wave == 0) sE[lane] = expf((float)cd.lcum);
+            // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16.
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int pr = wave + 4 * i;
+#pragma unroll
+                for (int m = 0; m < NP / 64; ++m) {
+                    const int n = lane + 64 * m;
+                    float v = 0.0f;
+                    if (pr < pw && n < N) {
+                        const long long off = head_off + (long long)(p0 + pr) * N + n;
+                        v = es * sg_s[off];
+                        if (cis > 0) v += (float)sl_s[off];
+                    }
+                    sBS[pr * RS + n] = to_bf16(v);
+                }
+            }
+            __syncthreads();
+
+            // G3, row scale, G2.
+            f32x16 acc = zero16();
+#pragma unroll 4
+            for (int s = 0; s < NP / 16; ++s) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sC[(tb * 32 + lo) * RS + 16 * s + 8 * hi]);
+                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sBS[(pb * 32 + lo) * RS + 16 * s + 8 * hi]);
+                acc = mfma_bf16(av, bv, acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
+            for (int s = 0; s < 2 * (tb + 1); ++s) {
+                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sM[(tb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
+                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sXt[(pb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
+                acc = mfma_bf16(av, bv, acc);
+            }
+
+            float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
+            const int pp = pb * 32 + lo;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = tb * 32 + acc_row(r, hi);
+                if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
+            }
+            __syncthreads();
+        }
+    }
+}
+
+#define HELIX_PASS_C_BF16(NP)                                                                   \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_out_bf16_n##NP(           \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_out_bf16_impl<NP>(p, b);                                                          \
+    }
+
+HELIX_PASS_C_BF16(64)
+HELIX_PASS_C_BF16(128)
+HELIX_PASS_C_BF16(256)

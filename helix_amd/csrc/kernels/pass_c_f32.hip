@@ -1,0 +1,211 @@
+// pass_c_f32.hip -- Pass C on fp32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// Reference counterpart: helix_chunk_out_f32 (src/kernels/
+// helix_scan_multipass.metal:225-361):
+//   G1  CB = C . B^T, causal tiles only, masked          (64 x 64, K = N)
+//   G2  y_intra = (CB . exp(Lcum_t - Lcum_j)) . dtX      (64 x 64, K = 64)
+//   G3  y_inter = C . S_init                             (64 x 64, K = N)
+//   y   = y_intra + exp(Lcum_t) . y_inter
+//
+// MI355X layout: one workgroup per (seq, chunk, B/C group, head block). CB
+// depends only on (seq, chunk, group), so G1 runs once and is reused by every
+// head of the block instead of once per head. Then for each (head, P slab):
+//   - S_init = R_c + exp(ld_c) S_seg(s) is assembled while staging (the two
+//     halves of the two-level scan produced by Passes A and B),
+//   - G3 accumulates straight into the output tile, the rows are scaled by
+//     exp(Lcum_t), and G2 accumulates on top, so y leaves in one store.
+// The chunk's C stays resident in LDS for every head; B is only needed for
+// G1 and its LDS is recycled for S_init / dtX / M.
+//
+// Waves: wave w owns output tile (t block w >> 1, P block w & 1). G2 skips
+// the all-zero upper tile (t block 0 only reads j < 32). Rows past tlen are
+// zero in C and B and clamped in Lcum, so the ragged last chunk takes the
+// same path (reference helix_pad.metal:1-46 does this with a padded copy;
+// here the padding happens during staging).
+#include "helix_common.h"
+
+template <int NP>
+__device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int KS  = NP > 128 ? 128 : NP;  // S_init staged in K blocks of KS
+    constexpr int NKB = NP / KS;
+    constexpr int RSC = NP + 1;               // odd strides: 32 rows x 1 column reads
+    constexpr int RSS = KS + 1;
+    constexpr int RSM = HELIX_CS + 1;
+    constexpr int RSX = HELIX_HD;
+
+    constexpr int SZ_C  = HELIX_CS * RSC;
+    constexpr int SZ_B  = HELIX_CS * RSC;
+    constexpr int SZ_S  = HELIX_HD * RSS;
+    constexpr int SZ_X  = HELIX_CS * RSX;
+    constexpr int SZ_M  = HELIX_CS * RSM;
+    constexpr int SZ_R  = (SZ_B > SZ_S + SZ_X + SZ_M) ? SZ_B : (SZ_S + SZ_X + SZ_M);
+    constexpr int OFF_R = SZ_C;
+    constexpr int OFF_CB = OFF_R + SZ_R;
+    constexpr int OFF_E  = OFF_CB + HELIX_CS * RSM;
+    constexpr int TOTAL  = OFF_E + HELIX_CS;
+    __shared__ __attribute__((aligned(16))) float lds[TOTAL];
+    float* sC  = lds;
+    float* sB  = lds + OFF_R;            // G1 only
+    float* sS  = lds + OFF_R;            // S_init[p][k] block, after G1
+    float* sX  = sS + SZ_S;              // dtX[j][p]
+    float* sM  = sX + SZ_X;              // M[t][j] = CB[t][j] exp(Lcum_t - Lcum_j)
+    float* sCB = lds + OFF_CB;           // masked CB[t][j]
+    float* sE  = lds + OFF_E;            // exp(Lcum_t)
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+
+    const int cg  = blockIdx.x;
+    const int g   = blockIdx.y / p.n_hblk;
+    const int hb  = blockIdx.y % p.n_hblk;
+    const int seq = blockIdx.z;
+    const int t0   = (p.chunk_base + cg) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int N = p.d_state, P = p.head_dim;
+    const int seg = cg / p.seg_len;
+    const int cis = cg % p.seg_len;
+
+    const int h_begin = g * p.heads_per_group + hb * p.hblk;
+    const int h_end   = min(h_begin + p.hblk, (g + 1) * p.heads_per_group);
+    if (h_begin >= h_end) return;
+
+    // ---- stage C and B of this (seq, chunk, group) ---------------------------
+    {
+        const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
+        const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int n = lane + 64 * m;
+                float vc = 0.0f, vb = 0.0f;
+                if (j < tlen && n < N) {
+                    vc = C_g[(long long)j * p.s_c[0] + n];
+                    vb = B_g[(long long)j * p.s_b[0] + n];
+                }
+                sC[j * RSC + n] = vc;
+                sB[j * RSC + n] = vb;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- G1: CB tiles (0,0), (1,0), (1,1) on waves 0..2 ----------------------
+    if (wave < 3) {
+        const int tb = wave == 0 ? 0 : 1;
+        const int jb = wave == 2 ? 1 : 0;
+        f32x16 acc = zero16();
+#pragma unroll 8
+        for (int s = 0; s < NP / 2; ++s) {
+            const float av = sC[(tb * 32 + lo) * RSC + 2 * s + hi];
+            const float bv = sB[(jb * 32 + lo) * RSC + 2 * s + hi];
+            acc = mfma_f32(av, bv, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = tb * 32 + acc_row(r, hi);
+            const int j = jb * 32 + lo;
+            sCB[t * RSM + j] = (j <= t) ? acc[r] : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    const int tb = wave >> 1, pb = wave & 1;
+    const float* __restrict__ x_s  = b.x + seq * p.seq_x;
+    const float* __restrict__ dt_s = b.dt + seq * p.seq_dt;
+    const float* __restrict__ sl_s = static_cast<const float*>(b.s_local) + seq * p.sl_seq + (long long)cg * p.sl_cg;
+    const float* __restrict__ sg_s = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg;
+
+    for (int h = h_begin; h < h_end; ++h) {
+        const float A_h = b.A[(long long)h * p.s_a];
+        const ChunkDecay cd = chunk_decay(p, dt_s + h * p.s_dt[1], t0, tlen, A_h);
+        const float es = expf(b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h]);
+        const long long head_off = (long long)h * P * N;
+
+        for (int slab = 0; slab < p.n_pslab; ++slab) {
+            const int p0 = slab * HELIX_HD;
+            const int pw = min(HELIX_HD, P - p0);
+
+            // dtX[j][p]
+            const float* xh = x_s + h * p.s_x[1] + p0 * p.s_x[2];
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int j = wave + 4 * i;
+                const float dj = bcast(cd.dtv, j);
+                float v = 0.0f;
+                if (j < tlen && lane < pw) v = dj * xh[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
+                sX[j * RSX + lane] = v;
+            }
+            // M[t][j] for this head; lane = j, so Lcum_j is this lane's own.
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int t = wave + 4 * i;
+                const double lt = bcast(cd.lcum, t);
+                sM[t * RSM + lane] = (lane <= t) ? sCB[t * RSM + lane] * exp_diff(lt, cd.lcum) : 0.0f;
+            }
+            if (wave == 0) sE[lane] = expf((float)cd.lcum);
+
+            f32x16 acc = zero16();
+            for (int kb = 0; kb < NKB; ++kb) {
+                // S_init[p][k] = R_c + exp(ld_c) S_seg, zero past the slab and d_state.
+#pragma unroll 4
+                for (int i = 0; i < 16; ++i) {
+                    const int pr = wave + 4 * i;
+#pragma unroll
+                    for (int m = 0; m < KS / 64; ++m) {
+                        const int k = lane + 64 * m;
+                        const int n = kb * KS + k;
+                        float v = 0.0f;
+                        if (pr < pw && n < N) {
+                            const long long off = head_off + (long long)(p0 + pr) * N + n;
+                            v = es * sg_s[off];
+                            if (cis > 0) v += sl_s[off];
+                        }
+                        sS[pr * RSS + k] = v;
+                    }
+                }
+                __syncthreads();
+                // G3 partial: y += C[:, kblock] . S_init[kblock, :]
+#pragma unroll 8
+                for (int s = 0; s < KS / 2; ++s) {
+                    const float av = sC[(tb * 32 + lo) * RSC + kb * KS + 2 * s + hi];
+                    const float bv = sS[(pb * 32 + lo) * RSS + 2 * s + hi];
+                    acc = mfma_f32(av, bv, acc);
+                }
+                if (kb + 1 < NKB) __syncthreads();
+            }
+
+            // rows scaled by exp(Lcum_t), then G2 on top.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
+            const int ksteps = 16 * (tb + 1);
+#pragma unroll 8
+            for (int s = 0; s < ksteps; ++s) {
+                const int j = 2 * s + hi;
+                const float av = sM[(tb * 32 + lo) * RSM + j];
+                const float bv = sX[j * RSX + pb * 32 + lo];
+                acc = mfma_f32(av, bv, acc);
+            }
+
+            float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
+            const int pp = pb * 32 + lo;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = tb * 32 + acc_row(r, hi);
+                if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
+            }
+            __syncthreads();
+        }
+    }
+}
+
+#define HELIX_PASS_C_F32(NP)                                                                    \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_out_f32_n##NP(            \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_out_f32_impl<NP>(p, b);                                                           \
+    }
+
+HELIX_PASS_C_F32(64)
+HELIX_PASS_C_F32(128)
+HELIX_PASS_C_F32(256)

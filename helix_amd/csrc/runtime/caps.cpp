@@ -1,0 +1,273 @@
+// caps.cpp -- shape gate, backend selection, scratch planning, params packing.
+//
+// Counterpart of the reference's src/runtime/caps.mm:1-306. The contract is
+// the same: helix_scan_supported() == false means the caller keeps its own
+// kernel, selection never fails, and helix_scan_scratch_size() agrees exactly
+// with what the encoder lays out. Everything here is plain C++ and runs
+// without a GPU (ctx may be a host-only context or null for planning).
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "helix_internal.h"
+
+namespace {
+
+// The fp32 path: all three passes on v_mfma_f32_32x32x2_f32 (FP32 matrix and
+// FP32 vector peaks are both 157.3 TFLOP/s on MI355X; the matrix path keeps
+// the operands in LDS/registers instead of spending VALU issue slots).
+constexpr HelixMatmulTraits kF32Traits[] = {
+    {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=64)", "helix_chunk_state_f32_n64",
+     "helix_state_scan_f32", "helix_chunk_out_f32_n64", false,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 64},
+    {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=128)", "helix_chunk_state_f32_n128",
+     "helix_state_scan_f32", "helix_chunk_out_f32_n128", false,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 128},
+    {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=256)", "helix_chunk_state_f32_n256",
+     "helix_state_scan_f32", "helix_chunk_out_f32_n256", false,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 256},
+};
+
+// The bf16 path (the reference's MPP slot): Pass C on v_mfma_f32_32x32x16_bf16
+// with fp32 accumulators; Passes A and B stay fp32, so the carried state and
+// s1 keep fp32 accuracy. The per-chunk state Pass C reads is stored as bf16.
+constexpr HelixMatmulTraits kBf16Traits[] = {
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=64)", "helix_chunk_state_sbf_n64",
+     "helix_state_scan_f32", "helix_chunk_out_bf16_n64", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 64},
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=128)", "helix_chunk_state_sbf_n128",
+     "helix_state_scan_f32", "helix_chunk_out_bf16_n128", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 128},
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=256)", "helix_chunk_state_sbf_n256",
+     "helix_state_scan_f32", "helix_chunk_out_bf16_n256", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256},
+};
+
+const char* const kKernelNames[] = {
+    "helix_chunk_state_f32_n64",  "helix_chunk_state_f32_n128", "helix_chunk_state_f32_n256",
+    "helix_chunk_state_sbf_n64",  "helix_chunk_state_sbf_n128", "helix_chunk_state_sbf_n256",
+    "helix_state_scan_f32",
+    "helix_chunk_out_f32_n64",    "helix_chunk_out_f32_n128",   "helix_chunk_out_f32_n256",
+    "helix_chunk_out_bf16_n64",   "helix_chunk_out_bf16_n128",  "helix_chunk_out_bf16_n256",
+};
+
+int np_index(int d_state) {
+    if (d_state <= 64) return 0;
+    if (d_state <= 128) return 1;
+    return 2;
+}
+
+// Workgroup counts the planner aims for: 256 CUs with a few resident
+// workgroups each, so a launch fills the chip with a short tail.
+constexpr long kTargetWgA = 1024;
+constexpr long kTargetWgC = 2048;
+
+long env_long(const char* name, long dflt) {
+    if (const char* v = std::getenv(name)) {
+        char* end = nullptr;
+        const long x = std::strtol(v, &end, 10);
+        if (end != v && x > 0) return x;
+    }
+    return dflt;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+thread_local std::string t_last_error;
+thread_local const helix_ctx* t_last_ctx = nullptr;
+
+}  // namespace
+
+namespace helix::rt {
+
+const char* const* all_kernel_names(size_t* count) {
+    *count = sizeof(kKernelNames) / sizeof(kKernelNames[0]);
+    return kKernelNames;
+}
+
+void set_error(const helix_ctx* ctx, const std::string& msg) {
+    t_last_ctx = ctx;
+    t_last_error = msg;
+}
+
+const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d) {
+    (void)ctx;
+    const int k = np_index(d.d_state);
+    // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
+    if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
+        if (f[0] == 's') return kF32Traits[k];
+    const bool want_bf16 = d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP;
+    if (want_bf16 && d.multipass) return kBf16Traits[k];
+    return kF32Traits[k];
+}
+
+size_t scratch_budget_bytes() {
+    // Default sized for MI355X's 288 GB: a 64-head 8K-token prefill keeps all
+    // of its chunks in one group. $HELIX_SCRATCH_MB=1 forces many groups.
+    return (size_t)env_long("HELIX_SCRATCH_MB", 2048) << 20;
+}
+
+namespace {
+
+// Chunks per segment for a group of `cpg` chunks: enough segments that Pass A
+// has ~kTargetWgA workgroups, and no more (a longer walk keeps more of the
+// chunk recurrence in registers and shortens Pass B).
+int choose_seg_len(const helix_scan_desc& d, int cpg) {
+    if (const char* v = std::getenv("HELIX_SEG_LEN")) {
+        const long x = std::strtol(v, nullptr, 10);
+        if (x > 0) return (int)std::min<long>(x, cpg);
+    }
+    const long n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
+    const long items = (long)d.n_seq * d.n_head * n_pslab;
+    const long segs = std::max<long>(1, (kTargetWgA + items - 1) / items);
+    const long len = (cpg + segs - 1) / segs;
+    return (int)std::max<long>(1, std::min<long>(len, cpg));
+}
+
+void layout(const helix_scan_desc& d, bool bf16_state, int cpg, MultipassPlan* pl) {
+    const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
+    pl->chunks_per_group = cpg;
+    pl->seg_len = choose_seg_len(d, cpg);
+    pl->segs_per_group = (cpg + pl->seg_len - 1) / pl->seg_len;
+    pl->sl_elem_bytes = bf16_state ? 2 : 4;
+    pl->sl_elems = pl->seg_len > 1 ? state * (size_t)cpg : 0;
+    pl->sg_elems = state * (size_t)pl->segs_per_group;
+    pl->ld_elems = (size_t)d.n_seq * cpg * d.n_head;
+    pl->sd_elems = (size_t)d.n_seq * pl->segs_per_group * d.n_head;
+    size_t off = 0;
+    pl->off_sl = off; off += align256(pl->sl_elems * pl->sl_elem_bytes);
+    pl->off_sg = off; off += align256(pl->sg_elems * sizeof(float));
+    pl->off_ld = off; off += align256(pl->ld_elems * sizeof(float));
+    pl->off_sd = off; off += align256(pl->sd_elems * sizeof(float));
+    pl->total_bytes = off;
+}
+
+}  // namespace
+
+MultipassPlan plan_multipass(const helix_scan_desc& d, bool bf16_state) {
+    MultipassPlan pl;
+    if (d.n_tok <= 0 || d.n_seq <= 0 || d.n_head <= 0 || d.head_dim <= 0 || d.d_state <= 0 ||
+        d.n_group <= 0)
+        return pl;
+    pl.n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
+
+    const size_t budget = scratch_budget_bytes();
+    const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
+    const size_t per_chunk = state * (bf16_state ? 2 : 4);
+    long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
+    cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
+    for (;;) {
+        layout(d, bf16_state, (int)cpg, &pl);
+        if (pl.total_bytes <= budget || cpg == 1) break;
+        cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
+    }
+    pl.n_groups = (pl.n_chunks + pl.chunks_per_group - 1) / pl.chunks_per_group;
+
+    // Pass C head blocks: share C.B^T over as many heads as possible while
+    // keeping ~kTargetWgC workgroups per group launch.
+    const int hpg = d.n_head / std::max(1, d.n_group);
+    const long base = (long)d.n_seq * pl.chunks_per_group * d.n_group;
+    long want_blocks = std::max<long>(1, (kTargetWgC + base - 1) / base);
+    if (const char* v = std::getenv("HELIX_HBLK")) {
+        const long x = std::strtol(v, nullptr, 10);
+        if (x > 0) want_blocks = (hpg + x - 1) / x;
+    }
+    want_blocks = std::min<long>(want_blocks, hpg);
+    pl.hblk = (int)((hpg + want_blocks - 1) / want_blocks);
+    pl.n_hblk = (hpg + pl.hblk - 1) / pl.hblk;
+    return pl;
+}
+
+bool build_params(const helix_scan_desc& d, HelixScanParams* o, std::string* why) {
+    std::memset(o, 0, sizeof(*o));
+    o->n_tok = d.n_tok;
+    o->n_seq = d.n_seq;
+    o->n_head = d.n_head;
+    o->head_dim = d.head_dim;
+    o->d_state = d.d_state;
+    o->n_group = d.n_group;
+    o->heads_per_group = d.n_head / d.n_group;
+    o->n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
+    for (int i = 0; i < 3; ++i) {
+        o->s_x[i] = d.s_x[i];
+        o->s_b[i] = d.s_b[i];
+        o->s_c[i] = d.s_c[i];
+        o->s_s[i] = d.s_s[i];
+        o->s_y[i] = d.s_y[i];
+    }
+    o->s_dt[0] = d.s_dt[0];
+    o->s_dt[1] = d.s_dt[1];
+    o->seq_x = d.seq_x;
+    o->seq_b = d.seq_b;
+    o->seq_c = d.seq_c;
+    o->seq_dt = d.seq_dt;
+    o->seq_s = d.seq_s;
+    o->seq_y = d.seq_y;
+    o->s_a = d.s_a;
+    o->dt_min = d.dt_min;
+    o->dt_max = d.dt_max;
+
+    // Grid y and z are 16-bit on the hardware dispatch packet.
+    const long kMaxYZ = 65535;
+    const long zA = (long)d.n_seq * o->n_pslab;
+    if (d.n_head > kMaxYZ || zA > kMaxYZ || d.n_seq > kMaxYZ || (long)d.n_head > kMaxYZ) {
+        if (why) *why = "launch grid exceeds 65535 in y or z (n_head or n_seq*n_pslab too large)";
+        return false;
+    }
+    return true;
+}
+
+}  // namespace helix::rt
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" const char* helix_ctx_last_error(const helix_ctx* ctx) {
+    if (!ctx) return t_last_ctx == nullptr && !t_last_error.empty() ? t_last_error.c_str() : "null context";
+    return t_last_ctx == ctx ? t_last_error.c_str() : "";
+}
+
+extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
+    if (!ctx || !d) return false;
+    if (d->n_tok <= 0 || d->n_seq <= 0 || d->n_head <= 0 || d->head_dim <= 0 ||
+        d->d_state <= 0 || d->n_group <= 0)
+        return false;
+    if (d->n_head % d->n_group != 0) return false;
+    // The chunked reassociation needs one decay scalar per (head, token).
+    if (d->a_form != HELIX_A_SCALAR_PER_HEAD) return false;
+    // fp16/bf16 storage is not served; bf16 compute is chosen by backend.
+    if (d->io_dtype != HELIX_F32 || d->compute_dtype != HELIX_F32) return false;
+    if (d->d_state % 8 != 0 || d->head_dim % 8 != 0) return false;
+    if (d->d_state > HELIX_N_MAX) return false;
+    // B, C rows and state rows are staged as contiguous d_state vectors.
+    if (d->s_b[2] != 1 || d->s_c[2] != 1 || d->s_s[2] != 1) return false;
+    if (d->s_s[1] != d->d_state) return false;
+    if (d->chunk != 0 && d->chunk != HELIX_CS) return false;
+    // Only the three-pass path is built; a single-pass request is declined so
+    // the caller keeps its own kernel (helix.h: false => fall back).
+    if (!d->multipass) return false;
+    if (d->backend == HELIX_BACKEND_REF) return false;
+    HelixScanParams unused;
+    return helix::rt::build_params(*d, &unused, nullptr);
+}
+
+extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
+    if (!d || !d->multipass) return 0;
+    const bool bf16 = helix::rt::select_traits(ctx, *d).bf16_state;
+    return helix::rt::plan_multipass(*d, bf16).total_bytes;
+}
+
+extern "C" helix_backend helix_ctx_select_backend(helix_ctx* ctx, const helix_scan_desc* d) {
+    if (!ctx || !d) return HELIX_BACKEND_REF;
+    if (d->backend == HELIX_BACKEND_SGMMA) return HELIX_BACKEND_SGMMA;
+    return helix::rt::select_traits(ctx, *d).backend;
+}
+
+extern "C" const char* helix_ctx_backend_desc(helix_ctx* ctx, const helix_scan_desc* d) {
+    if (!ctx || !d) return "unavailable (null context)";
+    if (!helix_scan_supported(ctx, d)) return "declined (shape unsupported)";
+    return helix::rt::select_traits(ctx, *d).name;
+}

@@ -1,0 +1,215 @@
+// dispatch.cpp -- the encoder.
+//
+// Counterpart of the reference's src/runtime/dispatch.mm:55-287. HELIX
+// enqueues onto the caller's HIP stream and never allocates, synchronizes or
+// waits. Every check (arguments, shape gate, scratch size, kernel handles,
+// launch limits) happens before the first launch, so an error leaves nothing
+// enqueued. Stream order sequences the passes; there are no barriers to
+// insert.
+//
+// Per super-chunk group, in stream order:
+//   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
+//   Pass B  grid (ceil(P*N/256), n_head, n_seq)         x 256 threads
+//   Pass C  grid (chunks, n_group * n_hblk, n_seq)      x 256 threads
+// The ragged-tail padding and the bf16 staging of B and C that the reference
+// runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
+// staging here, so there is nothing to launch before the group loop.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "helix/helix_host.h"
+#include "helix_internal.h"
+
+namespace {
+
+using helix::rt::set_error;
+
+inline void* dptr(helix_tensor t) {
+    return t.buf ? static_cast<char*>(t.buf) + t.offset : nullptr;
+}
+
+helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
+                         helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
+                         helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
+                         helix_tensor s1, helix_tensor scratch) {
+    if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
+        set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
+        return HELIX_ERR_INVALID_ARG;
+    }
+    if (!helix_scan_supported(ctx, d)) {
+        set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
+        return HELIX_ERR_UNSUPPORTED_SHAPE;
+    }
+    if (!ctx->module) {
+        set_error(ctx, "context has no device (host-only context)");
+        return HELIX_ERR_NO_DEVICE;
+    }
+
+    HelixScanParams params;
+    std::string why;
+    if (!helix::rt::build_params(*d, &params, &why)) {
+        set_error(ctx, why);
+        return HELIX_ERR_INVALID_ARG;
+    }
+    params.has_ids = ids.buf ? 1 : 0;
+
+    const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(*d, tr.bf16_state);
+    if (plan.n_chunks <= 0) {
+        set_error(ctx, "empty problem");
+        return HELIX_ERR_INVALID_ARG;
+    }
+    if (plan.total_bytes > 0) {
+        if (!scratch.buf) {
+            set_error(ctx, "multipass requires a scratch buffer of helix_scan_scratch_size() bytes");
+            return HELIX_ERR_SCRATCH_TOO_SMALL;
+        }
+        // The reference checks the MTLBuffer length (dispatch.mm:150-153);
+        // the HIP analogue is the allocation containing the pointer.
+        hipDeviceptr_t base = nullptr;
+        size_t size = 0;
+        void* sp = dptr(scratch);
+        if (hipMemGetAddressRange(&base, &size, sp) == hipSuccess) {
+            const size_t avail = (size_t)((char*)base + size - (char*)sp);
+            if (avail < plan.total_bytes) {
+                set_error(ctx, "scratch buffer smaller than helix_scan_scratch_size()");
+                return HELIX_ERR_SCRATCH_TOO_SMALL;
+            }
+        } else {
+            (void)hipGetLastError();  // not a hipMalloc allocation: cannot verify, trust the caller
+        }
+    }
+
+    auto fn = [&](const char* name) -> hipFunction_t {
+        auto it = ctx->kernels.find(name);
+        return it == ctx->kernels.end() ? nullptr : it->second;
+    };
+    hipFunction_t fA = fn(tr.k_chunk_state), fB = fn(tr.k_state_scan), fC = fn(tr.k_chunk_out);
+    if (!fA || !fB || !fC) {
+        set_error(ctx, "kernel not resolved in code object");
+        return HELIX_ERR_PIPELINE;
+    }
+
+    // Scratch strides (helix_params.h layout).
+    const long long HPN = (long long)d->n_head * d->head_dim * d->d_state;
+    params.seg_len = plan.seg_len;
+    params.hblk    = plan.hblk;
+    params.n_hblk  = plan.n_hblk;
+    params.sl_cg   = HPN;
+    params.sl_seq  = (long long)plan.chunks_per_group * HPN;
+    params.sg_seg  = HPN;
+    params.sg_seq  = (long long)plan.segs_per_group * HPN;
+    params.ld_seq  = (long long)plan.chunks_per_group * d->n_head;
+    params.sd_seq  = (long long)plan.segs_per_group * d->n_head;
+
+    HelixScanBuffers bufs;
+    std::memset(&bufs, 0, sizeof(bufs));
+    bufs.s0  = static_cast<const float*>(dptr(s0));
+    bufs.x   = static_cast<const float*>(dptr(x));
+    bufs.dt  = static_cast<const float*>(dptr(dt));
+    bufs.A   = static_cast<const float*>(dptr(A));
+    bufs.B   = static_cast<const float*>(dptr(B));
+    bufs.C   = static_cast<const float*>(dptr(C));
+    bufs.ids = static_cast<const int*>(dptr(ids));
+    bufs.y   = static_cast<float*>(dptr(y));
+    bufs.s1  = static_cast<float*>(dptr(s1));
+    char* sc = static_cast<char*>(dptr(scratch));
+    bufs.s_local = plan.sl_elems ? sc + plan.off_sl : nullptr;
+    bufs.s_seg   = reinterpret_cast<float*>(sc + plan.off_sg);
+    bufs.ld      = reinterpret_cast<float*>(sc + plan.off_ld);
+    bufs.segld   = reinterpret_cast<float*>(sc + plan.off_sd);
+
+    // Debug-only per-pass timing split (reference dispatch.mm:207-216):
+    // HELIX_ONLY_PASS=A|B|C enqueues just that pass; the output is then
+    // meaningless. 'X' (the reference's pad/cast passes) enqueues nothing,
+    // because that work is fused into the Pass A/C staging here.
+    const char* only = std::getenv("HELIX_ONLY_PASS");
+    const bool do_a = !only || *only == 'A';
+    const bool do_b = !only || *only == 'B';
+    const bool do_c = !only || *only == 'C';
+
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    if (prev != ctx->device && hipSetDevice(ctx->device) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(ctx, "hipSetDevice failed");
+        return HELIX_ERR_NO_DEVICE;
+    }
+
+    helix_status st = HELIX_OK;
+    const unsigned PN = (unsigned)(d->head_dim * d->d_state);
+    void* args[] = {&params, &bufs};
+    for (int base = 0; base < plan.n_chunks && st == HELIX_OK; base += plan.chunks_per_group) {
+        params.chunk_base  = base;
+        params.n_cg        = std::min(plan.chunks_per_group, plan.n_chunks - base);
+        params.n_seg       = (params.n_cg + plan.seg_len - 1) / plan.seg_len;
+        params.first_group = base == 0 ? 1 : 0;
+
+        hipError_t e = hipSuccess;
+        if (do_a)
+            e = hipModuleLaunchKernel(fA, (unsigned)params.n_seg, (unsigned)d->n_head,
+                                      (unsigned)(d->n_seq * params.n_pslab), HELIX_WG, 1, 1, 0,
+                                      stream, args, nullptr);
+        if (e == hipSuccess && do_b)
+            e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
+                                      (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
+        if (e == hipSuccess && do_c)
+            e = hipModuleLaunchKernel(fC, (unsigned)params.n_cg,
+                                      (unsigned)(d->n_group * plan.n_hblk), (unsigned)d->n_seq,
+                                      HELIX_WG, 1, 1, 0, stream, args, nullptr);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(ctx, std::string("kernel launch failed: ") + hipGetErrorString(e));
+            st = HELIX_ERR_PIPELINE;
+        }
+    }
+    if (prev >= 0 && prev != ctx->device) (void)hipSetDevice(prev);
+    return st;
+}
+
+}  // namespace
+
+extern "C" helix_status helix_scan_encode(helix_ctx* ctx, void* cmd_buffer, const helix_scan_desc* d,
+                                          helix_tensor s0, helix_tensor x, helix_tensor dt,
+                                          helix_tensor A, helix_tensor B, helix_tensor C,
+                                          helix_tensor ids, helix_tensor y, helix_tensor s1,
+                                          helix_tensor scratch) {
+    if (!ctx || !d) return HELIX_ERR_INVALID_ARG;
+    return encode_core(ctx, static_cast<hipStream_t>(cmd_buffer), d, s0, x, dt, A, B, C, ids, y, s1,
+                       scratch);
+}
+
+extern "C" helix_status helix_scan_encode_into(helix_ctx* ctx, void* encoder, const helix_scan_desc* d,
+                                               helix_tensor s0, helix_tensor x, helix_tensor dt,
+                                               helix_tensor A, helix_tensor B, helix_tensor C,
+                                               helix_tensor ids, helix_tensor y, helix_tensor s1,
+                                               helix_tensor scratch) {
+    if (!ctx || !d) return HELIX_ERR_INVALID_ARG;
+    return encode_core(ctx, static_cast<hipStream_t>(encoder), d, s0, x, dt, A, B, C, ids, y, s1,
+                       scratch);
+}
+
+extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
+                                             helix_plan_info* out) {
+    if (!ctx || !d || !out) return HELIX_ERR_INVALID_ARG;
+    if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
+    const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr.bf16_state);
+    std::memset(out, 0, sizeof(*out));
+    out->n_chunks = pl.n_chunks;
+    out->chunks_per_group = pl.chunks_per_group;
+    out->n_groups = pl.n_groups;
+    out->seg_len = pl.seg_len;
+    out->segs_per_group = pl.segs_per_group;
+    out->hblk = pl.hblk;
+    out->n_hblk = pl.n_hblk;
+    out->bf16_state = tr.bf16_state ? 1 : 0;
+    out->total_bytes = pl.total_bytes;
+    out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
+    out->s_seg_bytes = pl.sg_elems * sizeof(float);
+    out->launches = 3 * pl.n_groups;
+    out->np = tr.np;
+    return HELIX_OK;
+}

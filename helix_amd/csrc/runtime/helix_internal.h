@@ -1,0 +1,86 @@
+// helix_internal.h -- C++ internals of the MI355X HELIX runtime. Not part of
+// the ABI. Counterpart of the reference's src/runtime/helix_internal.h:12-112
+// with the Metal device/library/pipeline objects replaced by one hipModule
+// whose kernels are all resolved when the context is created.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <string>
+#include <unordered_map>
+
+#include "helix/helix.h"
+#include "../kernels/helix_params.h"
+
+struct helix_ctx {
+    int         device = -1;
+    hipModule_t module = nullptr;
+    std::string arch;          // gcnArchName, e.g. "gfx950:sramecc+:xnack-"
+    std::string code_object;   // "<embedded>" or the file it was loaded from
+    int         n_cu = 0;
+    // Filled once at creation and only read afterwards, so encoding from
+    // several host threads needs no lock.
+    std::unordered_map<std::string, hipFunction_t> kernels;
+};
+
+// Which kernels a descriptor runs. Counterpart of the reference's
+// HelixMatmulTraits (helix_internal.h:38-48, caps.mm:18-61): chosen per
+// descriptor, never fails, and names the CDNA4 MFMA shape each pass uses.
+struct HelixMatmulTraits {
+    helix_backend backend;
+    const char*   name;            // what helix_ctx_backend_desc reports
+    const char*   k_chunk_state;   // Pass A
+    const char*   k_state_scan;    // Pass B
+    const char*   k_chunk_out;     // Pass C
+    bool          bf16_state;      // s_local kept in bf16 (Pass C takes bf16 operands)
+    const char*   mfma_a;          // MFMA instruction of Pass A
+    const char*   mfma_c;          // MFMA instruction of Pass C
+    int           np;              // d_state padding the kernels are built for
+};
+
+namespace helix::rt {
+
+// Every kernel name in the traits tables; all are resolved at context creation.
+const char* const* all_kernel_names(size_t* count);
+
+// Never fails: falls back to the fp32 path whenever bf16 is not requested or
+// not serviceable. Valid with ctx == nullptr (host-only planning).
+const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d);
+
+// How the multipass scan is tiled over the sequence (see helix_params.h):
+// super-chunk groups bound live scratch; segments of seg_len chunks are the
+// unit of Pass A's in-register walk and of Pass B's scan; head blocks are the
+// unit of Pass C's reuse of C.B^T. A pure function of the descriptor, the
+// state precision and the environment, so helix_scan_scratch_size() and the
+// encoder agree exactly.
+struct MultipassPlan {
+    int    n_chunks         = 0;
+    int    chunks_per_group = 0;
+    int    n_groups         = 0;
+    int    seg_len          = 0;
+    int    segs_per_group   = 0;
+    int    hblk             = 0;
+    int    n_hblk           = 0;
+    size_t sl_elems         = 0;   // s_local elements (0 when seg_len == 1)
+    size_t sl_elem_bytes    = 4;   // 4 (fp32 path) or 2 (bf16 path)
+    size_t sg_elems         = 0;   // s_seg elements (fp32)
+    size_t ld_elems         = 0;
+    size_t sd_elems         = 0;
+    size_t off_sl = 0, off_sg = 0, off_ld = 0, off_sd = 0;
+    size_t total_bytes      = 0;
+};
+
+MultipassPlan plan_multipass(const helix_scan_desc& d, bool bf16_state);
+
+// Scratch budget in bytes: $HELIX_SCRATCH_MB or the default.
+size_t scratch_budget_bytes();
+
+// Fills the kernel-side params from the public descriptor. Returns false and
+// sets *why when a launch dimension would exceed the hardware grid limits.
+bool build_params(const helix_scan_desc& d, HelixScanParams* out, std::string* why);
+
+// Thread-local last-error bookkeeping.
+void set_error(const helix_ctx* ctx, const std::string& msg);
+
+}  // namespace helix::rt

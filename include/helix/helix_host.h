@@ -1,0 +1,47 @@
+/* helix_host.h -- host-side extras of the MI355X HELIX build.
+ *
+ * Neither entry point has a counterpart in the reference ABI; both exist for
+ * callers that plan without a GPU (build machines, schedulers sizing scratch
+ * pools ahead of time) and for the CPU test suite.
+ */
+#ifndef HELIX_HOST_H
+#define HELIX_HOST_H
+
+#include "helix/helix.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A context bound to no device. helix_scan_supported, helix_scan_scratch_size,
+ * helix_ctx_select_backend, helix_ctx_backend_desc and helix_scan_plan_info
+ * answer exactly as on a gfx950 context; helix_scan_encode* return
+ * HELIX_ERR_NO_DEVICE without touching HIP. Free with helix_ctx_free. */
+helix_status helix_ctx_create_host(helix_ctx** out);
+
+/* The multipass plan helix_scan_encode would use for `d`. */
+typedef struct {
+    int32_t  n_chunks;          /* ceil(n_tok / 64)                              */
+    int32_t  chunks_per_group;  /* chunks per super-chunk group (scratch bound)  */
+    int32_t  n_groups;          /* sequential groups, carried through s1         */
+    int32_t  seg_len;           /* chunks per Pass A segment                     */
+    int32_t  segs_per_group;
+    int32_t  hblk;              /* heads per Pass C workgroup                    */
+    int32_t  n_hblk;            /* head blocks per B/C group                     */
+    int32_t  bf16_state;        /* 1 on the bf16 path                            */
+    uint64_t total_bytes;       /* == helix_scan_scratch_size()                  */
+    uint64_t s_local_bytes;     /* per-chunk states                              */
+    uint64_t s_seg_bytes;       /* segment aggregates / segment initial states   */
+    int32_t  launches;          /* kernel launches per encode                    */
+    int32_t  np;                /* d_state padding of the selected kernels       */
+} helix_plan_info;
+
+/* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */
+helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
+                                  helix_plan_info* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELIX_HOST_H */

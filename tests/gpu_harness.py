@@ -1,0 +1,68 @@
+"""GPU-side test harness: runs one Problem through the C ABI and returns host
+arrays. Counterpart of the reference's Gpu helper (tests/test_metal_parity.mm:
+40-68): upload, allocate outputs and scratch, encode on a stream, wait.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from contextlib import contextmanager
+
+import numpy as np
+import torch
+
+from helix_amd.desc import HELIX_OK, HELIX_TENSOR_NULL, HelixTensor
+
+# Calibrated per-element tolerances of the reference parity test
+# (tests/test_metal_parity.mm:35-38), selected by the backend that runs.
+F32_REL, F32_ABS = 5e-6, 5e-7
+BF16_REL, BF16_ABS = 1.5e-2, 3e-3
+# BASELINE.json gates on max|dy|/max|y| (and likewise for the final state).
+F32_GATE, BF16_GATE = 1e-4, 2e-2
+
+
+@contextmanager
+def env(**kv):
+    old = {k: os.environ.get(k) for k in kv}
+    try:
+        for k, v in kv.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = str(v)
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def T(t: torch.Tensor | None) -> HelixTensor:
+    return HELIX_TENSOR_NULL if t is None else HelixTensor(t.data_ptr(), 0)
+
+
+def upload(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run(ctx, p, desc=None, use_ids=False, s0_gpu=None, y_gpu=None, s1_gpu=None, stream=None,
+        into=False, check=True):
+    """Encode the scan for Problem `p` and return (status, y, s1) as numpy."""
+    d = desc if desc is not None else p.d
+    dev_s0 = s0_gpu if s0_gpu is not None else upload(p.s0)
+    x, dt, A = upload(p.x), upload(p.dt), upload(p.A)
+    B, C = upload(p.B), upload(p.C)
+    ids = upload(p.ids) if (use_ids and p.ids is not None) else None
+    y = y_gpu if y_gpu is not None else torch.full(p.y_shape(), float("nan"), device="cuda")
+    s1 = s1_gpu if s1_gpu is not None else torch.full(p.s_shape(), float("nan"), device="cuda")
+    nbytes = ctx.scratch_size(d)
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda") if nbytes else None
+    st = stream if stream is not None else torch.cuda.current_stream()
+    rc = ctx.encode(st.cuda_stream, d, T(dev_s0), T(x), T(dt), T(A), T(B), T(C), T(ids), T(y),
+                    T(s1), T(scratch), into=into)
+    if check and rc != HELIX_OK:
+        raise RuntimeError(f"encode failed rc={rc}: {ctx.last_error()}")
+    torch.cuda.synchronize()
+    return rc, y.cpu().numpy(), s1.cpu().numpy()
