@@ -23,13 +23,14 @@ template <int NP, bool SBF>
 __device__ __forceinline__ void store_state_tiles(const f32x16* acc, void* dst_base, int pw, int N,
                                                   int pt, int nt0, int lo, int hi) {
     constexpr int NTW = NP / 64;
+    const bool full = (pw == HELIX_HD) && (N == NP);
 #pragma unroll
     for (int i = 0; i < NTW; ++i) {
         const int n = (nt0 + 2 * i) * 32 + lo;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int pr = pt * 32 + acc_row(r, hi);
-            if (pr < pw && n < N) {
+            if (full || (pr < pw && n < N)) {
                 const long long off = (long long)pr * N + n;
                 if (SBF)
                     static_cast<__bf16*>(dst_base)[off] = to_bf16(acc[i][r]);
@@ -37,6 +38,38 @@ __device__ __forceinline__ void store_state_tiles(const f32x16* acc, void* dst_b
                     static_cast<float*>(dst_base)[off] = acc[i][r];
             }
         }
+    }
+}
+
+// Registers holding one chunk's global inputs for this thread, so the loads
+// of chunk c+1 are in flight while chunk c runs on the MFMA pipe. Every load
+// reads an in-bounds address (rows clamped to the last valid token, columns to
+// the last valid index) and the tile masks are applied afterwards: a guarded
+// load would compile to a branch and a wait per element.
+template <int NP>
+struct StageA {
+    float dtraw;
+    float x[16];
+    float b[16][NP / 64];
+};
+
+template <int NP>
+__device__ __forceinline__ void load_stage_a(StageA<NP>& st, const HelixScanParams& p,
+                                             const float* __restrict__ dt_h,
+                                             const float* __restrict__ x_h,
+                                             const float* __restrict__ B_g, int c, int lane,
+                                             int wave, int pw, int N) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    st.dtraw = dt_h[(long long)(t0 + min(lane, tlen - 1)) * p.s_dt[0]];
+    const long long xc = (long long)min(lane, pw - 1) * p.s_x[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int jr = min(wave + 4 * i, tlen - 1);
+        st.x[i] = x_h[(long long)(t0 + jr) * p.s_x[0] + xc];
+        const float* brow = B_g + (long long)(t0 + jr) * p.s_b[0];
+#pragma unroll
+        for (int m = 0; m < NP / 64; ++m) st.b[i][m] = brow[min(lane + 64 * m, N - 1)];
     }
 }
 
@@ -82,35 +115,30 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
     for (int i = 0; i < NTW; ++i) acc[i] = zero16();
     float lam = 0.0f;  // log-decay accumulated over this segment before chunk c
 
+    StageA<NP> st;
+    load_stage_a<NP>(st, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
+
     for (int c = c_begin; c < c_end; ++c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
 
-        const ChunkDecay cd = chunk_decay(p, dt_h, t0, tlen, A_h);
-        const float sdec = (lane < tlen) ? exp_diff(cd.lend, cd.lcum) : 0.0f;
-        const float cf   = sdec * cd.dtv;
+        // Decay preamble from the staged dt (dtv = 0 past tlen).
+        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
+        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lend = __shfl(lcum, 63, 64);
+        const float cf = (lane < tlen) ? exp_diff(lend, lcum) * dtv : 0.0f;
 
-        // dtXs[j][p] = exp(L_end - Lcum_j) dt_j x[j][p]; rows past tlen and
-        // columns past the slab are zero.
-#pragma unroll 4
+        // dtXs[j][p] = exp(L_end - Lcum_j) dt_j x[j][p] (cf_j = 0 past tlen);
+        // B[j][n] zero past tlen and d_state.
+#pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = wave + 4 * i;
             const float cj = bcast(cf, j);
-            float v = 0.0f;
-            if (j < tlen && lane < pw) v = cj * x_h[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
-            sX[j * RSX + lane] = v;
-        }
-        // B chunk, zero-padded past tlen and past d_state.
-#pragma unroll 4
-        for (int i = 0; i < 16; ++i) {
-            const int j = wave + 4 * i;
-            const float* brow = B_g + (long long)(t0 + j) * p.s_b[0];
+            sX[j * RSX + lane] = lane < pw ? cj * st.x[i] : 0.0f;
 #pragma unroll
             for (int m = 0; m < NP / 64; ++m) {
                 const int n = lane + 64 * m;
-                float v = 0.0f;
-                if (j < tlen && n < N) v = brow[n];
-                sB[j * RSB + n] = v;
+                sB[j * RSB + n] = (j < tlen && n < N) ? st.b[i][m] : 0.0f;
             }
         }
 
@@ -120,11 +148,14 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
         if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
         __syncthreads();
 
-        const float a_c = expf((float)cd.lend);
+        // Next chunk's inputs travel while this chunk's GEMM runs.
+        if (c + 1 < c_end) load_stage_a<NP>(st, p, dt_h, x_h, B_g, c + 1, lane, wave, pw, N);
+
+        const float a_c = expf((float)lend);
 #pragma unroll
         for (int i = 0; i < NTW; ++i) acc[i] *= a_c;
 
-#pragma unroll 4
+#pragma unroll 8
         for (int s = 0; s < HELIX_CS / 2; ++s) {
             const int j = 2 * s + hi;
             const float av = sX[j * RSX + pt * 32 + lo];
@@ -134,7 +165,7 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
                 acc[i] = mfma_f32(av, bv, acc[i]);
             }
         }
-        lam += (float)cd.lend;
+        lam += (float)lend;
         __syncthreads();
     }
 

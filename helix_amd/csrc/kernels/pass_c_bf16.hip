@@ -18,6 +18,8 @@
 //   S^T[p][n]          (K = n for G3; s_local is already [P][N])
 #include "helix_common.h"
 
+#include "pass_c_stage.h"
+
 template <int NP>
 __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int RS  = NP + 8;          // bf16 row stride of C, B, S^T (16-byte aligned rows)
@@ -52,19 +54,26 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
     {
         const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
         const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
-#pragma unroll 4
+        float vc[16][NP / 64], vb[16][NP / 64];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int jr = min(wave + 4 * i, tlen - 1);
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int nc = min(lane + 64 * m, N - 1);
+                vc[i][m] = C_g[(long long)jr * p.s_c[0] + nc];
+                vb[i][m] = B_g[(long long)jr * p.s_b[0] + nc];
+            }
+        }
+#pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = wave + 4 * i;
 #pragma unroll
             for (int m = 0; m < NP / 64; ++m) {
                 const int n = lane + 64 * m;
-                float vc = 0.0f, vb = 0.0f;
-                if (j < tlen && n < N) {
-                    vc = C_g[(long long)j * p.s_c[0] + n];
-                    vb = B_g[(long long)j * p.s_b[0] + n];
-                }
-                sC[j * RS + n]  = to_bf16(vc);
-                sBS[j * RS + n] = to_bf16(vb);
+                const bool ok = j < tlen && n < N;
+                sC[j * RS + n]  = to_bf16(ok ? vc[i][m] : 0.0f);
+                sBS[j * RS + n] = to_bf16(ok ? vb[i][m] : 0.0f);
             }
         }
     }
@@ -96,78 +105,79 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
     const __bf16* __restrict__ sl_s = static_cast<const __bf16*>(b.s_local) + seq * p.sl_seq + (long long)cg * p.sl_cg;
     const float* __restrict__ sg_s = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg;
 
-    for (int h = h_begin; h < h_end; ++h) {
-        const float A_h = b.A[(long long)h * p.s_a];
-        const ChunkDecay cd = chunk_decay(p, dt_s + h * p.s_dt[1], t0, tlen, A_h);
-        const float es = expf(b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h]);
-        const long long head_off = (long long)h * P * N;
+    const int n_items = (h_end - h_begin) * p.n_pslab;
+    StageC<NP, __bf16> st;
+    load_stage_c<NP, __bf16>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, h_begin, 0,
+                             lane, wave);
 
-        for (int slab = 0; slab < p.n_pslab; ++slab) {
-            const int p0 = slab * HELIX_HD;
-            const int pw = min(HELIX_HD, P - p0);
+    for (int item = 0; item < n_items; ++item) {
+        const int h    = h_begin + item / p.n_pslab;
+        const int slab = item % p.n_pslab;
+        const int p0 = slab * HELIX_HD;
+        const int pw = min(HELIX_HD, P - p0);
 
-            // dtX^T[p][j] (bf16)
-            const float* xh = x_s + h * p.s_x[1] + p0 * p.s_x[2];
-#pragma unroll 4
-            for (int i = 0; i < 16; ++i) {
-                const int j = wave + 4 * i;
-                const float dj = bcast(cd.dtv, j);
-                float v = 0.0f;
-                if (j < tlen && lane < pw) v = dj * xh[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
-                sXt[lane * RSJ + j] = to_bf16(v);
-            }
-            // M[t][j] (bf16), zero above the diagonal.
-#pragma unroll 4
-            for (int i = 0; i < 16; ++i) {
-                const int t = wave + 4 * i;
-                const double lt = bcast(cd.lcum, t);
-                const float m = (lane <= t) ? sCB[t * RSCB + lane] * exp_diff(lt, cd.lcum) : 0.0f;
-                sM[t * RSJ + lane] = to_bf16(m);
-            }
-            if (wave == 0) sE[lane] = expf((float)cd.lcum);
-            // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16.
-#pragma unroll 4
-            for (int i = 0; i < 16; ++i) {
-                const int pr = wave + 4 * i;
+        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
+        const double lcum = wave_incl_sum((double)st.A * (double)dtv);
+        const float es = expf(st.ld);
+
+        // dtX^T[p][j] (bf16); dtv_j = 0 past tlen.
 #pragma unroll
-                for (int m = 0; m < NP / 64; ++m) {
-                    const int n = lane + 64 * m;
-                    float v = 0.0f;
-                    if (pr < pw && n < N) {
-                        const long long off = head_off + (long long)(p0 + pr) * N + n;
-                        v = es * sg_s[off];
-                        if (cis > 0) v += (float)sl_s[off];
-                    }
-                    sBS[pr * RS + n] = to_bf16(v);
-                }
-            }
-            __syncthreads();
-
-            // G3, row scale, G2.
-            f32x16 acc = zero16();
-#pragma unroll 4
-            for (int s = 0; s < NP / 16; ++s) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sC[(tb * 32 + lo) * RS + 16 * s + 8 * hi]);
-                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sBS[(pb * 32 + lo) * RS + 16 * s + 8 * hi]);
-                acc = mfma_bf16(av, bv, acc);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
-            for (int s = 0; s < 2 * (tb + 1); ++s) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sM[(tb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
-                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sXt[(pb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
-                acc = mfma_bf16(av, bv, acc);
-            }
-
-            float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
-            const int pp = pb * 32 + lo;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = tb * 32 + acc_row(r, hi);
-                if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
-            }
-            __syncthreads();
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+            sXt[lane * RSJ + j] = to_bf16(lane < pw ? bcast(dtv, j) * st.x[i] : 0.0f);
         }
+        // M[t][j] (bf16), zero above the diagonal.
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int t = wave + 4 * i;
+            const double lt = bcast(lcum, t);
+            const float m = (lane <= t) ? sCB[t * RSCB + lane] * exp_diff(lt, lcum) : 0.0f;
+            sM[t * RSJ + lane] = to_bf16(m);
+        }
+        if (wave == 0) sE[lane] = expf((float)lcum);
+        // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16.
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int pr = wave + 4 * i;
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int n = lane + 64 * m;
+                float v = es * st.sg[i][m];
+                if (cis > 0) v += (float)st.sl[i][m];
+                sBS[pr * RS + n] = to_bf16((pr < pw && n < N) ? v : 0.0f);
+            }
+        }
+        __syncthreads();
+        if (item + 1 < n_items) {
+            const int hn = h_begin + (item + 1) / p.n_pslab;
+            load_stage_c<NP, __bf16>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, hn,
+                                     (item + 1) % p.n_pslab, lane, wave);
+        }
+
+        // G3, row scale, G2.
+        f32x16 acc = zero16();
+#pragma unroll 4
+        for (int s = 0; s < NP / 16; ++s) {
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sC[(tb * 32 + lo) * RS + 16 * s + 8 * hi]);
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sBS[(pb * 32 + lo) * RS + 16 * s + 8 * hi]);
+            acc = mfma_bf16(av, bv, acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
+        for (int s = 0; s < 2 * (tb + 1); ++s) {
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sM[(tb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sXt[(pb * 32 + lo) * RSJ + 16 * s + 8 * hi]);
+            acc = mfma_bf16(av, bv, acc);
+        }
+
+        float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
+        const int pp = pb * 32 + lo;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = tb * 32 + acc_row(r, hi);
+            if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
+        }
+        __syncthreads();
     }
 }
 

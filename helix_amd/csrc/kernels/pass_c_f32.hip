@@ -24,6 +24,8 @@
 // here the padding happens during staging).
 #include "helix_common.h"
 
+#include "pass_c_stage.h"
+
 template <int NP>
 __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int KS  = NP > 128 ? 128 : NP;  // S_init staged in K blocks of KS
@@ -73,19 +75,26 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
     {
         const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
         const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
-#pragma unroll 4
+        float vc[16][NP / 64], vb[16][NP / 64];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int jr = min(wave + 4 * i, tlen - 1);
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int nc = min(lane + 64 * m, N - 1);
+                vc[i][m] = C_g[(long long)jr * p.s_c[0] + nc];
+                vb[i][m] = B_g[(long long)jr * p.s_b[0] + nc];
+            }
+        }
+#pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = wave + 4 * i;
 #pragma unroll
             for (int m = 0; m < NP / 64; ++m) {
                 const int n = lane + 64 * m;
-                float vc = 0.0f, vb = 0.0f;
-                if (j < tlen && n < N) {
-                    vc = C_g[(long long)j * p.s_c[0] + n];
-                    vb = B_g[(long long)j * p.s_b[0] + n];
-                }
-                sC[j * RSC + n] = vc;
-                sB[j * RSC + n] = vb;
+                const bool ok = j < tlen && n < N;
+                sC[j * RSC + n] = ok ? vc[i][m] : 0.0f;
+                sB[j * RSC + n] = ok ? vb[i][m] : 0.0f;
             }
         }
     }
@@ -117,86 +126,90 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
     const float* __restrict__ sl_s = static_cast<const float*>(b.s_local) + seq * p.sl_seq + (long long)cg * p.sl_cg;
     const float* __restrict__ sg_s = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg;
 
-    for (int h = h_begin; h < h_end; ++h) {
-        const float A_h = b.A[(long long)h * p.s_a];
-        const ChunkDecay cd = chunk_decay(p, dt_s + h * p.s_dt[1], t0, tlen, A_h);
-        const float es = expf(b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h]);
-        const long long head_off = (long long)h * P * N;
+    const int n_items = (h_end - h_begin) * p.n_pslab;
+    StageC<NP, float> st;
+    load_stage_c<NP, float>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, h_begin, 0,
+                            lane, wave);
 
-        for (int slab = 0; slab < p.n_pslab; ++slab) {
-            const int p0 = slab * HELIX_HD;
-            const int pw = min(HELIX_HD, P - p0);
+    for (int item = 0; item < n_items; ++item) {
+        const int h    = h_begin + item / p.n_pslab;
+        const int slab = item % p.n_pslab;
+        const int p0 = slab * HELIX_HD;
+        const int pw = min(HELIX_HD, P - p0);
 
-            // dtX[j][p]
-            const float* xh = x_s + h * p.s_x[1] + p0 * p.s_x[2];
+        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
+        const double lcum = wave_incl_sum((double)st.A * (double)dtv);
+        const float es = expf(st.ld);
+
+        // dtX[j][p] (dtv_j = 0 past tlen)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+            sX[j * RSX + lane] = lane < pw ? bcast(dtv, j) * st.x[i] : 0.0f;
+        }
+        // M[t][j] for this head; lane = j, so Lcum_j is this lane's own.
 #pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int t = wave + 4 * i;
+            const double lt = bcast(lcum, t);
+            sM[t * RSM + lane] = (lane <= t) ? sCB[t * RSM + lane] * exp_diff(lt, lcum) : 0.0f;
+        }
+        if (wave == 0) sE[lane] = expf((float)lcum);
+
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            // S_init[p][k] = R_c + exp(ld_c) S_seg, zero past the slab and d_state.
+#pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int j = wave + 4 * i;
-                const float dj = bcast(cd.dtv, j);
-                float v = 0.0f;
-                if (j < tlen && lane < pw) v = dj * xh[(long long)(t0 + j) * p.s_x[0] + lane * p.s_x[2]];
-                sX[j * RSX + lane] = v;
-            }
-            // M[t][j] for this head; lane = j, so Lcum_j is this lane's own.
-#pragma unroll 4
-            for (int i = 0; i < 16; ++i) {
-                const int t = wave + 4 * i;
-                const double lt = bcast(cd.lcum, t);
-                sM[t * RSM + lane] = (lane <= t) ? sCB[t * RSM + lane] * exp_diff(lt, cd.lcum) : 0.0f;
-            }
-            if (wave == 0) sE[lane] = expf((float)cd.lcum);
-
-            f32x16 acc = zero16();
-            for (int kb = 0; kb < NKB; ++kb) {
-                // S_init[p][k] = R_c + exp(ld_c) S_seg, zero past the slab and d_state.
-#pragma unroll 4
-                for (int i = 0; i < 16; ++i) {
-                    const int pr = wave + 4 * i;
+                const int pr = wave + 4 * i;
 #pragma unroll
-                    for (int m = 0; m < KS / 64; ++m) {
-                        const int k = lane + 64 * m;
-                        const int n = kb * KS + k;
-                        float v = 0.0f;
-                        if (pr < pw && n < N) {
-                            const long long off = head_off + (long long)(p0 + pr) * N + n;
-                            v = es * sg_s[off];
-                            if (cis > 0) v += sl_s[off];
-                        }
-                        sS[pr * RSS + k] = v;
-                    }
+                for (int m = 0; m < KS / 64; ++m) {
+                    const int k = lane + 64 * m;
+                    const int n = kb * KS + k;
+                    const int mm = kb * (KS / 64) + m;
+                    float v = es * st.sg[i][mm];
+                    if (cis > 0) v += st.sl[i][mm];
+                    sS[pr * RSS + k] = (pr < pw && n < N) ? v : 0.0f;
                 }
-                __syncthreads();
-                // G3 partial: y += C[:, kblock] . S_init[kblock, :]
-#pragma unroll 8
-                for (int s = 0; s < KS / 2; ++s) {
-                    const float av = sC[(tb * 32 + lo) * RSC + kb * KS + 2 * s + hi];
-                    const float bv = sS[(pb * 32 + lo) * RSS + 2 * s + hi];
-                    acc = mfma_f32(av, bv, acc);
-                }
-                if (kb + 1 < NKB) __syncthreads();
-            }
-
-            // rows scaled by exp(Lcum_t), then G2 on top.
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
-            const int ksteps = 16 * (tb + 1);
-#pragma unroll 8
-            for (int s = 0; s < ksteps; ++s) {
-                const int j = 2 * s + hi;
-                const float av = sM[(tb * 32 + lo) * RSM + j];
-                const float bv = sX[j * RSX + pb * 32 + lo];
-                acc = mfma_f32(av, bv, acc);
-            }
-
-            float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
-            const int pp = pb * 32 + lo;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = tb * 32 + acc_row(r, hi);
-                if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
             }
             __syncthreads();
+            // The next item's inputs travel during the last block's GEMMs.
+            if (kb + 1 == NKB && item + 1 < n_items) {
+                const int hn = h_begin + (item + 1) / p.n_pslab;
+                load_stage_c<NP, float>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, hn,
+                                        (item + 1) % p.n_pslab, lane, wave);
+            }
+            // G3 partial: y += C[:, kblock] . S_init[kblock, :]
+#pragma unroll 8
+            for (int s = 0; s < KS / 2; ++s) {
+                const float av = sC[(tb * 32 + lo) * RSC + kb * KS + 2 * s + hi];
+                const float bv = sS[(pb * 32 + lo) * RSS + 2 * s + hi];
+                acc = mfma_f32(av, bv, acc);
+            }
+            if (kb + 1 < NKB) __syncthreads();
         }
+
+        // rows scaled by exp(Lcum_t), then G2 on top.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
+        const int ksteps = 16 * (tb + 1);
+#pragma unroll 8
+        for (int s = 0; s < ksteps; ++s) {
+            const int j = 2 * s + hi;
+            const float av = sM[(tb * 32 + lo) * RSM + j];
+            const float bv = sX[j * RSX + pb * 32 + lo];
+            acc = mfma_f32(av, bv, acc);
+        }
+
+        float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
+        const int pp = pb * 32 + lo;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = tb * 32 + acc_row(r, hi);
+            if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
+        }
+        __syncthreads();
     }
 }
 
