@@ -157,6 +157,9 @@ def main():
     ap.add_argument("--warmup-ms", type=float, default=800.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
+                    help="also run a plain device copy of this size (a known-traffic kernel "
+                         "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -270,6 +273,14 @@ def main():
             "kernel": results["fp32"]["kernel"],
         },
     }
+    if args.calib_copy:
+        n = args.calib_copy * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = n * 4
     if not args.no_cpu:
         out.update(cpu_baseline(args.cpu_budget))
     print(json.dumps(out), flush=True)

@@ -80,6 +80,19 @@ HELIX_DEV ChunkDecay chunk_decay(const HelixScanParams& p, const float* __restri
 // exp of a (small, non-positive in practice) fp64 log-decay difference.
 HELIX_DEV float exp_diff(double a, double b) { return expf((float)(a - b)); }
 
+// MI355X hands the workgroups of a launch to its 8 XCDs round-robin (linear
+// id i runs on XCD i % 8), and each XCD has its own L2. This maps the linear
+// id to a logical id so that a contiguous run of logical ids shares one XCD:
+// work items that read the same data (chunks of one segment, heads of one
+// group) then share an L2 instead of each XCD fetching its own copy.
+// A bijection on [0, total); the ragged tail past a multiple of 8 is kept.
+HELIX_DEV unsigned xcd_logical_id(unsigned linear, unsigned total) {
+    constexpr unsigned kXcd = 8;
+    const unsigned per = total / kXcd;
+    if (linear >= per * kXcd) return linear;
+    return (linear % kXcd) * per + linear / kXcd;
+}
+
 // Wave-uniform broadcast of lane `src`'s value (src must be wave-uniform).
 HELIX_DEV float bcast(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));

@@ -57,10 +57,17 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
 
-    const int cg  = blockIdx.x;
-    const int g   = blockIdx.y / p.n_hblk;
-    const int hb  = blockIdx.y % p.n_hblk;
-    const int seq = blockIdx.z;
+    // 1-D grid of n_cg * (n_group * n_hblk) * n_seq workgroups, chunk fastest
+    // in the logical order so a segment's chunks (which share S_seg) and a
+    // chunk's head blocks (which share B and C) stay on one XCD.
+    const unsigned n_gh  = (unsigned)(p.n_group * p.n_hblk);
+    const unsigned total = (unsigned)p.n_cg * n_gh * (unsigned)p.n_seq;
+    const unsigned wid   = xcd_logical_id(blockIdx.x, total);
+    const int cg  = (int)(wid % (unsigned)p.n_cg);
+    const int gh  = (int)((wid / (unsigned)p.n_cg) % n_gh);
+    const int seq = (int)(wid / ((unsigned)p.n_cg * n_gh));
+    const int g   = gh / p.n_hblk;
+    const int hb  = gh % p.n_hblk;
     const int t0   = (p.chunk_base + cg) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int N = p.d_state, P = p.head_dim;

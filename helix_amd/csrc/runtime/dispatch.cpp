@@ -10,7 +10,8 @@
 // Per super-chunk group, in stream order:
 //   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
 //   Pass B  grid (ceil(P*N/256), n_head, n_seq)         x 256 threads
-//   Pass C  grid (chunks, n_group * n_hblk, n_seq)      x 256 threads
+//   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
+//           decoded XCD-aware in the kernel)
 // The ragged-tail padding and the bf16 staging of B and C that the reference
 // runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
 // staging here, so there is nothing to launch before the group loop.
@@ -156,9 +157,9 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c)
-            e = hipModuleLaunchKernel(fC, (unsigned)params.n_cg,
-                                      (unsigned)(d->n_group * plan.n_hblk), (unsigned)d->n_seq,
-                                      HELIX_WG, 1, 1, 0, stream, args, nullptr);
+            e = hipModuleLaunchKernel(fC, (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) *
+                                          (unsigned)d->n_seq,
+                                      1, 1, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e != hipSuccess) {
             (void)hipGetLastError();
             set_error(ctx, std::string("kernel launch failed: ") + hipGetErrorString(e));

@@ -1,0 +1,323 @@
+"""Host-side logic of libhelix.so, runnable without a GPU.
+
+Covers what the reference keeps in caps.mm / dispatch.mm / desc.cpp:
+descriptor defaults, the shape gate, backend selection, scratch planning and
+argument validation, plus the ABI surface itself (every symbol the headers
+declare is exported, struct layouts match the reference). A host-only context
+(include/helix/helix_host.h) answers exactly as a gfx950 context would, and
+its encode returns HELIX_ERR_NO_DEVICE without touching HIP.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+
+from helix_amd import abi
+from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_REF,
+                            HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_ERR_INVALID_ARG,
+                            HELIX_ERR_NO_DEVICE, HELIX_ERR_SCRATCH_TOO_SMALL,
+                            HELIX_ERR_UNSUPPORTED_SHAPE, HELIX_A_DIAG_PER_CHANNEL,
+                            HELIX_TENSOR_NULL, HelixScanDesc, HelixTensor, algorithmic_bytes,
+                            algorithmic_flops, desc_init)
+from oracle import pyoracle as po
+from algebra_model import two_level_scan
+from gpu_harness import env
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CONFIG_SHAPES = {
+    "cfg0": (256, 1, 8, 64, 64, 1), "cfg1": (2048, 1, 64, 64, 128, 8),
+    "cfg2": (8192, 1, 64, 64, 128, 8), "cfg3": (1000, 4, 32, 128, 128, 1),
+    "cfg4a": (4096, 8, 80, 64, 128, 1), "cfg4b": (4096, 8, 27, 192, 128, 1),
+}
+
+
+@pytest.fixture(scope="module")
+def host():
+    c = abi.Context(host_only=True)
+    yield c
+    c.close()
+
+
+def mp(shape, backend=HELIX_BACKEND_AUTO):
+    d = abi.desc_init_c(*shape)
+    d.multipass = True
+    d.backend = backend
+    return d
+
+
+# ---------------------------------------------------------------------------
+# ABI surface
+# ---------------------------------------------------------------------------
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", "helix", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(helix_[a-z_]+)\s*\(", text)) - {"helix_tensor_is_null"}
+
+
+def test_library_exports_every_declared_symbol():
+    L = abi.lib()
+    declared = _declared("helix.h") | _declared("helix_host.h")
+    assert declared == set(abi.ABI_SYMBOLS) | set(abi.HOST_SYMBOLS)
+    for name in declared:
+        assert hasattr(L, name), f"{name} not exported by libhelix.so"
+
+
+def test_abi_version_and_enums_match_header():
+    text = open(os.path.join(ROOT, "include", "helix", "helix.h")).read()
+    assert "#define HELIX_ABI_VERSION 1" in text
+    for name, val in [("HELIX_OK", 0), ("HELIX_ERR_UNSUPPORTED_SHAPE", 1),
+                      ("HELIX_ERR_NO_DEVICE", 2), ("HELIX_ERR_SCRATCH_TOO_SMALL", 3),
+                      ("HELIX_ERR_INVALID_ARG", 4), ("HELIX_ERR_PIPELINE", 5),
+                      ("HELIX_BACKEND_AUTO", 0), ("HELIX_BACKEND_SGMMA", 1),
+                      ("HELIX_BACKEND_MPP", 2), ("HELIX_BACKEND_REF", 3),
+                      ("HELIX_F32", 0), ("HELIX_F16", 1), ("HELIX_BF16", 2)]:
+        assert re.search(rf"\b{name}\s*=\s*{val}\b", text), name
+
+
+def test_desc_layout_matches_reference():
+    assert ctypes.sizeof(HelixScanDesc) == 248
+    assert ctypes.sizeof(HelixTensor) == 16
+    R = po.ref_lib()
+    if R is not None:
+        assert R.ref_desc_size() == ctypes.sizeof(HelixScanDesc)
+
+
+@pytest.mark.parametrize("shape", list(CONFIG_SHAPES.values()) + [(1, 1, 1, 8, 8, 1), (509, 3, 6, 72, 40, 2)])
+def test_desc_init_c_python_and_reference_agree(shape):
+    c = abi.desc_init_c(*shape)
+    py = desc_init(*shape)
+    assert bytes(c) == bytes(py)
+    assert c.dt_max == math.inf and c.multipass is False and c.chunk == 0
+    R = po.ref_lib()
+    if R is not None:
+        r = HelixScanDesc()
+        R.ref_desc_init(ctypes.byref(r), *shape)
+        assert bytes(r) == bytes(c)
+
+
+# ---------------------------------------------------------------------------
+# Shape gate (reference caps.mm:112-151, plus this build's own limits)
+# ---------------------------------------------------------------------------
+
+def test_all_baseline_configs_supported(host):
+    for name, shape in CONFIG_SHAPES.items():
+        for b in (HELIX_BACKEND_AUTO, HELIX_BACKEND_SGMMA, HELIX_BACKEND_MPP):
+            assert host.supported(mp(shape, b)), name
+
+
+def _declined(host, mutate):
+    d = mp((256, 2, 4, 64, 128, 2))
+    assert host.supported(d)
+    mutate(d)
+    return not host.supported(d)
+
+
+@pytest.mark.parametrize("why,mutate", [
+    ("zero tokens", lambda d: setattr(d, "n_tok", 0)),
+    ("negative heads", lambda d: setattr(d, "n_head", -4)),
+    ("heads not a multiple of groups", lambda d: setattr(d, "n_group", 3)),
+    ("diagonal A", lambda d: setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL)),
+    ("bf16 storage", lambda d: setattr(d, "io_dtype", HELIX_BF16)),
+    ("bf16 compute dtype", lambda d: setattr(d, "compute_dtype", HELIX_BF16)),
+    ("d_state not a multiple of 8", lambda d: setattr(d, "d_state", 60)),
+    ("head_dim not a multiple of 8", lambda d: setattr(d, "head_dim", 60)),
+    ("d_state above 256", lambda d: setattr(d, "d_state", 264)),
+    ("strided B state", lambda d: d.s_b.__setitem__(2, 2)),
+    ("strided C state", lambda d: d.s_c.__setitem__(2, 2)),
+    ("strided s state", lambda d: d.s_s.__setitem__(2, 2)),
+    ("s rows not d_state apart", lambda d: d.s_s.__setitem__(1, 256)),
+    ("chunk 32", lambda d: setattr(d, "chunk", 32)),
+    ("single pass", lambda d: setattr(d, "multipass", False)),
+    ("REF backend", lambda d: setattr(d, "backend", HELIX_BACKEND_REF)),
+    ("grid z overflow", lambda d: setattr(d, "n_seq", 70000)),
+])
+def test_gate_declines(host, why, mutate):
+    assert _declined(host, mutate), why
+
+
+def test_gate_accepts_ragged_strided_and_odd_shapes(host):
+    for shape in [(1, 1, 1, 8, 8, 1), (1000, 3, 6, 72, 40, 2), (129, 2, 4, 192, 256, 4)]:
+        assert host.supported(mp(shape))
+    d = mp((300, 2, 4, 64, 128, 1))
+    d.s_x[0] = 4 * 64 + 16          # padded token rows (a ggml view)
+    d.s_x[2] = 1
+    d.s_y[2] = 1
+    d.chunk = 64
+    assert host.supported(d)
+
+
+def test_null_context_and_desc():
+    L = abi.lib()
+    d = mp((64, 1, 1, 8, 8, 1))
+    assert not L.helix_scan_supported(None, ctypes.byref(d))
+    assert L.helix_ctx_select_backend(None, ctypes.byref(d)) == HELIX_BACKEND_REF
+    assert L.helix_ctx_backend_desc(None, ctypes.byref(d)) == b"unavailable (null context)"
+    assert L.helix_scan_scratch_size(None, None) == 0
+
+
+# ---------------------------------------------------------------------------
+# Backend selection (reference caps.mm:79-110)
+# ---------------------------------------------------------------------------
+
+def test_backend_selection(host):
+    shape = CONFIG_SHAPES["cfg2"]
+    assert host.select_backend(mp(shape, HELIX_BACKEND_AUTO)) == HELIX_BACKEND_MPP
+    assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_MPP
+    assert host.select_backend(mp(shape, HELIX_BACKEND_SGMMA)) == HELIX_BACKEND_SGMMA
+    assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
+    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
+    assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C (d_state<=256)"
+    assert host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=64)"
+    d = mp(shape)
+    d.multipass = False
+    assert host.backend_desc(d) == "declined (shape unsupported)"
+    with env(HELIX_FORCE_BACKEND="sgmma"):
+        assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_SGMMA
+
+
+# ---------------------------------------------------------------------------
+# Scratch planning (reference caps.mm:153-241)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(CONFIG_SHAPES))
+@pytest.mark.parametrize("backend", [HELIX_BACKEND_SGMMA, HELIX_BACKEND_MPP])
+def test_plan_invariants(host, name, backend):
+    shape = CONFIG_SHAPES[name]
+    L, S, H, P, N, G = shape
+    d = mp(shape, backend)
+    info = host.plan_info(d)
+    assert info.total_bytes == host.scratch_size(d)
+    assert info.n_chunks == (L + 63) // 64
+    assert 1 <= info.chunks_per_group <= info.n_chunks
+    assert info.n_groups * info.chunks_per_group >= info.n_chunks
+    assert (info.n_groups - 1) * info.chunks_per_group < info.n_chunks
+    assert 1 <= info.seg_len <= info.chunks_per_group
+    assert info.segs_per_group == -(-info.chunks_per_group // info.seg_len)
+    hpg = H // G
+    assert info.hblk * info.n_hblk >= hpg and (info.n_hblk - 1) * info.hblk < hpg
+    state = S * H * P * N
+    es = 2 if backend == HELIX_BACKEND_MPP else 4
+    assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
+    want_sl = state * info.chunks_per_group * es if info.seg_len > 1 else 0
+    assert info.s_local_bytes == want_sl
+    assert info.s_seg_bytes == state * info.segs_per_group * 4
+    # every region 256-byte aligned and the total covers them all
+    assert info.total_bytes % 256 == 0
+    assert info.total_bytes >= want_sl + info.s_seg_bytes
+    assert info.launches == 3 * info.n_groups
+
+
+def test_plan_single_group_for_baseline_configs(host):
+    # With the default budget every BASELINE config runs as one group.
+    for name, shape in CONFIG_SHAPES.items():
+        for b in (HELIX_BACKEND_SGMMA, HELIX_BACKEND_MPP):
+            assert host.plan_info(mp(shape, b)).n_groups == 1, name
+
+
+def test_tiny_budget_forces_many_groups(host):
+    shape = (2048, 1, 8, 64, 128, 2)
+    with env(HELIX_SCRATCH_MB=1):
+        info = host.plan_info(mp(shape))
+        assert info.n_groups > 1
+        # 1 MiB admits at least one chunk; never more than the budget unless
+        # a single chunk alone exceeds it.
+        one_chunk = 8 * 64 * 128 * 2
+        assert info.total_bytes <= max(1 << 20, 2 * one_chunk + 4096) or info.chunks_per_group == 1
+    with env(HELIX_SCRATCH_MB=None):
+        assert host.plan_info(mp(shape)).n_groups == 1
+
+
+def test_scratch_zero_for_single_pass(host):
+    d = mp(CONFIG_SHAPES["cfg1"])
+    d.multipass = False
+    assert host.scratch_size(d) == 0
+
+
+def test_seg_len_and_hblk_overrides(host):
+    shape = CONFIG_SHAPES["cfg2"]
+    with env(HELIX_SEG_LEN=4, HELIX_HBLK=8):
+        info = host.plan_info(mp(shape))
+        assert info.seg_len == 4 and info.hblk == 8 and info.n_hblk == 1
+
+
+# ---------------------------------------------------------------------------
+# Encode argument validation (reference dispatch.mm:55-153): no GPU needed,
+# every error is detected before anything is enqueued.
+# ---------------------------------------------------------------------------
+
+def _tensors(n=10, ptr=0x1000):
+    return [HelixTensor(ptr + 0x100 * i, 0) for i in range(n)]
+
+
+def test_encode_errors(host):
+    d = mp((128, 1, 2, 64, 128, 1))
+    s0, x, dt, A, B, C, ids, y, s1, sc = _tensors()
+    L = abi.lib()
+    # null context / descriptor
+    assert L.helix_scan_encode(None, None, ctypes.byref(d), s0, x, dt, A, B, C, ids, y, s1, sc) == HELIX_ERR_INVALID_ARG
+    assert L.helix_scan_encode(host.handle, None, None, s0, x, dt, A, B, C, ids, y, s1, sc) == HELIX_ERR_INVALID_ARG
+    # null required tensor
+    assert host.encode(0, d, s0, x, HELIX_TENSOR_NULL, A, B, C, ids, y, s1, sc) == HELIX_ERR_INVALID_ARG
+    assert "null tensor" in host.last_error()
+    # unsupported shape
+    bad = d.copy()
+    bad.chunk = 32
+    assert host.encode(0, bad, s0, x, dt, A, B, C, ids, y, s1, sc) == HELIX_ERR_UNSUPPORTED_SHAPE
+    # host-only context: refuses before touching HIP
+    assert host.encode(0, d, s0, x, dt, A, B, C, ids, y, s1, sc) == HELIX_ERR_NO_DEVICE
+    assert host.encode(0, d, s0, x, dt, A, B, C, ids, y, s1, sc, into=True) == HELIX_ERR_NO_DEVICE
+    assert "host-only" in host.last_error()
+
+
+def test_last_error_is_per_thread(host):
+    import threading
+    d = mp((128, 1, 2, 64, 128, 1))
+    d.chunk = 32
+    t = _tensors()
+    host.encode(0, d, *t)
+    mine = host.last_error()
+    seen = []
+    th = threading.Thread(target=lambda: seen.append(host.last_error()))
+    th.start()
+    th.join()
+    assert mine and seen == [""]
+
+
+def test_ctx_create_reports_missing_device():
+    # No GPU in this container: creation must fail cleanly with a message.
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(abi.HelixError) as e:
+        abi.Context(0)
+    assert e.value.status == HELIX_ERR_NO_DEVICE
+
+
+# ---------------------------------------------------------------------------
+# Kernel algebra on the CPU: the two-level scheme equals the recurrence
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("seg_len,cpg", [(1, None), (3, None), (4, 5), (2, 1), (16, None)])
+@pytest.mark.parametrize("memory", ["short", "long"])
+def test_two_level_algebra(seg_len, cpg, memory):
+    p = po.problem_harness(700, 2, 4, 24, 16, 2, 4242, memory)
+    p.ids = np.array([1, 0], np.int32)
+    y, s1 = po.scan(p)
+    ym, sm = two_level_scan(p.s0, p.x, p.dt, p.A, p.B, p.C, ids=p.ids, seg_len=seg_len,
+                            chunks_per_group=cpg)
+    assert po.allclose_ratio(ym, y, 1e-6, 1e-9) <= 1.0
+    assert po.allclose_ratio(sm, s1, 1e-6, 1e-9) <= 1.0
+
+
+def test_flop_and_byte_counts_match_baseline():
+    # BASELINE.md section 2 / reference bench_scan.mm:205-209.
+    assert abs(algorithmic_flops(2048, 1, 64, 64, 128) / 1e9 - 5.931) < 1e-3
+    assert abs(algorithmic_flops(8192, 1, 64, 64, 128) / 1e9 - 23.723) < 1e-3
+    assert abs(algorithmic_bytes(8192, 1, 64, 64, 128, 8) / 1e6 - 341.8) < 0.1
+    assert abs(algorithmic_flops(4096, 8, 80, 64, 128) / 1e9 - 118.615) < 1e-2
