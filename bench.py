@@ -57,9 +57,11 @@ def make_inputs(seed: int, dev):
 
 
 class Variant:
-    def __init__(self, name, ctx, backend, tensors):
+    def __init__(self, name, ctx, backend, tensors, env=None):
         self.name = name
         self.ctx = ctx
+        self.env = env or {}
+        saved = self._push()
         x, dt, A, B, C, s0 = tensors
         self.y = torch.empty_like(x)
         self.s1 = torch.empty_like(s0)
@@ -71,11 +73,26 @@ class Variant:
         self.scratch = torch.empty(max(1, ctx.scratch_size(self.d)), dtype=torch.uint8,
                                    device=x.device)
         self.args = [tensor_arg(t) for t in (s0, x, dt, A, B, C)]
+        self._pop(saved)
+
+    def _push(self):
+        saved = {k: os.environ.get(k) for k in self.env}
+        os.environ.update(self.env)
+        return saved
+
+    def _pop(self, saved):
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
     def encode(self, stream):
         s0, x, dt, A, B, C = self.args
+        saved = self._push()
         rc = self.ctx.encode(stream.cuda_stream, self.d, s0, x, dt, A, B, C, tensor_arg(None),
                              tensor_arg(self.y), tensor_arg(self.s1), tensor_arg(self.scratch))
+        self._pop(saved)
         if rc != HELIX_OK:
             raise RuntimeError(f"{self.name}: encode failed {rc}: {self.ctx.last_error()}")
 
@@ -157,6 +174,8 @@ def main():
     ap.add_argument("--warmup-ms", type=float, default=800.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--variants", action="store_true",
+                    help="also time alternative kernel choices (reported under 'variants')")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
                     help="also run a plain device copy of this size (a known-traffic kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -174,6 +193,10 @@ def main():
     stream = torch.cuda.current_stream(dev)
     variants = [Variant("bf16", ctx, HELIX_BACKEND_MPP, tensors),
                 Variant("fp32", ctx, HELIX_BACKEND_SGMMA, tensors)]
+    if args.variants:
+        # Alternative kernel choices, timed interleaved in the same process.
+        variants.append(Variant("bf16-walk", ctx, HELIX_BACKEND_MPP, tensors,
+                                env={"HELIX_BF16_PASSC": "walk"}))
 
     # Warm-up: W steps each, then alternate until the wall clock has run
     # warmup_ms (the reference's protocol against clock ramps).
@@ -273,6 +296,11 @@ def main():
             "kernel": results["fp32"]["kernel"],
         },
     }
+    extra = [v for v in variants if v.name not in ("bf16", "fp32")]
+    if extra:
+        out["variants"] = {v.name: {"ms_per_step": results[v.name]["ms"], "kernel": results[v.name]["kernel"],
+                                    "passes_ms_median": {k: results[v.name]["passes"][k]["median"] for k in "ABC"}}
+                           for v in extra}
     if args.calib_copy:
         n = args.calib_copy * (1 << 20) // 4
         src = torch.randn(n, device=dev)

@@ -5,3 +5,4 @@
 #include "pass_b.hip"
 #include "pass_c_f32.hip"
 #include "pass_c_bf16.hip"
+#include "pass_c_walk.hip"

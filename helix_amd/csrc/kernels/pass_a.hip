@@ -73,8 +73,12 @@ __device__ __forceinline__ void load_stage_a(StageA<NP>& st, const HelixScanPara
     }
 }
 
-template <int NP, bool SBF>
+// MODE 0: store R_c as fp32 (fp32 path); 1: as bf16 (bf16 chunk-parallel
+// Pass C); 2: store nothing per chunk, only the segment aggregate D_s (the
+// chunk-walking Pass C recomputes R_c itself).
+template <int NP, int MODE>
 __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr bool SBF = MODE == 1;
     constexpr int NTW = NP / 64;      // N tiles per wave (NP/32 tiles over 2 waves)
     constexpr int RSX = HELIX_HD;     // row stride of dtXs
     constexpr int RSB = NP;           // row stride of B
@@ -142,7 +146,7 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
             }
         }
 
-        if (c > c_begin)
+        if (MODE != 2 && c > c_begin)
             store_state_tiles<NP, SBF>(acc, sl_base + (long long)c * p.sl_cg * (SBF ? 2 : 4),
                                        pw, N, pt, nt0, lo, hi);
         if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
@@ -177,11 +181,15 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
 #define HELIX_PASS_A(NP)                                                                        \
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_f32_n##NP(          \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        chunk_state_impl<NP, false>(p, b);                                                      \
+        chunk_state_impl<NP, 0>(p, b);                                                          \
     }                                                                                           \
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_sbf_n##NP(          \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        chunk_state_impl<NP, true>(p, b);                                                       \
+        chunk_state_impl<NP, 1>(p, b);                                                          \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_agg_n##NP(          \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_impl<NP, 2>(p, b);                                                          \
     }
 
 HELIX_PASS_A(64)

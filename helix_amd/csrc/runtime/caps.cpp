@@ -21,13 +21,13 @@ namespace {
 constexpr HelixMatmulTraits kF32Traits[] = {
     {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=64)", "helix_chunk_state_f32_n64",
      "helix_state_scan_f32", "helix_chunk_out_f32_n64", false,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 64},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 64, false},
     {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=128)", "helix_chunk_state_f32_n128",
      "helix_state_scan_f32", "helix_chunk_out_f32_n128", false,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 128},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 128, false},
     {HELIX_BACKEND_SGMMA, "mfma fp32 (d_state<=256)", "helix_chunk_state_f32_n256",
      "helix_state_scan_f32", "helix_chunk_out_f32_n256", false,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 256},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x2_f32", 256, false},
 };
 
 // The bf16 path (the reference's MPP slot): Pass C on v_mfma_f32_32x32x16_bf16
@@ -36,13 +36,28 @@ constexpr HelixMatmulTraits kF32Traits[] = {
 constexpr HelixMatmulTraits kBf16Traits[] = {
     {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=64)", "helix_chunk_state_sbf_n64",
      "helix_state_scan_f32", "helix_chunk_out_bf16_n64", true,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 64},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 64, false},
     {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=128)", "helix_chunk_state_sbf_n128",
      "helix_state_scan_f32", "helix_chunk_out_bf16_n128", true,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 128},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 128, false},
     {HELIX_BACKEND_MPP, "mfma bf16 pass C (d_state<=256)", "helix_chunk_state_sbf_n256",
      "helix_state_scan_f32", "helix_chunk_out_bf16_n256", true,
-     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256},
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256, false},
+};
+
+// Alternative bf16 path: Pass A stores only segment aggregates (fp32) and
+// Pass C walks each segment's chunks with the state in registers, so no
+// per-chunk state is written or read. Passes A and B remain fp32.
+constexpr HelixMatmulTraits kBf16WalkTraits[] = {
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C, chunk walk (d_state<=64)", "helix_chunk_state_agg_n64",
+     "helix_state_scan_f32", "helix_scan_walk_bf16_n64", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 64, true},
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C, chunk walk (d_state<=128)", "helix_chunk_state_agg_n128",
+     "helix_state_scan_f32", "helix_scan_walk_bf16_n128", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 128, true},
+    {HELIX_BACKEND_MPP, "mfma bf16 pass C, chunk walk (d_state<=256)", "helix_chunk_state_agg_n256",
+     "helix_state_scan_f32", "helix_scan_walk_bf16_n256", true,
+     "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256, true},
 };
 
 const char* const kKernelNames[] = {
@@ -51,6 +66,8 @@ const char* const kKernelNames[] = {
     "helix_state_scan_f32",
     "helix_chunk_out_f32_n64",    "helix_chunk_out_f32_n128",   "helix_chunk_out_f32_n256",
     "helix_chunk_out_bf16_n64",   "helix_chunk_out_bf16_n128",  "helix_chunk_out_bf16_n256",
+    "helix_chunk_state_agg_n64",  "helix_chunk_state_agg_n128", "helix_chunk_state_agg_n256",
+    "helix_scan_walk_bf16_n64",   "helix_scan_walk_bf16_n128",  "helix_scan_walk_bf16_n256",
 };
 
 int np_index(int d_state) {
@@ -99,7 +116,14 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
         if (f[0] == 's') return kF32Traits[k];
     const bool want_bf16 = d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP;
-    if (want_bf16 && d.multipass) return kBf16Traits[k];
+    if (want_bf16 && d.multipass) {
+        // HELIX_BF16_PASSC=walk selects the chunk-walking Pass C (state in
+        // registers, no per-chunk scratch); the chunk-parallel one is the
+        // default while it is the faster of the two.
+        if (const char* v = std::getenv("HELIX_BF16_PASSC"))
+            if (v[0] == 'w') return kBf16WalkTraits[k];
+        return kBf16Traits[k];
+    }
     return kF32Traits[k];
 }
 
@@ -126,13 +150,13 @@ int choose_seg_len(const helix_scan_desc& d, int cpg) {
     return (int)std::max<long>(1, std::min<long>(len, cpg));
 }
 
-void layout(const helix_scan_desc& d, bool bf16_state, int cpg, MultipassPlan* pl) {
+void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int cpg, MultipassPlan* pl) {
     const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
     pl->chunks_per_group = cpg;
     pl->seg_len = choose_seg_len(d, cpg);
     pl->segs_per_group = (cpg + pl->seg_len - 1) / pl->seg_len;
     pl->sl_elem_bytes = bf16_state ? 2 : 4;
-    pl->sl_elems = pl->seg_len > 1 ? state * (size_t)cpg : 0;
+    pl->sl_elems = (pl->seg_len > 1 && !walk) ? state * (size_t)cpg : 0;
     pl->sg_elems = state * (size_t)pl->segs_per_group;
     pl->ld_elems = (size_t)d.n_seq * cpg * d.n_head;
     pl->sd_elems = (size_t)d.n_seq * pl->segs_per_group * d.n_head;
@@ -146,7 +170,8 @@ void layout(const helix_scan_desc& d, bool bf16_state, int cpg, MultipassPlan* p
 
 }  // namespace
 
-MultipassPlan plan_multipass(const helix_scan_desc& d, bool bf16_state) {
+MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& tr) {
+    const bool bf16_state = tr.bf16_state;
     MultipassPlan pl;
     if (d.n_tok <= 0 || d.n_seq <= 0 || d.n_head <= 0 || d.head_dim <= 0 || d.d_state <= 0 ||
         d.n_group <= 0)
@@ -155,11 +180,13 @@ MultipassPlan plan_multipass(const helix_scan_desc& d, bool bf16_state) {
 
     const size_t budget = scratch_budget_bytes();
     const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
-    const size_t per_chunk = state * (bf16_state ? 2 : 4);
+    // A walking Pass C keeps no per-chunk state; only segment aggregates
+    // (about one state per seg_len chunks) count against the budget.
+    const size_t per_chunk = tr.walk ? state : state * (bf16_state ? 2 : 4);
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(d, bf16_state, (int)cpg, &pl);
+        layout(d, bf16_state, tr.walk, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }
@@ -256,8 +283,7 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
 
 extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
     if (!d || !d->multipass) return 0;
-    const bool bf16 = helix::rt::select_traits(ctx, *d).bf16_state;
-    return helix::rt::plan_multipass(*d, bf16).total_bytes;
+    return helix::rt::plan_multipass(*d, helix::rt::select_traits(ctx, *d)).total_bytes;
 }
 
 extern "C" helix_backend helix_ctx_select_backend(helix_ctx* ctx, const helix_scan_desc* d) {

@@ -11,7 +11,8 @@
 //   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
 //   Pass B  grid (ceil(P*N/256), n_head, n_seq)         x 256 threads
 //   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
-//           decoded XCD-aware in the kernel)
+//           decoded XCD-aware in the kernel); the walking variant runs one
+//           workgroup per (segment, head, P slab, seq) instead
 // The ragged-tail padding and the bf16 staging of B and C that the reference
 // runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
 // staging here, so there is nothing to launch before the group loop.
@@ -57,7 +58,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     params.has_ids = ids.buf ? 1 : 0;
 
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
-    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(*d, tr.bf16_state);
+    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(*d, tr);
     if (plan.n_chunks <= 0) {
         set_error(ctx, "empty problem");
         return HELIX_ERR_INVALID_ARG;
@@ -156,10 +157,12 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         if (e == hipSuccess && do_b)
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
-        if (e == hipSuccess && do_c)
-            e = hipModuleLaunchKernel(fC, (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) *
-                                          (unsigned)d->n_seq,
-                                      1, 1, HELIX_WG, 1, 1, 0, stream, args, nullptr);
+        if (e == hipSuccess && do_c) {
+            const unsigned n_wg = tr.walk
+                ? (unsigned)params.n_seg * (unsigned)d->n_head * (unsigned)params.n_pslab * (unsigned)d->n_seq
+                : (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) * (unsigned)d->n_seq;
+            e = hipModuleLaunchKernel(fC, n_wg, 1, 1, HELIX_WG, 1, 1, 0, stream, args, nullptr);
+        }
         if (e != hipSuccess) {
             (void)hipGetLastError();
             set_error(ctx, std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -197,7 +200,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     if (!ctx || !d || !out) return HELIX_ERR_INVALID_ARG;
     if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
-    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr.bf16_state);
+    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr);
     std::memset(out, 0, sizeof(*out));
     out->n_chunks = pl.n_chunks;
     out->chunks_per_group = pl.chunks_per_group;

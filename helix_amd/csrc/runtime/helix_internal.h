@@ -37,6 +37,10 @@ struct HelixMatmulTraits {
     const char*   mfma_a;          // MFMA instruction of Pass A
     const char*   mfma_c;          // MFMA instruction of Pass C
     int           np;              // d_state padding the kernels are built for
+    // Pass C walks the chunks of each segment with the state in registers
+    // (one workgroup per segment x head x P slab); Pass A then stores only the
+    // segment aggregates and there is no per-chunk state in scratch.
+    bool          walk;
 };
 
 namespace helix::rt {
@@ -71,7 +75,7 @@ struct MultipassPlan {
     size_t total_bytes      = 0;
 };
 
-MultipassPlan plan_multipass(const helix_scan_desc& d, bool bf16_state);
+MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& tr);
 
 // Scratch budget in bytes: $HELIX_SCRATCH_MB or the default.
 size_t scratch_budget_bytes();

@@ -54,15 +54,18 @@ SHAPES = [
 ]
 
 MODES = [
-    # (label, backend, scratch_mb, memory)
-    ("fp32", HELIX_BACKEND_SGMMA, None, "short"),
-    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short"),
-    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long"),
-    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long"),
-    ("bf16", HELIX_BACKEND_MPP, None, "short"),
-    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short"),
-    ("bf16/long", HELIX_BACKEND_MPP, None, "long"),
-    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long"),
+    # (label, backend, scratch_mb, memory, bf16 Pass C variant)
+    ("fp32", HELIX_BACKEND_SGMMA, None, "short", None),
+    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", None),
+    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", None),
+    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", None),
+    ("bf16", HELIX_BACKEND_MPP, None, "short", None),
+    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", None),
+    ("bf16/long", HELIX_BACKEND_MPP, None, "long", None),
+    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long", None),
+    ("bf16walk", HELIX_BACKEND_MPP, None, "short", "walk"),
+    ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", "walk"),
+    ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", "walk"),
 ]
 
 
@@ -77,12 +80,12 @@ def _reference(shape, memory):
 @pytest.mark.parametrize("mode", MODES, ids=[m[0] for m in MODES])
 @pytest.mark.parametrize("shape", SHAPES, ids=[s[-1] for s in SHAPES])
 def test_shape_matrix(gpu, shape, mode):
-    label, backend, scratch_mb, memory = mode
+    label, backend, scratch_mb, memory, passc = mode
     p, y_ref, s_ref = _reference(shape, memory)
     d = p.d.copy()
     d.multipass = True
     d.backend = backend
-    with env(HELIX_SCRATCH_MB=scratch_mb):
+    with env(HELIX_SCRATCH_MB=scratch_mb, HELIX_BF16_PASSC=passc):
         assert gpu.supported(d), gpu.backend_desc(d)
         is_bf16 = gpu.select_backend(d) == HELIX_BACKEND_MPP
         _, y, s1 = run(gpu, p, desc=d)
@@ -114,6 +117,7 @@ def _baseline(name, memory):
 
 
 CASES = [(n, path, mem) for n, c in CONFIGS.items() for path in c.paths for mem in ("dist", "long")]
+CASES += [(n, "bf16walk", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
 
 
 @pytest.mark.parametrize("name,path,memory", CASES, ids=[f"{n}-{p}-{m}" for n, p, m in CASES])
@@ -122,11 +126,13 @@ def test_baseline_config(gpu, name, path, memory):
     p, y_ref, s_ref = _baseline(name, memory)
     d = p.d.copy()
     d.multipass = True
-    d.backend = HELIX_BACKEND_MPP if path == "bf16" else HELIX_BACKEND_SGMMA
-    assert gpu.supported(d)
-    assert (gpu.select_backend(d) == HELIX_BACKEND_MPP) == (path == "bf16")
-    print(f"[{name} {path} {memory}] {gpu.backend_desc(d)}", flush=True)
-    _, y, s1 = run(gpu, p, desc=d)
+    d.backend = HELIX_BACKEND_MPP if path.startswith("bf16") else HELIX_BACKEND_SGMMA
+    with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None):
+        assert gpu.supported(d)
+        assert (gpu.select_backend(d) == HELIX_BACKEND_MPP) == path.startswith("bf16")
+        print(f"[{name} {path} {memory}] {gpu.backend_desc(d)}", flush=True)
+        _, y, s1 = run(gpu, p, desc=d)
+    path = "bf16" if path.startswith("bf16") else path
     hs = list(c.check_heads)
     ey = po.max_rel_err(y[:, :, hs], y_ref[:, :, hs])
     es = po.max_rel_err(s1[:, hs], s_ref[:, hs])

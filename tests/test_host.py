@@ -173,6 +173,8 @@ def test_backend_selection(host):
     assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
     assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C (d_state<=256)"
+    with env(HELIX_BF16_PASSC="walk"):
+        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=64)"
     d = mp(shape)
     d.multipass = False
@@ -185,9 +187,15 @@ def test_backend_selection(host):
 # Scratch planning (reference caps.mm:153-241)
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("passc", [None, "walk"])
 @pytest.mark.parametrize("name", list(CONFIG_SHAPES))
 @pytest.mark.parametrize("backend", [HELIX_BACKEND_SGMMA, HELIX_BACKEND_MPP])
-def test_plan_invariants(host, name, backend):
+def test_plan_invariants(host, name, backend, passc):
+    with env(HELIX_BF16_PASSC=passc):
+        _plan_invariants(host, name, backend)
+
+
+def _plan_invariants(host, name, backend):
     shape = CONFIG_SHAPES[name]
     L, S, H, P, N, G = shape
     d = mp(shape, backend)
@@ -204,7 +212,8 @@ def test_plan_invariants(host, name, backend):
     state = S * H * P * N
     es = 2 if backend == HELIX_BACKEND_MPP else 4
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
-    want_sl = state * info.chunks_per_group * es if info.seg_len > 1 else 0
+    walk = backend == HELIX_BACKEND_MPP and os.environ.get("HELIX_BF16_PASSC") == "walk"
+    want_sl = state * info.chunks_per_group * es if (info.seg_len > 1 and not walk) else 0
     assert info.s_local_bytes == want_sl
     assert info.s_seg_bytes == state * info.segs_per_group * 4
     # every region 256-byte aligned and the total covers them all
