@@ -122,7 +122,145 @@ HELIX_DEV f32x16 zero16() {
     return z;
 }
 
+// Offset of one head's slab tile in the state scratch (see helix_params.h).
+HELIX_DEV long long state_tile_off(const HelixScanParams& p, int h, int slab) {
+    return ((long long)h * p.n_pslab + slab) * (long long)(64 * p.np);
+}
+
+// Slab tile layout (helix_params.h): 16-byte (fp32) or 8-byte (bf16) units of
+// four consecutive state indices n for one p, in the order of the MFMA result
+// registers of R[n][p] (M = n, N = p):
+//   unit(pt, nt, r4, lane) = ((pt * NT + nt) * 4 + r4) * 64 + lane
+//   holds p = pt*32 + lane%32, n = nt*32 + 8*r4 + 4*(lane/32) + 0..3,
+// i.e. result registers 4 r4 .. 4 r4 + 3 of tile (nt, pt).
+HELIX_DEV int tile_unit(int NT, int pt, int nt, int r4, int lane) {
+    return ((pt * NT + nt) * 4 + r4) * 64 + lane;
+}
+
 // Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
 HELIX_DEV __bf16 to_bf16(float v) { return (__bf16)v; }
+
+// Raw buffer access. The resource (base and byte range) sits in four SGPRs,
+// the lane's byte offset is one 32-bit VGPR, and a compile-time byte offset
+// goes to the instruction's soffset/immediate fields, so a run of loads from
+// one wave-uniform region costs no per-load address VGPRs (flat/global loads
+// need a 64-bit VGPR address each once offsets exceed the 4 KiB immediate).
+// `base` must be wave-uniform. Raw buffer range checking (stride 0) returns 0
+// for a read at or past `bytes` and drops such a write.
+typedef __amdgpu_buffer_rsrc_t helix_rsrc;
+
+HELIX_DEV helix_rsrc make_rsrc(const void* base, unsigned bytes) {
+    // Dword 3 = 0x00020000: DATA_FORMAT 32, the value gfx9-family untyped
+    // buffer instructions are used with.
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+HELIX_DEV float buf_f32(helix_rsrc r, int voff, int soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+HELIX_DEV __bf16 buf_bf16(helix_rsrc r, int voff, int soff) {
+    return __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+}
+// Element load from a buffer of T (float or __bf16); offsets in elements.
+template <typename T>
+HELIX_DEV T buf_elem(helix_rsrc r, int vidx, int sidx) {
+    if constexpr (sizeof(T) == 4)
+        return buf_f32(r, vidx * 4, sidx * 4);
+    else
+        return buf_bf16(r, vidx * 2, sidx * 2);
+}
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One tile unit (four state values) as fp32, from an fp32 or bf16 tile.
+// `unit` is the unit index; bf16 units are 8 bytes, fp32 units 16.
+template <typename T>
+HELIX_DEV f32x4 buf_unit(helix_rsrc r, int vunit, int sunit) {
+    f32x4 o;
+    if constexpr (sizeof(T) == 4) {
+        o = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vunit * 16, sunit * 16, 0));
+    } else {
+        const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vunit * 8, sunit * 8, 0);
+        o[0] = __builtin_bit_cast(float, w[0] << 16);
+        o[1] = __builtin_bit_cast(float, w[0] & 0xffff0000u);
+        o[2] = __builtin_bit_cast(float, w[1] << 16);
+        o[3] = __builtin_bit_cast(float, w[1] & 0xffff0000u);
+    }
+    return o;
+}
+// Raw 16-byte unit of an fp32 tile or 8-byte unit of a bf16 tile, kept as
+// loaded (no conversion, so the load has no consumer until it is used).
+template <typename T> struct RawUnit { typedef u32x4 type; };
+template <> struct RawUnit<__bf16> { typedef u32x2 type; };
+
+template <typename T>
+HELIX_DEV typename RawUnit<T>::type buf_unit_raw(helix_rsrc r, int vunit, int sunit) {
+    if constexpr (sizeof(T) == 4)
+        return __builtin_amdgcn_raw_buffer_load_b128(r, vunit * 16, sunit * 16, 0);
+    else
+        return __builtin_amdgcn_raw_buffer_load_b64(r, vunit * 8, sunit * 8, 0);
+}
+HELIX_DEV f32x4 unit_to_f32(u32x4 w) { return __builtin_bit_cast(f32x4, w); }
+HELIX_DEV f32x4 unit_to_f32(u32x2 w) {
+    f32x4 o;
+    o[0] = __builtin_bit_cast(float, w[0] << 16);
+    o[1] = __builtin_bit_cast(float, w[0] & 0xffff0000u);
+    o[2] = __builtin_bit_cast(float, w[1] << 16);
+    o[3] = __builtin_bit_cast(float, w[1] & 0xffff0000u);
+    return o;
+}
+
+// Store four values as one tile unit of T (fp32: 16 bytes; bf16: rounded,
+// 8 bytes). Values go in by value: a bit cast of a vector element in place
+// reads element 0 with this compiler.
+template <typename T>
+HELIX_DEV void buf_store_unit(helix_rsrc r, float v0, float v1, float v2, float v3, int vunit, int sunit) {
+    if constexpr (sizeof(T) == 4) {
+        u32x4 w;
+        w[0] = __builtin_bit_cast(unsigned, v0);
+        w[1] = __builtin_bit_cast(unsigned, v1);
+        w[2] = __builtin_bit_cast(unsigned, v2);
+        w[3] = __builtin_bit_cast(unsigned, v3);
+        __builtin_amdgcn_raw_buffer_store_b128(w, r, vunit * 16, sunit * 16, 0);
+    } else {
+        u32x2 w;
+        w[0] = (unsigned)__builtin_bit_cast(unsigned short, to_bf16(v0)) |
+               ((unsigned)__builtin_bit_cast(unsigned short, to_bf16(v1)) << 16);
+        w[1] = (unsigned)__builtin_bit_cast(unsigned short, to_bf16(v2)) |
+               ((unsigned)__builtin_bit_cast(unsigned short, to_bf16(v3)) << 16);
+        __builtin_amdgcn_raw_buffer_store_b64(w, r, vunit * 8, sunit * 8, 0);
+    }
+}
+
+// Raw-register form of an element of T: a float stays a float, a bf16 stays
+// its 16 bits zero-extended in a 32-bit register. Loads into this form carry
+// no data dependence (nothing packs two 16-bit results into one register), so
+// a run of prefetch loads stays in flight until the value is used.
+template <typename T> struct RawReg { typedef float type; };
+template <> struct RawReg<__bf16> { typedef unsigned type; };
+
+template <typename T>
+HELIX_DEV typename RawReg<T>::type buf_raw(helix_rsrc r, int vidx, int sidx) {
+    if constexpr (sizeof(T) == 4)
+        return buf_f32(r, vidx * 4, sidx * 4);
+    else
+        return (unsigned)__builtin_amdgcn_raw_buffer_load_b16(r, vidx * 2, sidx * 2, 0);
+}
+HELIX_DEV float raw_to_f32(float v) { return v; }
+HELIX_DEV float raw_to_f32(unsigned bits) { return __builtin_bit_cast(float, bits << 16); }
+
+// Element store of v, as T (float, or rounded to __bf16); offsets in elements.
+template <typename T>
+HELIX_DEV void buf_store_elem(helix_rsrc r, float v, int vidx, int sidx) {
+    if constexpr (sizeof(T) == 4)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, vidx * 4, sidx * 4, 0);
+    else
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, to_bf16(v)), r, vidx * 2,
+                                              sidx * 2, 0);
+}
+
+// This thread's wave index, as a wave-uniform (SGPR) value: everything derived
+// from it (row offsets, branch conditions) then stays scalar.
+HELIX_DEV int wave_uniform() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 #endif  // HELIX_COMMON_H

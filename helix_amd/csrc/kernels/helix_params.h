@@ -25,12 +25,22 @@
  *           y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C S_init).
  *
  * Scratch layouts (elements; every region 256-byte aligned):
- *   s_local [seq][cg][head][P][N]    f32 (fp32 path) or bf16 (bf16 path)
- *   s_seg   [seq][seg][head][P][N]   f32: D_s from Pass A, S_seg after Pass B
- *   ld      [seq][cg][head]          f32: sum of chunk log-decays before c
- *                                         within c's segment
- *   segld   [seq][seg][head]         f32: whole-segment log-decay
- * [P][N] is the caller's state layout, so Pass B and s0/s1 coalesce together.
+ *   s_local [seq][cg][head][slab] x TILE   f32 (fp32 path) or bf16 (bf16 path)
+ *   s_seg   [seq][seg][head][slab] x TILE  f32: D_s from Pass A, S_seg after Pass B
+ *   ld      [seq][cg][head]                f32: sum of chunk log-decays before c
+ *                                               within c's segment
+ *   segld   [seq][seg][head]               f32: whole-segment log-decay
+ * A TILE holds one 64-channel slab of one head's state, [64 p][np n] padded,
+ * in the order Pass A's MFMA result registers hold it (v_mfma_f32_32x32x2_f32
+ * computing R[n][p], M = n, N = p), grouped in units of four registers:
+ *   unit(pt, nt, r4, lane) = ((pt * np/32 + nt) * 4 + r4) * 64 + lane
+ *   holds state[p = pt*32 + lane%32][n = nt*32 + 8*r4 + 4*(lane/32) + 0..3]
+ * A unit is four consecutive n of one p: 16 bytes in fp32, 8 in bf16. Each
+ * group of four result registers stores as one 16-byte (8-byte) write per
+ * lane, 1 KiB (512 B) contiguous per wave; Pass B moves s0/s1 as 16-byte runs
+ * of the caller's [P][N] layout; and a lane's units are the B operand of
+ * Pass C's C . S GEMM as they stand (the K order of an MFMA is free as long as
+ * both operands use the same one).
  */
 #ifndef HELIX_PARAMS_H
 #define HELIX_PARAMS_H
@@ -75,11 +85,12 @@ typedef struct HelixScanParams {
     int n_seg;            /* segments in this group = ceil(n_cg / seg_len) */
     int hblk;             /* heads per Pass C workgroup */
     int n_hblk;           /* head blocks per B/C group */
-    int pad0, pad1;
+    int np;               /* d_state padded to the kernels' tile width (64/128/256) */
+    int pad0;
 
     /* Scratch strides in elements (see the layout comment above). */
-    long long sl_cg, sl_seq;     /* s_local: chunk stride (H*P*N), seq stride */
-    long long sg_seg, sg_seq;    /* s_seg: segment stride (H*P*N), seq stride */
+    long long sl_cg, sl_seq;     /* s_local: chunk stride (H*n_pslab*64*np), seq stride */
+    long long sg_seg, sg_seq;    /* s_seg: segment stride (H*n_pslab*64*np), seq stride */
     long long ld_seq;            /* ld: seq stride (n_cg_max * H); chunk stride H */
     long long sd_seq;            /* segld: seq stride (n_seg_max * H); seg stride H */
 } HelixScanParams;

@@ -12,31 +12,36 @@
 // so the per-chunk states reach HBM once (s_local) instead of three times,
 // and only the segment aggregates D_s go through Pass B.
 //
-// Tiling: the workgroup computes R^T[p][n] (64 x N) with v_mfma_f32_32x32x2_f32,
-// M = p, N = n, K = token. Wave w owns P tile (w & 1) and N tiles
-// (w >> 1) + 2i, so the A operand is loaded once per K step and reused across
-// its N tiles. Both operands come from LDS in their natural row-major staging
-// (dtXs[j][p], B[j][n]); R^T tiles store as 128-byte rows of the [P][N] layout.
+// Tiling: the workgroup computes R[n][p] (N x 64) with v_mfma_f32_32x32x2_f32,
+// M = n, N = p, K = token. Wave w owns P tile (w & 1) and N tiles
+// (w >> 1) + 2i, so the dtXs operand is loaded once per K step and reused
+// across its N tiles. Both operands come from LDS in their natural row-major
+// staging (dtXs[j][p], B[j][n]); the result registers store as the scratch
+// tile's units (four consecutive n of one p per lane).
 #include "helix_common.h"
 
+// Store this wave's accumulator tiles (R[n][p] tiles (nt0 + 2i, pt)) into a
+// slab tile (helix_params.h layout): result registers 4 r4 .. 4 r4 + 3 are
+// one unit, so each lane writes 16 (fp32) or 8 (bf16) bytes per four registers
+// and a wave 1 KiB / 512 B contiguous. No guards: the padding of a partial
+// slab or of d_state < np holds zeros, because the matching dtXs columns and
+// B columns were staged as zeros.
 template <int NP, bool SBF>
-__device__ __forceinline__ void store_state_tiles(const f32x16* acc, void* dst_base, int pw, int N,
-                                                  int pt, int nt0, int lo, int hi) {
+__device__ __forceinline__ void store_state_tiles(const f32x16* acc, helix_rsrc dst, int pt, int nt0,
+                                                  int lane) {
+    constexpr int NT = NP / 32;
     constexpr int NTW = NP / 64;
-    const bool full = (pw == HELIX_HD) && (N == NP);
 #pragma unroll
     for (int i = 0; i < NTW; ++i) {
-        const int n = (nt0 + 2 * i) * 32 + lo;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int pr = pt * 32 + acc_row(r, hi);
-            if (full || (pr < pw && n < N)) {
-                const long long off = (long long)pr * N + n;
-                if (SBF)
-                    static_cast<__bf16*>(dst_base)[off] = to_bf16(acc[i][r]);
-                else
-                    static_cast<float*>(dst_base)[off] = acc[i][r];
-            }
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int u = tile_unit(NT, pt, nt0 + 2 * i, r4, 0);
+            const float v0 = acc[i][4 * r4], v1 = acc[i][4 * r4 + 1];
+            const float v2 = acc[i][4 * r4 + 2], v3 = acc[i][4 * r4 + 3];
+            if (SBF)
+                buf_store_unit<__bf16>(dst, v0, v1, v2, v3, lane, u);
+            else
+                buf_store_unit<float>(dst, v0, v1, v2, v3, lane, u);
         }
     }
 }
@@ -61,15 +66,20 @@ __device__ __forceinline__ void load_stage_a(StageA<NP>& st, const HelixScanPara
                                              int wave, int pw, int N) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
-    st.dtraw = dt_h[(long long)(t0 + min(lane, tlen - 1)) * p.s_dt[0]];
-    const long long xc = (long long)min(lane, pw - 1) * p.s_x[2];
+    // One buffer resource per tensor, based at the chunk's first token; the
+    // host keeps a chunk's extent below 2 GiB so the offsets fit 32 bits.
+    const int sdt = (int)p.s_dt[0], sx0 = (int)p.s_x[0], sx2 = (int)p.s_x[2], sb0 = (int)p.s_b[0];
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    const helix_rsrc rb  = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int jr = min(wave + 4 * i, tlen - 1);
-        st.x[i] = x_h[(long long)(t0 + jr) * p.s_x[0] + xc];
-        const float* brow = B_g + (long long)(t0 + jr) * p.s_b[0];
+        st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
 #pragma unroll
-        for (int m = 0; m < NP / 64; ++m) st.b[i][m] = brow[min(lane + 64 * m, N - 1)];
+        for (int m = 0; m < NP / 64; ++m) st.b[i][m] = buf_elem<float>(rb, min(lane + 64 * m, N - 1), jr * sb0);
     }
 }
 
@@ -86,7 +96,7 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
     __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSB];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
 
     const int seg  = blockIdx.x;
     const int h    = blockIdx.y;
@@ -95,7 +105,6 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
     const int p0   = slab * HELIX_HD;
     const int pw   = min(HELIX_HD, p.head_dim - p0);
     const int N    = p.d_state;
-    const int P    = p.head_dim;
     const int g    = h / p.heads_per_group;
 
     const int c_begin = seg * p.seg_len;
@@ -107,9 +116,8 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
     const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
     const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
 
-    const long long head_off = (long long)h * P * N + (long long)p0 * N;
-    char* sl_base = static_cast<char*>(b.s_local) +
-                    (seq * p.sl_seq + head_off) * (SBF ? 2 : 4);
+    const long long tile_off = state_tile_off(p, h, slab);
+    const unsigned tile_elems = 64u * NP;
 
     const int pt  = wave & 1;
     const int nt0 = wave >> 1;
@@ -146,9 +154,12 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
             }
         }
 
-        if (MODE != 2 && c > c_begin)
-            store_state_tiles<NP, SBF>(acc, sl_base + (long long)c * p.sl_cg * (SBF ? 2 : 4),
-                                       pw, N, pt, nt0, lo, hi);
+        if (MODE != 2 && c > c_begin) {
+            const long long off = seq * p.sl_seq + (long long)c * p.sl_cg + tile_off;
+            const void* dst = SBF ? (const void*)(static_cast<const __bf16*>(b.s_local) + off)
+                                  : (const void*)(static_cast<const float*>(b.s_local) + off);
+            store_state_tiles<NP, SBF>(acc, make_rsrc(dst, tile_elems * (SBF ? 2u : 4u)), pt, nt0, lane);
+        }
         if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
         __syncthreads();
 
@@ -159,22 +170,24 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
 #pragma unroll
         for (int i = 0; i < NTW; ++i) acc[i] *= a_c;
 
+        // R[n][p] += sum_j B[j][n] dtXs[j][p]: A operand B (M = n), B operand
+        // dtXs (N = p), K = token.
 #pragma unroll 8
         for (int s = 0; s < HELIX_CS / 2; ++s) {
             const int j = 2 * s + hi;
-            const float av = sX[j * RSX + pt * 32 + lo];
+            const float xv = sX[j * RSX + pt * 32 + lo];
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
                 const float bv = sB[j * RSB + (nt0 + 2 * i) * 32 + lo];
-                acc[i] = mfma_f32(av, bv, acc[i]);
+                acc[i] = mfma_f32(bv, xv, acc[i]);
             }
         }
         lam += (float)lend;
         __syncthreads();
     }
 
-    float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + head_off;
-    store_state_tiles<NP, false>(acc, sg, pw, N, pt, nt0, lo, hi);
+    const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
+    store_state_tiles<NP, false>(acc, make_rsrc(sg, tile_elems * 4u), pt, nt0, lane);
     if (slab == 0 && tid == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
 }
 

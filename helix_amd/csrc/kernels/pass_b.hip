@@ -6,11 +6,11 @@
 // (a1, b1).(a2, b2) = (a1 a2, a2 b1 + b2) (multipass.metal:10-15).
 //
 // Pass A has already folded each segment's chunks into one (decay, D) pair,
-// so this walk is seg_len times shorter than the reference's. One lane per
-// state element of one (seq, head): the [P][N] element index is contiguous,
-// so every segment row, s0 row and s1 row moves as full 256-byte wave
-// transactions. The D loads of a block of segments are issued before the
-// dependent FMA chain so the loads overlap.
+// so this walk is seg_len times shorter than the reference's. One thread per
+// tile unit (four consecutive n of one p, helix_params.h layout) of one
+// (seq, head): every segment row moves as 16-byte lane accesses, 1 KiB
+// contiguous per wave. The D loads of a block of segments are issued before
+// the dependent FMA chain so the loads overlap.
 //
 //   carry = s0[ids[seq]] (first group) or s1[seq] (later groups)
 //   for s: S_seg(s) = carry (in place over D_s); carry = exp(segld_s) carry + D_s
@@ -20,36 +20,60 @@
 extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(HelixScanParams p,
                                                                            HelixScanBuffers b) {
     constexpr int BLK = 8;
-    const long long PN = (long long)p.head_dim * p.d_state;
-    const long long e  = (long long)blockIdx.x * HELIX_WG + threadIdx.x;
+    const int units_tile = 16 * p.np;                    // 64 * np / 4
+    const int per_head = p.n_pslab * units_tile;
+    const int u   = blockIdx.x * HELIX_WG + threadIdx.x; // unit within (seq, head)
     const int h   = blockIdx.y;
     const int seq = blockIdx.z;
-    if (e >= PN) return;
+    if (u >= per_head) return;
+
+    // Unit -> (p, n..n+3).
+    const int NT   = p.np / 32;
+    const int slab = u / units_tile;
+    const int q    = u % units_tile;
+    const int lane = q & 63, r4 = (q >> 6) & 3, t = q >> 8;
+    const int pr = slab * HELIX_HD + (t / NT) * 32 + (lane & 31);
+    const int n  = (t % NT) * 32 + 8 * r4 + 4 * (lane >> 5);
+    // Tile padding carries zeros; d_state % 8 == 0, so n..n+3 are all valid or
+    // all padding.
+    const bool valid = pr < p.head_dim && n < p.d_state;
 
     const int src = p.has_ids ? b.ids[seq] : seq;
-    const long long s_out = seq * p.seq_s + h * p.s_s[0] + e;
-    float carry = p.first_group ? b.s0[src * p.seq_s + h * p.s_s[0] + e] : b.s1[s_out];
+    const long long soff = h * p.s_s[0] + (long long)pr * p.s_s[1] + n;
+    f32x4 carry = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (valid) {
+        const float* cs = p.first_group ? b.s0 + src * p.seq_s + soff : b.s1 + seq * p.seq_s + soff;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) carry[k] = cs[k];
+    }
 
-    float* __restrict__ base = b.s_seg + seq * p.sg_seq + h * PN + e;
+    f32x4* __restrict__ base =
+        reinterpret_cast<f32x4*>(b.s_seg + seq * p.sg_seq + (long long)h * per_head * 4) + u;
+    const long long seg_stride = p.sg_seg / 4;           // in units
     const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
 
     for (int s0 = 0; s0 < p.n_seg; s0 += BLK) {
         const int nb = min(BLK, p.n_seg - s0);
-        float d[BLK], a[BLK];
+        f32x4 d[BLK];
+        float a[BLK];
 #pragma unroll
         for (int k = 0; k < BLK; ++k) {
             if (k < nb) {
-                d[k] = base[(long long)(s0 + k) * p.sg_seg];
+                d[k] = base[(long long)(s0 + k) * seg_stride];
                 a[k] = expf(sd[(long long)(s0 + k) * p.n_head]);
             }
         }
 #pragma unroll
         for (int k = 0; k < BLK; ++k) {
             if (k < nb) {
-                base[(long long)(s0 + k) * p.sg_seg] = carry;
+                base[(long long)(s0 + k) * seg_stride] = carry;
                 carry = a[k] * carry + d[k];
             }
         }
     }
-    b.s1[s_out] = carry;
+    if (valid) {
+        float* cs = b.s1 + seq * p.seq_s + soff;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) cs[k] = carry[k];
+    }
 }

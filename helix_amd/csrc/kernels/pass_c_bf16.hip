@@ -34,7 +34,7 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
     __shared__ __attribute__((aligned(16))) float sE[HELIX_CS];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
 
     // 1-D grid of n_cg * (n_group * n_hblk) * n_seq workgroups, chunk fastest
     // in the logical order so a segment's chunks (which share S_seg) and a
@@ -59,19 +59,8 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
 
     // ---- stage C and B as bf16 ----------------------------------------------
     {
-        const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
-        const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
         float vc[16][NP / 64], vb[16][NP / 64];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int jr = min(wave + 4 * i, tlen - 1);
-#pragma unroll
-            for (int m = 0; m < NP / 64; ++m) {
-                const int nc = min(lane + 64 * m, N - 1);
-                vc[i][m] = C_g[(long long)jr * p.s_c[0] + nc];
-                vb[i][m] = B_g[(long long)jr * p.s_b[0] + nc];
-            }
-        }
+        load_cb_rows<NP>(vc, vb, p, b, seq, g, t0, tlen, lane, wave);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = wave + 4 * i;
@@ -142,17 +131,18 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
             sM[t * RSJ + lane] = to_bf16(m);
         }
         if (wave == 0) sE[lane] = expf((float)lcum);
-        // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16.
+        // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16: four
+        // consecutive n per unit, one 8-byte LDS write.
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int pr = wave + 4 * i;
+        for (int m = 0; m < NP / 16; ++m) {
+            const int pr = (m / (NP / 32)) * 32 + lo;
+            const int n  = (m % (NP / 32)) * 32 + 8 * wave + 4 * hi;
+            const f32x4 g = unit_to_f32(st.sg[m]), l = unit_to_f32(st.sl[m]);
+            const bool ok = pr < pw && n < N;
+            bf16x4 v;
 #pragma unroll
-            for (int m = 0; m < NP / 64; ++m) {
-                const int n = lane + 64 * m;
-                float v = es * st.sg[i][m];
-                if (cis > 0) v += (float)st.sl[i][m];
-                sBS[pr * RS + n] = to_bf16((pr < pw && n < N) ? v : 0.0f);
-            }
+            for (int k = 0; k < 4; ++k) v[k] = to_bf16(ok ? es * g[k] + l[k] : 0.0f);
+            *reinterpret_cast<bf16x4*>(&sBS[pr * RS + n]) = v;
         }
         __syncthreads();
         if (item + 1 < n_items) {
@@ -177,13 +167,7 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
             acc = mfma_bf16(av, bv, acc);
         }
 
-        float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
-        const int pp = pb * 32 + lo;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = tb * 32 + acc_row(r, hi);
-            if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
-        }
+        store_y_tile(acc, p, b, seq, h, t0, tlen, p0, pw, tb, pb, lo, hi);
         __syncthreads();
     }
 }

@@ -55,7 +55,7 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
     float* sE  = lds + OFF_E;            // exp(Lcum_t)
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
 
     // 1-D grid of n_cg * (n_group * n_hblk) * n_seq workgroups, chunk fastest
     // in the logical order so a segment's chunks (which share S_seg) and a
@@ -80,19 +80,8 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
 
     // ---- stage C and B of this (seq, chunk, group) ---------------------------
     {
-        const float* C_g = b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0];
-        const float* B_g = b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0];
         float vc[16][NP / 64], vb[16][NP / 64];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int jr = min(wave + 4 * i, tlen - 1);
-#pragma unroll
-            for (int m = 0; m < NP / 64; ++m) {
-                const int nc = min(lane + 64 * m, N - 1);
-                vc[i][m] = C_g[(long long)jr * p.s_c[0] + nc];
-                vb[i][m] = B_g[(long long)jr * p.s_b[0] + nc];
-            }
-        }
+        load_cb_rows<NP>(vc, vb, p, b, seq, g, t0, tlen, lane, wave);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = wave + 4 * i;
@@ -168,16 +157,17 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
         for (int kb = 0; kb < NKB; ++kb) {
             // S_init[p][k] = R_c + exp(ld_c) S_seg, zero past the slab and d_state.
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int pr = wave + 4 * i;
+            for (int pt = 0; pt < 2; ++pt) {
 #pragma unroll
-                for (int m = 0; m < KS / 64; ++m) {
-                    const int k = lane + 64 * m;
-                    const int n = kb * KS + k;
-                    const int mm = kb * (KS / 64) + m;
-                    float v = es * st.sg[i][mm];
-                    if (cis > 0) v += st.sl[i][mm];
-                    sS[pr * RSS + k] = (pr < pw && n < N) ? v : 0.0f;
+                for (int nt = kb * (KS / 32); nt < (kb + 1) * (KS / 32); ++nt) {
+                    const int m  = pt * (NP / 32) + nt;
+                    const int pr = pt * 32 + lo;
+                    const int n  = nt * 32 + 8 * wave + 4 * hi;
+                    const f32x4 g = unit_to_f32(st.sg[m]), l = unit_to_f32(st.sl[m]);
+                    const bool ok = pr < pw && n < N;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        sS[pr * RSS + (n - kb * KS) + k] = ok ? es * g[k] + l[k] : 0.0f;
                 }
             }
             __syncthreads();
@@ -209,13 +199,7 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
             acc = mfma_f32(av, bv, acc);
         }
 
-        float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
-        const int pp = pb * 32 + lo;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = tb * 32 + acc_row(r, hi);
-            if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
-        }
+        store_y_tile(acc, p, b, seq, h, t0, tlen, p0, pw, tb, pb, lo, hi);
         __syncthreads();
     }
 }

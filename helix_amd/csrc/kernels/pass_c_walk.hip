@@ -123,18 +123,20 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
     const int tb = wave >> 1, pb = wave & 1;
     const int pp = pb * 32 + lo;                  // this lane's P column in the slab
 
-    // R[n][p] for p in this wave's P block, from S_seg(s) ([P][N] layout).
+    // R[n][p] for p in this wave's P block: the slab tile of S_seg(s) is
+    // stored in exactly this register layout, so each group of four result
+    // registers is one 16-byte unit load.
     f32x16 R[NT];
     {
-        const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg +
-                          (long long)h * P * N + (long long)(p0 + min(pp, pw - 1)) * N;
+        const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + state_tile_off(p, h, slab);
+        const helix_rsrc rg = make_rsrc(sg, 64u * NP * sizeof(float));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = nt * 32 + acc_row(r, hi);
-                const float v = sg[min(n, N - 1)];
-                R[nt][r] = (n < N && pp < pw) ? v : 0.0f;
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const f32x4 v = buf_unit<float>(rg, lane, tile_unit(NT, pb, nt, r4, 0));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) R[nt][4 * r4 + k] = v[k];
             }
     }
 

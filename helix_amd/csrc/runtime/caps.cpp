@@ -150,8 +150,10 @@ int choose_seg_len(const helix_scan_desc& d, int cpg) {
     return (int)std::max<long>(1, std::min<long>(len, cpg));
 }
 
-void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int cpg, MultipassPlan* pl) {
-    const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
+void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int np, int cpg, MultipassPlan* pl) {
+    // State scratch is stored as padded slab tiles of 64 x np (helix_params.h).
+    const size_t n_pslab = (size_t)(d.head_dim + HELIX_HD - 1) / HELIX_HD;
+    const size_t state = (size_t)d.n_seq * d.n_head * n_pslab * 64 * (size_t)np;
     pl->chunks_per_group = cpg;
     pl->seg_len = choose_seg_len(d, cpg);
     pl->segs_per_group = (cpg + pl->seg_len - 1) / pl->seg_len;
@@ -179,14 +181,15 @@ MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& 
     pl.n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
 
     const size_t budget = scratch_budget_bytes();
-    const size_t state = (size_t)d.n_seq * d.n_head * d.head_dim * d.d_state;
+    const size_t state = (size_t)d.n_seq * d.n_head * ((d.head_dim + HELIX_HD - 1) / HELIX_HD) * 64 *
+                         (size_t)tr.np;
     // A walking Pass C keeps no per-chunk state; only segment aggregates
     // (about one state per seg_len chunks) count against the budget.
     const size_t per_chunk = tr.walk ? state : state * (bf16_state ? 2 : 4);
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(d, bf16_state, tr.walk, (int)cpg, &pl);
+        layout(d, bf16_state, tr.walk, tr.np, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }
@@ -235,6 +238,29 @@ bool build_params(const helix_scan_desc& d, HelixScanParams* o, std::string* why
     o->s_a = d.s_a;
     o->dt_min = d.dt_min;
     o->dt_max = d.dt_max;
+
+    // The kernels address one chunk of a tensor through a buffer resource
+    // based at the chunk's first element, with 32-bit byte offsets: every
+    // stride must be non-negative and a chunk's extent stay below 2 GiB.
+    const long long strides[] = {d.s_x[0], d.s_x[1], d.s_x[2], d.s_b[0], d.s_b[1], d.s_c[0],
+                                 d.s_c[1], d.s_dt[0], d.s_dt[1], d.s_y[0], d.s_y[1], d.s_y[2],
+                                 d.seq_x, d.seq_b, d.seq_c, d.seq_dt, d.seq_s, d.seq_y, d.s_a};
+    for (long long s : strides) {
+        if (s < 0) {
+            if (why) *why = "negative stride";
+            return false;
+        }
+    }
+    const long long kCs = HELIX_CS - 1, kHd = HELIX_HD - 1;
+    const long long spans[] = {kCs * d.s_x[0] + kHd * d.s_x[2] + 1, kCs * d.s_y[0] + kHd * d.s_y[2] + 1,
+                               kCs * d.s_b[0] + d.d_state, kCs * d.s_c[0] + d.d_state,
+                               kCs * d.s_dt[0] + 1};
+    for (long long e : spans) {
+        if (e * (long long)sizeof(float) >= (1LL << 31)) {
+            if (why) *why = "one chunk of a tensor spans 2 GiB or more";
+            return false;
+        }
+    }
 
     // Grid y and z are 16-bit on the hardware dispatch packet.
     const long kMaxYZ = 65535;

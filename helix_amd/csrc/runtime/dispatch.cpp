@@ -9,7 +9,7 @@
 //
 // Per super-chunk group, in stream order:
 //   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
-//   Pass B  grid (ceil(P*N/256), n_head, n_seq)         x 256 threads
+//   Pass B  grid (ceil(n_pslab*16*np/256), n_head, n_seq) x 256 threads
 //   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
 //           decoded XCD-aware in the kernel); the walking variant runs one
 //           workgroup per (segment, head, P slab, seq) instead
@@ -94,15 +94,16 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_ERR_PIPELINE;
     }
 
-    // Scratch strides (helix_params.h layout).
-    const long long HPN = (long long)d->n_head * d->head_dim * d->d_state;
+    // Scratch strides (helix_params.h layout: per head, n_pslab tiles of 64*np).
+    const long long HT = (long long)d->n_head * params.n_pslab * 64 * tr.np;
+    params.np      = tr.np;
     params.seg_len = plan.seg_len;
     params.hblk    = plan.hblk;
     params.n_hblk  = plan.n_hblk;
-    params.sl_cg   = HPN;
-    params.sl_seq  = (long long)plan.chunks_per_group * HPN;
-    params.sg_seg  = HPN;
-    params.sg_seq  = (long long)plan.segs_per_group * HPN;
+    params.sl_cg   = HT;
+    params.sl_seq  = (long long)plan.chunks_per_group * HT;
+    params.sg_seg  = HT;
+    params.sg_seq  = (long long)plan.segs_per_group * HT;
     params.ld_seq  = (long long)plan.chunks_per_group * d->n_head;
     params.sd_seq  = (long long)plan.segs_per_group * d->n_head;
 
@@ -141,7 +142,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     }
 
     helix_status st = HELIX_OK;
-    const unsigned PN = (unsigned)(d->head_dim * d->d_state);
+    const unsigned PN = (unsigned)(params.n_pslab * 16 * tr.np);   // Pass B threads (tile units) per head
     void* args[] = {&params, &bufs};
     for (int base = 0; base < plan.n_chunks && st == HELIX_OK; base += plan.chunks_per_group) {
         params.chunk_base  = base;

@@ -209,7 +209,9 @@ def _plan_invariants(host, name, backend):
     assert info.segs_per_group == -(-info.chunks_per_group // info.seg_len)
     hpg = H // G
     assert info.hblk * info.n_hblk >= hpg and (info.n_hblk - 1) * info.hblk < hpg
-    state = S * H * P * N
+    # State scratch is stored as padded 64 x np slab tiles (helix_params.h).
+    state = S * H * (-(-P // 64)) * 64 * info.np
+    assert info.np == (64 if N <= 64 else 128 if N <= 128 else 256)
     es = 2 if backend == HELIX_BACKEND_MPP else 4
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
     walk = backend == HELIX_BACKEND_MPP and os.environ.get("HELIX_BF16_PASSC") == "walk"
