@@ -80,6 +80,13 @@ HELIX_DEV ChunkDecay chunk_decay(const HelixScanParams& p, const float* __restri
 // exp of a (small, non-positive in practice) fp64 log-decay difference.
 HELIX_DEV float exp_diff(double a, double b) { return expf((float)(a - b)); }
 
+// The same through the hardware base-2 exponential (v_exp_f32, about 1 ulp):
+// the difference is scaled by log2(e) in fp64, so the only fp32 rounding
+// before the exponential is that of the final argument.
+HELIX_DEV float exp2_diff(double a, double b) {
+    return __builtin_amdgcn_exp2f((float)((a - b) * 1.4426950408889634074));
+}
+
 // MI355X hands the workgroups of a launch to its 8 XCDs round-robin (linear
 // id i runs on XCD i % 8), and each XCD has its own L2. This maps the linear
 // id to a logical id so that a contiguous run of logical ids shares one XCD:
@@ -94,6 +101,9 @@ HELIX_DEV unsigned xcd_logical_id(unsigned linear, unsigned total) {
 }
 
 // Wave-uniform broadcast of lane `src`'s value (src must be wave-uniform).
+// Call it where every lane executes (never inside a divergent branch or one
+// arm of a divergent ?:): under a partial exec mask the compiler may read the
+// lane from a register copy that was only written for the active lanes.
 HELIX_DEV float bcast(float v, int src) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
@@ -257,6 +267,50 @@ HELIX_DEV void buf_store_elem(helix_rsrc r, float v, int vidx, int sidx) {
     else
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, to_bf16(v)), r, vidx * 2,
                                               sidx * 2, 0);
+}
+
+// Branch- and mask-free selects. A compare feeding a select or a guarded
+// store is a 64-bit lane mask in SGPRs; when the compare is loop-invariant
+// the optimizer hoists it and keeps the masks of every row live across the
+// loop. These forms keep the condition in a VGPR instead.
+//   keep_if_le(v, a, b)  = a <= b ? v : 0.0f
+HELIX_DEV float keep_if_le(float v, int a, int b) {
+    const unsigned m = (unsigned)((b - a) >> 31);          // all ones iff a > b
+    return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, v) & ~m);
+}
+//   pick_hi(a, b, hi) = hi ? b : a, as a bitwise select (hi is 0 or 1)
+HELIX_DEV double pick_hi(double a, double b, int hi) {
+    const unsigned long long m = 0ull - (unsigned long long)hi;
+    const unsigned long long ua = __builtin_bit_cast(unsigned long long, a);
+    const unsigned long long ub = __builtin_bit_cast(unsigned long long, b);
+    return __builtin_bit_cast(double, (ua & ~m) | (ub & m));
+}
+//   keep_if_lt2(v, a, la, b, lb) = (a < la && b < lb) ? v : 0.0f
+HELIX_DEV float keep_if_lt2(float v, int a, int la, int b, int lb) {
+    const unsigned bad = (unsigned)(((la - 1 - a) | (lb - 1 - b)) >> 31);
+    return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, v) & ~bad);
+}
+//   keep_if_lt(v, a, la) = a < la ? v : 0.0f
+HELIX_DEV float keep_if_lt(float v, int a, int la) {
+    const unsigned bad = (unsigned)((la - 1 - a) >> 31);
+    return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, v) & ~bad);
+}
+// Byte offset for a raw buffer store, or one past any range (>= 2^31, which
+// the resource's range check drops) when the lane's element is not valid.
+// valid iff a < la && b < lb.
+HELIX_DEV int store_off_if_lt(int off, int a, int la, int b, int lb) {
+    const unsigned bad = (unsigned)(((la - 1 - a) | (lb - 1 - b)) >> 31);   // all ones iff invalid
+    return (int)((unsigned)off | (bad & 0x80000000u));
+}
+
+// A wave-uniform value the optimizer must treat as produced here. Applied to a
+// stride inside a loop, it keeps the products formed from it (one per row of
+// a staged tile) from being hoisted out of the loop as dozens of SGPRs that
+// stay live across it and spill; they are recomputed by the scalar unit
+// instead, which costs no vector issue slots.
+HELIX_DEV int sgpr_fresh(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
 }
 
 // This thread's wave index, as a wave-uniform (SGPR) value: everything derived

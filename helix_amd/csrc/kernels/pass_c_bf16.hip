@@ -112,23 +112,45 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
         const int p0 = slab * HELIX_HD;
         const int pw = min(HELIX_HD, P - p0);
 
-        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
         const double lcum = wave_incl_sum((double)st.A * (double)dtv);
         const float es = expf(st.ld);
 
-        // dtX^T[p][j] (bf16); dtv_j = 0 past tlen.
+        // dtX^T[p][j] (bf16); dtv_j = 0 past tlen. Wave w holds tokens
+        // 16w .. 16w+15 of its lane's channel: two 16-byte LDS writes.
+        {
+            bf16x8 v0, v1;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int j = wave + 4 * i;
-            sXt[lane * RSJ + j] = to_bf16(lane < pw ? bcast(dtv, j) * st.x[i] : 0.0f);
+            for (int i = 0; i < 8; ++i) {
+                v0[i] = to_bf16(keep_if_lt(bcast(dtv, 16 * wave + i) * st.x[i], lane, pw));
+                v1[i] = to_bf16(keep_if_lt(bcast(dtv, 16 * wave + 8 + i) * st.x[8 + i], lane, pw));
+            }
+            *reinterpret_cast<bf16x8*>(&sXt[lane * RSJ + 16 * wave]) = v0;
+            *reinterpret_cast<bf16x8*>(&sXt[lane * RSJ + 16 * wave + 8]) = v1;
         }
-        // M[t][j] (bf16), zero above the diagonal.
+        // M[t][j] = CB[t][j] exp(Lcum_t - Lcum_j) (bf16), zero above the
+        // diagonal. Only the three causal 32 x 32 blocks are built, in 48 row
+        // steps: steps 0..15 pair row s (lanes 0-31) with row s + 16 (lanes
+        // 32-63) of block (0,0), columns j = lo; steps 16..47 are the full rows
+        // t = s + 16 of blocks (1,0) and (1,1), j = lane. Wave w takes steps
+        // w + 4k, so k < 4 are the paired steps for every wave.
+        {
+            const double l_lo = __shfl(lcum, lo, 64);    // Lcum of token lane % 32
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int s = wave + 4 * k;
+                const int t = s + 16 * hi;
+                const double lt = pick_hi(bcast(lcum, s), bcast(lcum, s + 16), hi);
+                const float m = keep_if_le(sCB[t * RSCB + lo] * exp2_diff(lt, l_lo), lo, t);
+                sM[t * RSJ + lo] = to_bf16(m);
+            }
 #pragma unroll 4
-        for (int i = 0; i < 16; ++i) {
-            const int t = wave + 4 * i;
-            const double lt = bcast(lcum, t);
-            const float m = (lane <= t) ? sCB[t * RSCB + lane] * exp_diff(lt, lcum) : 0.0f;
-            sM[t * RSJ + lane] = to_bf16(m);
+            for (int k = 4; k < 12; ++k) {
+                const int t = wave + 4 * k + 16;
+                const double lt = bcast(lcum, t);
+                const float m = keep_if_le(sCB[t * RSCB + lane] * exp2_diff(lt, lcum), lane, t);
+                sM[t * RSJ + lane] = to_bf16(m);
+            }
         }
         if (wave == 0) sE[lane] = expf((float)lcum);
         // S^T[p][n] = R_c + exp(ld_c) S_seg, in fp32 then rounded to bf16: four
@@ -138,10 +160,9 @@ __device__ __forceinline__ void chunk_out_bf16_impl(const HelixScanParams& p, co
             const int pr = (m / (NP / 32)) * 32 + lo;
             const int n  = (m % (NP / 32)) * 32 + 8 * wave + 4 * hi;
             const f32x4 g = unit_to_f32(st.sg[m]), l = unit_to_f32(st.sl[m]);
-            const bool ok = pr < pw && n < N;
             bf16x4 v;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = to_bf16(ok ? es * g[k] + l[k] : 0.0f);
+            for (int k = 0; k < 4; ++k) v[k] = to_bf16(keep_if_lt2(es * g[k] + l[k], pr, pw, n, N));
             *reinterpret_cast<bf16x4*>(&sBS[pr * RS + n]) = v;
         }
         __syncthreads();

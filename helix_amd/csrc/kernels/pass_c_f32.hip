@@ -133,22 +133,22 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
         const int p0 = slab * HELIX_HD;
         const int pw = min(HELIX_HD, P - p0);
 
-        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
         const double lcum = wave_incl_sum((double)st.A * (double)dtv);
         const float es = expf(st.ld);
 
         // dtX[j][p] (dtv_j = 0 past tlen)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int j = wave + 4 * i;
-            sX[j * RSX + lane] = lane < pw ? bcast(dtv, j) * st.x[i] : 0.0f;
+            const int j = 16 * wave + i;
+            sX[j * RSX + lane] = keep_if_lt(bcast(dtv, j) * st.x[i], lane, pw);
         }
         // M[t][j] for this head; lane = j, so Lcum_j is this lane's own.
 #pragma unroll 4
         for (int i = 0; i < 16; ++i) {
             const int t = wave + 4 * i;
             const double lt = bcast(lcum, t);
-            sM[t * RSM + lane] = (lane <= t) ? sCB[t * RSM + lane] * exp_diff(lt, lcum) : 0.0f;
+            sM[t * RSM + lane] = keep_if_le(sCB[t * RSM + lane] * exp_diff(lt, lcum), lane, t);
         }
         if (wave == 0) sE[lane] = expf((float)lcum);
 
@@ -164,10 +164,9 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
                     const int pr = pt * 32 + lo;
                     const int n  = nt * 32 + 8 * wave + 4 * hi;
                     const f32x4 g = unit_to_f32(st.sg[m]), l = unit_to_f32(st.sl[m]);
-                    const bool ok = pr < pw && n < N;
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        sS[pr * RSS + (n - kb * KS) + k] = ok ? es * g[k] + l[k] : 0.0f;
+                        sS[pr * RSS + (n - kb * KS) + k] = keep_if_lt2(es * g[k] + l[k], pr, pw, n, N);
                 }
             }
             __syncthreads();

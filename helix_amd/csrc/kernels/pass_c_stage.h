@@ -35,7 +35,7 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
     st.ld = b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h];
     // dt and x of this head and chunk through buffer resources based at the
     // chunk's first token (the host keeps a chunk's extent below 2 GiB).
-    const int sdt = (int)p.s_dt[0], sx0 = (int)p.s_x[0], sx2 = (int)p.s_x[2];
+    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
     const helix_rsrc rdt = make_rsrc(dt_s + h * p.s_dt[1] + (long long)t0 * p.s_dt[0],
                                      ((tlen - 1) * sdt + 1) * 4u);
     const helix_rsrc rx = make_rsrc(x_s + h * p.s_x[1] + (long long)t0 * p.s_x[0] + (long long)p0 * p.s_x[2],
@@ -44,7 +44,7 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int jr = min(wave + 4 * i, tlen - 1);
+        const int jr = min(16 * wave + i, tlen - 1);    // wave w: tokens 16w .. 16w+15
         st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
     }
     // The slab tile is one contiguous, wave-uniform region: buffer loads with
@@ -56,7 +56,7 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
     const helix_rsrc rl = make_rsrc(sl_s + toff, cis > 0 ? 64u * NP * sizeof(SL) : 0u);
 #pragma unroll
     for (int m = 0; m < NP / 16; ++m) {
-        const int u = (m * 4 + wave) * 64;           // tile_unit(NT, m / NT, m % NT, wave, 0)
+        const int u = sgpr_fresh((m * 4 + wave) * 64);   // tile_unit(NT, m / NT, m % NT, wave, 0)
         st.sg[m] = buf_unit_raw<float>(rg, lane, u);
         st.sl[m] = buf_unit_raw<SL>(rl, lane, u);
     }
@@ -92,19 +92,21 @@ __device__ __forceinline__ void load_cb_rows(float (&vc)[16][NP / 64], float (&v
 __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanParams& p,
                                              const HelixScanBuffers& b, int seq, int h, int t0,
                                              int tlen, int p0, int pw, int tb, int pb, int lo, int hi) {
-    const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
+    const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
     const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
                                         (long long)p0 * p.s_y[2],
                                     ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u);
     const int pp = pb * 32 + lo;
-    const int voff = 4 * hi * sy0 + pp * sy2;
+    const int voff = (4 * hi * sy0 + pp * sy2) * 4;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int t = tb * 32 + acc_row(r, hi);
         // The element goes through a float value: a bit cast applied to a
         // vector element in place reads element 0 with this compiler.
         const float v = acc[r];
-        if (t < tlen && pp < pw) buf_store_elem<float>(ry, v, voff, (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ry,
+                                              store_off_if_lt(voff, t, tlen, pp, pw),
+                                              (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * 4, 0);
     }
 }
 
