@@ -11,7 +11,8 @@
 //   v_mfma_f32_32x32x16_bf16 A[i][k]: lane holds A[lo][8*hi + e], e = 0..7
 //                            B[k][j]: lane holds B[8*hi + e][lo]
 //                            D as above
-// tests/test_gpu_mfma_layout.py checks these on the device.
+// Every kernel output depends on these layouts, so the device parity suite
+// (tests/test_gpu_parity.py) checks them end to end.
 #ifndef HELIX_COMMON_H
 #define HELIX_COMMON_H
 
@@ -38,17 +39,29 @@ HELIX_DEV float helix_dt(const HelixScanParams& p, float raw) {
     return fminf(fmaxf(helix_softplus(raw), p.dt_min), p.dt_max);
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (Kogge-Stone, 6 steps),
-// in fp64: the intra-chunk decays are exp(Lcum_t - Lcum_j), and with
-// |A*dt| summing to a few hundred per chunk an fp32 prefix would lose the
-// low digits that the difference of two nearby prefixes needs.
+// Lane-shifted copy of a double by a DPP move on each 32-bit half; lanes
+// without a source (and rows outside ROW_MASK) receive 0.
+template <int CTRL, int ROW_MASK>
+HELIX_DEV double dpp_f64(double v) {
+    const long long u = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)u, CTRL, ROW_MASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(u >> 32), CTRL, ROW_MASK, 0xf, true);
+    return __builtin_bit_cast(double, ((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave, in fp64: the intra-chunk
+// decays are exp(Lcum_t - Lcum_j), and with |A*dt| summing to a few hundred
+// per chunk an fp32 prefix would lose the low digits that the difference of
+// two nearby prefixes needs. Six DPP steps, no LDS: row_shr 1, 2, 4, 8 scan
+// each row of 16 lanes; row_bcast:15 adds row 0's total to row 1 and row 2's
+// to row 3; row_bcast:31 adds the total of rows 0-1 to rows 2 and 3.
 HELIX_DEV double wave_incl_sum(double v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const double n = __shfl_up(v, d, 64);
-        if (lane >= d) v += n;
-    }
+    v += dpp_f64<0x111, 0xf>(v);   // row_shr:1
+    v += dpp_f64<0x112, 0xf>(v);   // row_shr:2
+    v += dpp_f64<0x114, 0xf>(v);   // row_shr:4
+    v += dpp_f64<0x118, 0xf>(v);   // row_shr:8
+    v += dpp_f64<0x142, 0xa>(v);   // row_bcast:15 -> rows 1, 3
+    v += dpp_f64<0x143, 0xc>(v);   // row_bcast:31 -> rows 2, 3
     return v;
 }
 

@@ -1,0 +1,259 @@
+// pass_a_x6.hip -- Pass A on bf16 MFMA with three-way operand splitting.
+//
+// Same computation and outputs as pass_a.hip (reference helix_chunk_state_f32,
+// src/kernels/helix_scan_multipass.metal:51-149, walked over a segment):
+//     R <- exp(L_end_c) R + B_c^T . (decay . dt . x)_c
+// but the GEMM runs on v_mfma_f32_32x32x16_bf16, which MI355X issues at 16x
+// the fp32 matrix rate. Each fp32 operand v is split into three bf16 parts
+//     v = v0 + v1 + v2,  v0 = bf16(v), v1 = bf16(v - v0), v2 = bf16(v - v0 - v1)
+// (each residual is exact in fp32, and the three 8-bit significands cover
+// fp32's 24), and the product is accumulated in fp32 from the six terms whose
+// size is at least 2^-16 of the leading one:
+//     a.b ~ a0 b0 + (a0 b1 + a1 b0) + (a0 b2 + a1 b1 + a2 b0)
+// The dropped terms (a1 b2, a2 b1, a2 b2) are below 2^-24 relative, the size
+// of an fp32 rounding, so the state keeps fp32 accuracy (bf16x6 in the
+// literature: Henry, Tang, Heinecke, "Leveraging the bfloat16 Artificial
+// Intelligence Datatype For Higher-Precision Computations", ARITH 2019).
+// The terms are issued smallest first so the large ones are added last.
+//
+// Layout: the workgroup computes R[n][p] (N x 64), M = n, N = p, K = token.
+// The split operands are staged in LDS k-contiguous: three planes of
+// B^T[n][j] and three of dtXs^T[p][j], rows of 64 tokens (128 bytes, eight
+// 16-byte chunks). Chunk c of row r sits at chunk position c ^ ((r >> 1) & 7),
+// so the 16-byte reads of an MFMA operand (16 consecutive rows, one chunk
+// each) and the 16-byte staging writes both cover all 64 banks once per
+// 16 lanes. Wave w owns P tile (w & 1) and N tiles (w >> 1) + 2i, and stages
+// tokens 16w .. 16w+15 of every row, i.e. chunks 2w and 2w+1.
+#include "helix_common.h"
+
+// Three-way bf16 split of v (round to nearest even at each step).
+HELIX_DEV void split3(float v, __bf16& h0, __bf16& h1, __bf16& h2) {
+    h0 = to_bf16(v);
+    const float r1 = v - (float)h0;
+    h1 = to_bf16(r1);
+    const float r2 = r1 - (float)h1;
+    h2 = to_bf16(r2);
+}
+
+// Element offset of 16-byte chunk c of row r in plane k (rows of 64 bf16).
+template <int ROWS>
+HELIX_DEV int x6_chunk(int k, int r, int c) {
+    return ((k * ROWS + r) << 6) + ((c ^ ((r >> 1) & 7)) << 3);
+}
+
+template <int NP>
+struct StageX6 {
+    float dtraw;
+    float x[16];
+    float b[16][NP / 64];
+};
+
+// Chunk c's inputs for this thread: rows (tokens) 16 wave + i, clamped to the
+// last valid token; x at channel p = lane (clamped to the slab), B at state
+// index n = lane + 64 m (clamped to d_state). Masks are applied when staging.
+template <int NP>
+__device__ __forceinline__ void load_stage_x6(StageX6<NP>& st, const HelixScanParams& p,
+                                              const float* __restrict__ dt_h,
+                                              const float* __restrict__ x_h,
+                                              const float* __restrict__ B_g, int c, int lane,
+                                              int wave, int pw, int N) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const int sb0 = sgpr_fresh((int)p.s_b[0]);
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    const helix_rsrc rb  = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    const int xc = min(lane, pw - 1) * sx2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int jr = min(16 * wave + i, tlen - 1);
+        st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
+#pragma unroll
+        for (int m = 0; m < NP / 64; ++m) st.b[i][m] = buf_elem<float>(rb, min(lane + 64 * m, N - 1), jr * sb0);
+    }
+}
+
+// Stage 16 consecutive tokens (chunks c0, c0 + 1) of row r of a three-plane
+// operand from fp32 values v[0..15].
+template <int ROWS>
+HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[16]) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        bf16x8 q0, q1, q2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            __bf16 h0, h1, h2;
+            split3(v[8 * half + e], h0, h1, h2);
+            q0[e] = h0;
+            q1[e] = h1;
+            q2[e] = h2;
+        }
+        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(0, r, c0 + half)]) = q0;
+        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(1, r, c0 + half)]) = q1;
+        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(2, r, c0 + half)]) = q2;
+    }
+}
+
+// MODE as in pass_a.hip: 0 store R_c fp32, 1 store R_c bf16, 2 aggregates only.
+template <int NP, int MODE>
+__device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr bool SBF = MODE == 1;
+    constexpr int NTW = NP / 64;      // N tiles per wave
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];
+    __shared__ __attribute__((aligned(16))) __bf16 sXt[3 * HELIX_HD * HELIX_CS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
+
+    const int seg  = blockIdx.x;
+    const int h    = blockIdx.y;
+    const int slab = blockIdx.z % p.n_pslab;
+    const int seq  = blockIdx.z / p.n_pslab;
+    const int p0   = slab * HELIX_HD;
+    const int pw   = min(HELIX_HD, p.head_dim - p0);
+    const int N    = p.d_state;
+    const int g    = h / p.heads_per_group;
+
+    const int c_begin = seg * p.seg_len;
+    const int c_end   = min(c_begin + p.seg_len, p.n_cg);
+    if (c_begin >= c_end) return;
+
+    const float A_h = b.A[(long long)h * p.s_a];
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
+
+    const long long tile_off = state_tile_off(p, h, slab);
+    const unsigned tile_elems = 64u * NP;
+
+    const int pt  = wave & 1;
+    const int nt0 = wave >> 1;
+
+    f32x16 acc[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) acc[i] = zero16();
+    float lam = 0.0f;  // log-decay accumulated over this segment before chunk c
+
+    // Two register stages in turn: the loads of chunk c+2 are issued while
+    // chunks c and c+1 are processed (a copy between stages would wait on them).
+    auto step = [&](StageX6<NP>& st, int c) {
+        const int t0   = (p.chunk_base + c) * HELIX_CS;
+        const int tlen = min(HELIX_CS, p.n_tok - t0);
+
+        // Decay preamble (lane = token; dtv = 0 past tlen).
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lend = __shfl(lcum, 63, 64);
+        const float cf = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
+
+        // dtXs^T[p][j] = exp(L_end - Lcum_j) dt_j x[j][p], row p = lane.
+        {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = keep_if_lt(bcast(cf, 16 * wave + i) * st.x[i], lane, pw);
+            stage_split_row<HELIX_HD>(sXt, lane, 2 * wave, v);
+        }
+        // B^T[n][j], rows n = lane + 64 m; zero past tlen and d_state.
+#pragma unroll
+        for (int m = 0; m < NP / 64; ++m) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = keep_if_lt2(st.b[i][m], 16 * wave + i, tlen, lane + 64 * m, N);
+            stage_split_row<NP>(sBt, lane + 64 * m, 2 * wave, v);
+        }
+
+        if (MODE != 2 && c > c_begin) {
+            const long long off = seq * p.sl_seq + (long long)c * p.sl_cg + tile_off;
+            const void* dst = SBF ? (const void*)(static_cast<const __bf16*>(b.s_local) + off)
+                                  : (const void*)(static_cast<const float*>(b.s_local) + off);
+            const helix_rsrc rd = make_rsrc(dst, tile_elems * (SBF ? 2u : 4u));
+#pragma unroll
+            for (int i = 0; i < NTW; ++i) {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int u = tile_unit(NP / 32, pt, nt0 + 2 * i, r4, 0);
+                    const float v0 = acc[i][4 * r4], v1 = acc[i][4 * r4 + 1];
+                    const float v2 = acc[i][4 * r4 + 2], v3 = acc[i][4 * r4 + 3];
+                    if (SBF)
+                        buf_store_unit<__bf16>(rd, v0, v1, v2, v3, lane, u);
+                    else
+                        buf_store_unit<float>(rd, v0, v1, v2, v3, lane, u);
+                }
+            }
+        }
+        if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
+        __syncthreads();
+
+        // This register stage is free again: chunk c+2's inputs travel while
+        // this chunk's and the next one's GEMMs run.
+        if (c + 2 < c_end) load_stage_x6<NP>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
+
+        const float a_c = expf((float)lend);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) acc[i] *= a_c;
+
+        // R[n][p] += sum_j B^T[n][j] dtXs^T[p][j] over four K steps of 16 tokens.
+#pragma unroll
+        for (int s = 0; s < HELIX_CS / 16; ++s) {
+            const int cx = 2 * s + hi;
+            const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(0, pt * 32 + lo, cx)]);
+            const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(1, pt * 32 + lo, cx)]);
+            const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(2, pt * 32 + lo, cx)]);
+#pragma unroll
+            for (int i = 0; i < NTW; ++i) {
+                const int rn = (nt0 + 2 * i) * 32 + lo;
+                const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(0, rn, cx)]);
+                const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(1, rn, cx)]);
+                const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(2, rn, cx)]);
+                acc[i] = mfma_bf16(b2, x0, acc[i]);
+                acc[i] = mfma_bf16(b1, x1, acc[i]);
+                acc[i] = mfma_bf16(b0, x2, acc[i]);
+                acc[i] = mfma_bf16(b1, x0, acc[i]);
+                acc[i] = mfma_bf16(b0, x1, acc[i]);
+                acc[i] = mfma_bf16(b0, x0, acc[i]);
+            }
+        }
+        lam += (float)lend;
+        __syncthreads();
+    };
+    StageX6<NP> sa, sb;
+    load_stage_x6<NP>(sa, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
+    if (c_begin + 1 < c_end) load_stage_x6<NP>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
+    for (int c = c_begin; c < c_end; c += 2) {
+        step(sa, c);
+        if (c + 1 < c_end) step(sb, c + 1);
+    }
+
+    const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
+    const helix_rsrc rs = make_rsrc(sg, tile_elems * 4u);
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int u = tile_unit(NP / 32, pt, nt0 + 2 * i, r4, 0);
+            buf_store_unit<float>(rs, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2],
+                                  acc[i][4 * r4 + 3], lane, u);
+        }
+    }
+    if (slab == 0 && tid == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
+}
+
+#define HELIX_PASS_A_X6(NP)                                                                     \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6f32_n##NP(        \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 0>(p, b);                                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6sbf_n##NP(        \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 1>(p, b);                                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_n##NP(        \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2>(p, b);                                                       \
+    }
+
+HELIX_PASS_A_X6(64)
+HELIX_PASS_A_X6(128)
+HELIX_PASS_A_X6(256)

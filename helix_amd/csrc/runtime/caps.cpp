@@ -60,7 +60,50 @@ constexpr HelixMatmulTraits kBf16WalkTraits[] = {
      "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256, true},
 };
 
+// Pass A on bf16 MFMA with three-way operand splitting (pass_a_x6.hip):
+// fp32-equivalent state at 16x the fp32 matrix issue rate. The default on
+// every path; HELIX_PASSA=f32 selects the fp32-MFMA kernels above.
+constexpr const char* kX6StateF32[] = {"helix_chunk_state_x6f32_n64", "helix_chunk_state_x6f32_n128",
+                                       "helix_chunk_state_x6f32_n256"};
+constexpr const char* kX6StateSbf[] = {"helix_chunk_state_x6sbf_n64", "helix_chunk_state_x6sbf_n128",
+                                       "helix_chunk_state_x6sbf_n256"};
+constexpr const char* kX6StateAgg[] = {"helix_chunk_state_x6agg_n64", "helix_chunk_state_x6agg_n128",
+                                       "helix_chunk_state_x6agg_n256"};
+
+// The selectable trait sets: [family: fp32, bf16, bf16 walk][np index], with
+// Pass A on fp32 MFMA or bf16x6. Built once; names live as long as the process.
+struct TraitSets {
+    HelixMatmulTraits t[2][3][3];
+    std::string names[2][3][3];
+    TraitSets() {
+        const HelixMatmulTraits* base[3] = {kF32Traits, kBf16Traits, kBf16WalkTraits};
+        const char* const* x6[3] = {kX6StateF32, kX6StateSbf, kX6StateAgg};
+        for (int fam = 0; fam < 3; ++fam)
+            for (int k = 0; k < 3; ++k) {
+                t[0][fam][k] = base[fam][k];
+                HelixMatmulTraits& v = t[1][fam][k];
+                v = base[fam][k];
+                std::string nm = v.name;
+                const size_t at = nm.find(" (d_state");
+                names[1][fam][k] = nm.substr(0, at) + ", pass A bf16x6" + nm.substr(at);
+                v.name = names[1][fam][k].c_str();
+                v.k_chunk_state = x6[fam][k];
+                v.mfma_a = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
+            }
+    }
+};
+
+const HelixMatmulTraits& pick_traits(int fam, int k) {
+    static const TraitSets sets;
+    const char* v = std::getenv("HELIX_PASSA");
+    const int x6 = (v && v[0] == 'f') ? 0 : 1;
+    return sets.t[x6][fam][k];
+}
+
 const char* const kKernelNames[] = {
+    "helix_chunk_state_x6f32_n64", "helix_chunk_state_x6f32_n128", "helix_chunk_state_x6f32_n256",
+    "helix_chunk_state_x6sbf_n64", "helix_chunk_state_x6sbf_n128", "helix_chunk_state_x6sbf_n256",
+    "helix_chunk_state_x6agg_n64", "helix_chunk_state_x6agg_n128", "helix_chunk_state_x6agg_n256",
     "helix_chunk_state_f32_n64",  "helix_chunk_state_f32_n128", "helix_chunk_state_f32_n256",
     "helix_chunk_state_sbf_n64",  "helix_chunk_state_sbf_n128", "helix_chunk_state_sbf_n256",
     "helix_state_scan_f32",
@@ -114,17 +157,17 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
     const int k = np_index(d.d_state);
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
-        if (f[0] == 's') return kF32Traits[k];
+        if (f[0] == 's') return pick_traits(0, k);
     const bool want_bf16 = d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP;
     if (want_bf16 && d.multipass) {
         // HELIX_BF16_PASSC=walk selects the chunk-walking Pass C (state in
         // registers, no per-chunk scratch); the chunk-parallel one is the
         // default while it is the faster of the two.
         if (const char* v = std::getenv("HELIX_BF16_PASSC"))
-            if (v[0] == 'w') return kBf16WalkTraits[k];
-        return kBf16Traits[k];
+            if (v[0] == 'w') return pick_traits(2, k);
+        return pick_traits(1, k);
     }
-    return kF32Traits[k];
+    return pick_traits(0, k);
 }
 
 size_t scratch_budget_bytes() {

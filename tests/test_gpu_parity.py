@@ -6,8 +6,10 @@ Mirrors the reference's tests/test_metal_parity.mm:
     super-chunk groups (HELIX_SCRATCH_MB=1, :106-110);
   * per-element allclose with the tolerance of the backend that actually ran
     (:163-166); s1 always held to the fp32 bound (:214-218).
-Both MI355X paths are exercised explicitly (SGMMA -> fp32 MFMA, MPP -> bf16
-Pass C) because AUTO resolves to bf16 for every multipass shape here.
+Both MI355X paths are exercised explicitly (SGMMA -> fp32 MFMA Pass C, MPP ->
+bf16 Pass C) because AUTO resolves to bf16 for every multipass shape here, and
+each with Pass A on its default bf16x6 split products and on fp32 MFMA
+(HELIX_PASSA=f32).
 The single-pass modes are absent: this build declines multipass=false.
 
 Then the BASELINE.json configurations at full size, gated on
@@ -54,18 +56,23 @@ SHAPES = [
 ]
 
 MODES = [
-    # (label, backend, scratch_mb, memory, bf16 Pass C variant)
-    ("fp32", HELIX_BACKEND_SGMMA, None, "short", None),
-    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", None),
-    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", None),
-    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", None),
-    ("bf16", HELIX_BACKEND_MPP, None, "short", None),
-    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", None),
-    ("bf16/long", HELIX_BACKEND_MPP, None, "long", None),
-    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long", None),
-    ("bf16walk", HELIX_BACKEND_MPP, None, "short", "walk"),
-    ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", "walk"),
-    ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", "walk"),
+    # (label, backend, scratch_mb, memory, extra environment)
+    ("fp32", HELIX_BACKEND_SGMMA, None, "short", {}),
+    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", {}),
+    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}),
+    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {}),
+    ("bf16", HELIX_BACKEND_MPP, None, "short", {}),
+    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}),
+    ("bf16/long", HELIX_BACKEND_MPP, None, "long", {}),
+    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long", {}),
+    ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}),
+    ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}),
+    ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}),
+    # Pass A on fp32 MFMA instead of bf16x6 split products.
+    ("fp32/mmaA/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_PASSA": "f32"}),
+    ("bf16/mmaA/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA": "f32"}),
+    ("bf16walk/mmaA/long", HELIX_BACKEND_MPP, None, "long",
+     {"HELIX_PASSA": "f32", "HELIX_BF16_PASSC": "walk"}),
 ]
 
 
@@ -80,12 +87,12 @@ def _reference(shape, memory):
 @pytest.mark.parametrize("mode", MODES, ids=[m[0] for m in MODES])
 @pytest.mark.parametrize("shape", SHAPES, ids=[s[-1] for s in SHAPES])
 def test_shape_matrix(gpu, shape, mode):
-    label, backend, scratch_mb, memory, passc = mode
+    label, backend, scratch_mb, memory, extra = mode
     p, y_ref, s_ref = _reference(shape, memory)
     d = p.d.copy()
     d.multipass = True
     d.backend = backend
-    with env(HELIX_SCRATCH_MB=scratch_mb, HELIX_BF16_PASSC=passc):
+    with env(HELIX_SCRATCH_MB=scratch_mb, **extra):
         assert gpu.supported(d), gpu.backend_desc(d)
         is_bf16 = gpu.select_backend(d) == HELIX_BACKEND_MPP
         _, y, s1 = run(gpu, p, desc=d)
@@ -118,6 +125,7 @@ def _baseline(name, memory):
 
 CASES = [(n, path, mem) for n, c in CONFIGS.items() for path in c.paths for mem in ("dist", "long")]
 CASES += [(n, "bf16walk", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
+CASES += [(n, path + "/mmaA", "long") for n, c in CONFIGS.items() for path in c.paths]
 
 
 @pytest.mark.parametrize("name,path,memory", CASES, ids=[f"{n}-{p}-{m}" for n, p, m in CASES])
@@ -127,12 +135,13 @@ def test_baseline_config(gpu, name, path, memory):
     d = p.d.copy()
     d.multipass = True
     d.backend = HELIX_BACKEND_MPP if path.startswith("bf16") else HELIX_BACKEND_SGMMA
-    with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None):
+    with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None,
+             HELIX_PASSA="f32" if path.endswith("/mmaA") else None):
         assert gpu.supported(d)
         assert (gpu.select_backend(d) == HELIX_BACKEND_MPP) == path.startswith("bf16")
         print(f"[{name} {path} {memory}] {gpu.backend_desc(d)}", flush=True)
         _, y, s1 = run(gpu, p, desc=d)
-    path = "bf16" if path.startswith("bf16") else path
+    path = "bf16" if path.startswith("bf16") else "fp32"
     hs = list(c.check_heads)
     ey = po.max_rel_err(y[:, :, hs], y_ref[:, :, hs])
     es = po.max_rel_err(s1[:, hs], s_ref[:, hs])
