@@ -191,6 +191,12 @@ HELIX_DEV T buf_elem(helix_rsrc r, int vidx, int sidx) {
     else
         return buf_bf16(r, vidx * 2, sidx * 2);
 }
+// Bit casts through a by-value parameter. __builtin_bit_cast applied in place
+// to an element of an ext_vector_type lvalue (v[k]) reads element 0 with this
+// compiler; passing the element as an argument makes it a plain value first.
+HELIX_DEV float as_f32(unsigned v) { return __builtin_bit_cast(float, v); }
+HELIX_DEV unsigned as_u32(float v) { return __builtin_bit_cast(unsigned, v); }
+
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -41,6 +41,10 @@
  * of the caller's [P][N] layout; and a lane's units are the B operand of
  * Pass C's C . S GEMM as they stand (the K order of an MFMA is free as long as
  * both operands use the same one).
+ * Padding (p past head_dim in the last slab, n past d_state) holds finite
+ * values no result depends on: Pass C zeroes it when staging S_init (and C is
+ * zero past d_state), y is stored only for p < head_dim, and Pass B writes s1
+ * only for valid (p, n).
  */
 #ifndef HELIX_PARAMS_H
 #define HELIX_PARAMS_H

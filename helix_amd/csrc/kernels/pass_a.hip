@@ -23,9 +23,9 @@
 // Store this wave's accumulator tiles (R[n][p] tiles (nt0 + 2i, pt)) into a
 // slab tile (helix_params.h layout): result registers 4 r4 .. 4 r4 + 3 are
 // one unit, so each lane writes 16 (fp32) or 8 (bf16) bytes per four registers
-// and a wave 1 KiB / 512 B contiguous. No guards: the padding of a partial
-// slab or of d_state < np holds zeros, because the matching dtXs columns and
-// B columns were staged as zeros.
+// and a wave 1 KiB / 512 B contiguous. No guards: the whole padded tile is
+// written (here the padding of a partial slab or of d_state < np holds zeros,
+// because the matching dtXs columns and B columns were staged as zeros).
 template <int NP, bool SBF>
 __device__ __forceinline__ void store_state_tiles(const f32x16* acc, helix_rsrc dst, int pt, int nt0,
                                                   int lane) {

@@ -23,34 +23,56 @@
 // so the 16-byte reads of an MFMA operand (16 consecutive rows, one chunk
 // each) and the 16-byte staging writes both cover all 64 banks once per
 // 16 lanes. Wave w owns P tile (w & 1) and N tiles (w >> 1) + 2i, and stages
-// tokens 16w .. 16w+15 of every row, i.e. chunks 2w and 2w+1.
+// tokens 16w .. 16w+15 (chunks 2w and 2w+1) of every row: dtXs^T row p = lane
+// both chunks; B^T rows NB*lo .. NB*lo + NB-1 (NB = NP/32) chunk 2w + hi.
 #include "helix_common.h"
 
-// Three-way bf16 split of v (round to nearest even at each step).
-HELIX_DEV void split3(float v, __bf16& h0, __bf16& h1, __bf16& h2) {
-    h0 = to_bf16(v);
-    const float r1 = v - (float)h0;
-    h1 = to_bf16(r1);
-    const float r2 = r1 - (float)h1;
-    h2 = to_bf16(r2);
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even bf16 pair (element 0 in the low half), one
+// v_cvt_pk_bf16_f32, and its exact fp32 values.
+HELIX_DEV unsigned pk_bf16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+}
+HELIX_DEV float pk_lo(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+HELIX_DEV float pk_hi(unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// Three-way bf16 split of the pair (a, b), each part packed as a pair:
+// 11 VALU operations for two values.
+HELIX_DEV void split3_pair(float a, float b, unsigned& w0, unsigned& w1, unsigned& w2) {
+    w0 = pk_bf16(a, b);
+    const float ra = a - pk_lo(w0), rb = b - pk_hi(w0);
+    w1 = pk_bf16(ra, rb);
+    w2 = pk_bf16(ra - pk_lo(w1), rb - pk_hi(w1));
 }
 
 // Element offset of 16-byte chunk c of row r in plane k (rows of 64 bf16).
+// The chunk position is c ^ f(r), f(r) = ((r >> 1) ^ (r >> 4)) & 7: over any
+// 16 consecutive rows (an MFMA operand read) f takes every value once per row
+// parity, and over rows 4l + k, l = 0..15 (a B staging write) every value
+// twice, so reads are conflict-free and those writes at most two-way.
 template <int ROWS>
 HELIX_DEV int x6_chunk(int k, int r, int c) {
-    return ((k * ROWS + r) << 6) + ((c ^ ((r >> 1) & 7)) << 3);
+    return ((k * ROWS + r) << 6) + ((c ^ (((r >> 1) ^ (r >> 4)) & 7)) << 3);
 }
 
+// One chunk's global inputs for this thread, 1 + 16 + 8 loads (two stages
+// fit the 63 loads the vmcnt counter can track):
+//   x   tokens 16 wave + i (i < 16), channel p = lane
+//   B   tokens 16 wave + 8 hi + e (e < 8), state indices NB lo .. NB lo + NB-1,
+//       one 8/16/32-byte load per token (NB = NP/32 consecutive floats)
 template <int NP>
 struct StageX6 {
     float dtraw;
     float x[16];
-    float b[16][NP / 64];
+    float b[8][NP / 32];
 };
 
-// Chunk c's inputs for this thread: rows (tokens) 16 wave + i, clamped to the
-// last valid token; x at channel p = lane (clamped to the slab), B at state
-// index n = lane + 64 m (clamped to d_state). Masks are applied when staging.
+// Rows are clamped to the last valid token, channels to the slab and state
+// indices to d_state, so every load is in bounds; nothing is masked (see the
+// staging comment in the kernel).
 template <int NP>
 __device__ __forceinline__ void load_stage_x6(StageX6<NP>& st, const HelixScanParams& p,
                                               const float* __restrict__ dt_h,
@@ -70,8 +92,26 @@ __device__ __forceinline__ void load_stage_x6(StageX6<NP>& st, const HelixScanPa
     for (int i = 0; i < 16; ++i) {
         const int jr = min(16 * wave + i, tlen - 1);
         st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
+    }
+    constexpr int NB = NP / 32;
+    const int lo = lane & 31, hi = lane >> 5;
+    const int nb = min(NB * lo, N - NB) * 4;            // byte offset of the lane's run
 #pragma unroll
-        for (int m = 0; m < NP / 64; ++m) st.b[i][m] = buf_elem<float>(rb, min(lane + 64 * m, N - 1), jr * sb0);
+    for (int e = 0; e < 8; ++e) {
+        const int jr = min(16 * wave + 8 * hi + e, tlen - 1);
+        const int off = nb + jr * sb0 * 4;
+        if constexpr (NB == 2) {
+            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rb, off, 0, 0);
+            st.b[e][0] = as_f32(w[0]);
+            st.b[e][1] = as_f32(w[1]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NB / 4; ++q) {
+                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 16 * q, 0, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) st.b[e][4 * q + k] = as_f32(w[k]);
+            }
+        }
     }
 }
 
@@ -81,18 +121,18 @@ template <int ROWS>
 HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[16]) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-        bf16x8 q0, q1, q2;
+        u32x4 q0, q1, q2;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            __bf16 h0, h1, h2;
-            split3(v[8 * half + e], h0, h1, h2);
-            q0[e] = h0;
-            q1[e] = h1;
-            q2[e] = h2;
+        for (int e = 0; e < 4; ++e) {
+            unsigned w0, w1, w2;
+            split3_pair(v[8 * half + 2 * e], v[8 * half + 2 * e + 1], w0, w1, w2);
+            q0[e] = w0;
+            q1[e] = w1;
+            q2[e] = w2;
         }
-        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(0, r, c0 + half)]) = q0;
-        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(1, r, c0 + half)]) = q1;
-        *reinterpret_cast<bf16x8*>(&planes[x6_chunk<ROWS>(2, r, c0 + half)]) = q2;
+        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(0, r, c0 + half)]) = q0;
+        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(1, r, c0 + half)]) = q1;
+        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(2, r, c0 + half)]) = q2;
     }
 }
 
@@ -148,20 +188,33 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         const double lend = __shfl(lcum, 63, 64);
         const float cf = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
 
-        // dtXs^T[p][j] = exp(L_end - Lcum_j) dt_j x[j][p], row p = lane.
+        // dtXs^T[p][j] = exp(L_end - Lcum_j) dt_j x[j][p], row p = lane, and
+        // B^T[n][j] (rows below). No masks: tokens past tlen have
+        // cf_j = 0, so their B rows (clamped, finite) meet zeros; channels past
+        // the slab and state indices past d_state only reach padding rows and
+        // columns of R, which every consumer ignores.
         {
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = keep_if_lt(bcast(cf, 16 * wave + i) * st.x[i], lane, pw);
+            for (int i = 0; i < 16; ++i) v[i] = bcast(cf, 16 * wave + i) * st.x[i];
             stage_split_row<HELIX_HD>(sXt, lane, 2 * wave, v);
         }
-        // B^T[n][j], rows n = lane + 64 m; zero past tlen and d_state.
+        // B^T rows NB lo + k, chunk 2 wave + hi (tokens 16 wave + 8 hi + e).
 #pragma unroll
-        for (int m = 0; m < NP / 64; ++m) {
-            float v[16];
+        for (int k = 0; k < NP / 32; ++k) {
+            u32x4 q0, q1, q2;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = keep_if_lt2(st.b[i][m], 16 * wave + i, tlen, lane + 64 * m, N);
-            stage_split_row<NP>(sBt, lane + 64 * m, 2 * wave, v);
+            for (int e = 0; e < 4; ++e) {
+                unsigned w0, w1, w2;
+                split3_pair(st.b[2 * e][k], st.b[2 * e + 1][k], w0, w1, w2);
+                q0[e] = w0;
+                q1[e] = w1;
+                q2[e] = w2;
+            }
+            const int rn = (NP / 32) * lo + k;
+            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(0, rn, 2 * wave + hi)]) = q0;
+            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(1, rn, 2 * wave + hi)]) = q1;
+            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(2, rn, 2 * wave + hi)]) = q2;
         }
 
         if (MODE != 2 && c > c_begin) {
@@ -184,6 +237,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
             }
         }
         if (slab == 0 && tid == 0) b.ld[seq * p.ld_seq + (long long)c * p.n_head + h] = lam;
+
         __syncthreads();
 
         // This register stage is free again: chunk c+2's inputs travel while

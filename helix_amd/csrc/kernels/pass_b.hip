@@ -34,8 +34,9 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
     const int lane = q & 63, r4 = (q >> 6) & 3, t = q >> 8;
     const int pr = slab * HELIX_HD + (t / NT) * 32 + (lane & 31);
     const int n  = (t % NT) * 32 + 8 * r4 + 4 * (lane >> 5);
-    // Tile padding carries zeros; d_state % 8 == 0, so n..n+3 are all valid or
-    // all padding.
+    // Tile padding (p past head_dim, n past d_state) holds finite values that
+    // no result depends on; it is scanned like the rest but never reaches s1.
+    // d_state % 8 == 0, so n..n+3 are all valid or all padding.
     const bool valid = pr < p.head_dim && n < p.d_state;
 
     const int src = p.has_ids ? b.ids[seq] : seq;

@@ -121,7 +121,7 @@ int np_index(int d_state) {
 
 // Workgroup counts the planner aims for: 256 CUs with a few resident
 // workgroups each, so a launch fills the chip with a short tail.
-constexpr long kTargetWgA = 1024;
+constexpr long kTargetWgA = 512;
 constexpr long kTargetWgC = 1024;
 
 long env_long(const char* name, long dflt) {
