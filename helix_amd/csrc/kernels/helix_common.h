@@ -261,6 +261,86 @@ HELIX_DEV void buf_store_unit(helix_rsrc r, float v0, float v1, float v2, float 
     }
 }
 
+// ---- bf16x6: fp32 values as three bf16 parts --------------------------------
+// v = v0 + v1 + v2 with v0 = bf16(v), v1 = bf16(v - v0), v2 = bf16(v - v0 - v1)
+// (round to nearest even; each residual is exact in fp32 and the three 8-bit
+// significands cover fp32's 24). A product a.b accumulated from the six terms
+// a0 b0 + a0 b1 + a1 b0 + a0 b2 + a1 b1 + a2 b0 is accurate to about 2^-24
+// relative: the dropped terms are below that (bf16x6 in Henry, Tang,
+// Heinecke, "Leveraging the bfloat16 Artificial Intelligence Datatype For
+// Higher-Precision Computations", ARITH 2019).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even bf16 pair (element 0 in the low half), one
+// v_cvt_pk_bf16_f32, and its exact fp32 values.
+HELIX_DEV unsigned pk_bf16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+}
+HELIX_DEV float pk_lo(unsigned w) { return __builtin_bit_cast(float, w << 16); }
+HELIX_DEV float pk_hi(unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// Three-way bf16 split of the pair (a, b), each part packed as a pair:
+// 11 VALU operations for two values.
+HELIX_DEV void split3_pair(float a, float b, unsigned& w0, unsigned& w1, unsigned& w2) {
+    w0 = pk_bf16(a, b);
+    const float ra = a - pk_lo(w0), rb = b - pk_hi(w0);
+    w1 = pk_bf16(ra, rb);
+    w2 = pk_bf16(ra - pk_lo(w1), rb - pk_hi(w1));
+}
+
+// Six-product MFMA of split operands a[3] x b[3], smallest terms first.
+HELIX_DEV f32x16 mfma_x6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 acc) {
+    acc = mfma_bf16(a[2], b[0], acc);
+    acc = mfma_bf16(a[1], b[1], acc);
+    acc = mfma_bf16(a[0], b[2], acc);
+    acc = mfma_bf16(a[1], b[0], acc);
+    acc = mfma_bf16(a[0], b[1], acc);
+    acc = mfma_bf16(a[0], b[0], acc);
+    return acc;
+}
+
+// Split planes in LDS: [3][ROWS][NCH * 8] bf16, rows of NCH 16-byte chunks,
+// chunk c of row r stored at chunk position c ^ f(r):
+//   NCH = 8  (128-byte rows): f(r) = ((r >> 1) ^ (r >> 4)) & 7. Row bases
+//            alternate between two bank halves; over 16 consecutive rows f
+//            takes every value once per parity, and over rows 4l + k
+//            (l < 16) every value twice.
+//   NCH = 16 (256-byte rows, all starting at bank 0): f(r) = r & 15.
+// Either way the 16-byte reads of an MFMA operand (16 consecutive rows, one
+// chunk each) cover all 64 banks once per 16 lanes.
+template <int ROWS, int NCH>
+HELIX_DEV int x6_off(int k, int r, int c) {
+    static_assert(NCH == 8 || NCH == 16, "rows of 8 or 16 chunks");
+    const int f = NCH == 8 ? (((r >> 1) ^ (r >> 4)) & 7) : (r & 15);
+    return ((k * ROWS + r) * NCH + (c ^ f)) * 8;
+}
+
+// The three planes' chunk c of row r, as MFMA operands.
+template <int ROWS, int NCH>
+HELIX_DEV void x6_read(const __bf16* planes, int r, int c, bf16x8 (&o)[3]) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) o[k] = *reinterpret_cast<const bf16x8*>(&planes[x6_off<ROWS, NCH>(k, r, c)]);
+}
+
+// Split eight fp32 values and store them as chunk c of row r (three planes).
+template <int ROWS, int NCH>
+HELIX_DEV void x6_write8(__bf16* planes, int r, int c, const float* v) {
+    u32x4 q0, q1, q2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        unsigned w0, w1, w2;
+        split3_pair(v[2 * e], v[2 * e + 1], w0, w1, w2);
+        q0[e] = w0;
+        q1[e] = w1;
+        q2[e] = w2;
+    }
+    *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, NCH>(0, r, c)]) = q0;
+    *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, NCH>(1, r, c)]) = q1;
+    *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, NCH>(2, r, c)]) = q2;
+}
+
 // Raw-register form of an element of T: a float stays a float, a bf16 stays
 // its 16 bits zero-extended in a 32-bit register. Loads into this form carry
 // no data dependence (nothing packs two 16-bit results into one register), so

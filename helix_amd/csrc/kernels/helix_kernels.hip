@@ -6,4 +6,5 @@
 #include "pass_b.hip"
 #include "pass_c_f32.hip"
 #include "pass_c_bf16.hip"
+#include "pass_c_x6.hip"
 #include "pass_c_walk.hip"

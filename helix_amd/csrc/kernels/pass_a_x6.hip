@@ -6,57 +6,18 @@
 // but the GEMM runs on v_mfma_f32_32x32x16_bf16, which MI355X issues at 16x
 // the fp32 matrix rate. Each fp32 operand v is split into three bf16 parts
 //     v = v0 + v1 + v2,  v0 = bf16(v), v1 = bf16(v - v0), v2 = bf16(v - v0 - v1)
-// (each residual is exact in fp32, and the three 8-bit significands cover
-// fp32's 24), and the product is accumulated in fp32 from the six terms whose
-// size is at least 2^-16 of the leading one:
-//     a.b ~ a0 b0 + (a0 b1 + a1 b0) + (a0 b2 + a1 b1 + a2 b0)
-// The dropped terms (a1 b2, a2 b1, a2 b2) are below 2^-24 relative, the size
-// of an fp32 rounding, so the state keeps fp32 accuracy (bf16x6 in the
-// literature: Henry, Tang, Heinecke, "Leveraging the bfloat16 Artificial
-// Intelligence Datatype For Higher-Precision Computations", ARITH 2019).
+// (split3_pair and mfma_x6 in helix_common.h): fp32 accuracy from six bf16
+// products per fp32 product.
 // The terms are issued smallest first so the large ones are added last.
 //
 // Layout: the workgroup computes R[n][p] (N x 64), M = n, N = p, K = token.
 // The split operands are staged in LDS k-contiguous: three planes of
-// B^T[n][j] and three of dtXs^T[p][j], rows of 64 tokens (128 bytes, eight
-// 16-byte chunks). Chunk c of row r sits at chunk position c ^ ((r >> 1) & 7),
-// so the 16-byte reads of an MFMA operand (16 consecutive rows, one chunk
-// each) and the 16-byte staging writes both cover all 64 banks once per
-// 16 lanes. Wave w owns P tile (w & 1) and N tiles (w >> 1) + 2i, and stages
-// tokens 16w .. 16w+15 (chunks 2w and 2w+1) of every row: dtXs^T row p = lane
-// both chunks; B^T rows NB*lo .. NB*lo + NB-1 (NB = NP/32) chunk 2w + hi.
+// B^T[n][j] and three of dtXs^T[p][j], rows of 64 tokens (eight 16-byte
+// chunks, swizzled as x6_off describes). Wave w owns P tile (w & 1) and N
+// tiles (w >> 1) + 2i, and stages tokens 16w .. 16w+15 (chunks 2w and 2w+1)
+// of every row: dtXs^T row p = lane both chunks; B^T rows NB*lo ..
+// NB*lo + NB-1 (NB = NP/32) chunk 2w + hi.
 #include "helix_common.h"
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// Round-to-nearest-even bf16 pair (element 0 in the low half), one
-// v_cvt_pk_bf16_f32, and its exact fp32 values.
-HELIX_DEV unsigned pk_bf16(float a, float b) {
-    const f32x2 v = {a, b};
-    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
-}
-HELIX_DEV float pk_lo(unsigned w) { return __builtin_bit_cast(float, w << 16); }
-HELIX_DEV float pk_hi(unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
-
-// Three-way bf16 split of the pair (a, b), each part packed as a pair:
-// 11 VALU operations for two values.
-HELIX_DEV void split3_pair(float a, float b, unsigned& w0, unsigned& w1, unsigned& w2) {
-    w0 = pk_bf16(a, b);
-    const float ra = a - pk_lo(w0), rb = b - pk_hi(w0);
-    w1 = pk_bf16(ra, rb);
-    w2 = pk_bf16(ra - pk_lo(w1), rb - pk_hi(w1));
-}
-
-// Element offset of 16-byte chunk c of row r in plane k (rows of 64 bf16).
-// The chunk position is c ^ f(r), f(r) = ((r >> 1) ^ (r >> 4)) & 7: over any
-// 16 consecutive rows (an MFMA operand read) f takes every value once per row
-// parity, and over rows 4l + k, l = 0..15 (a B staging write) every value
-// twice, so reads are conflict-free and those writes at most two-way.
-template <int ROWS>
-HELIX_DEV int x6_chunk(int k, int r, int c) {
-    return ((k * ROWS + r) << 6) + ((c ^ (((r >> 1) ^ (r >> 4)) & 7)) << 3);
-}
 
 // One chunk's global inputs for this thread, 1 + 16 + 8 loads (two stages
 // fit the 63 loads the vmcnt counter can track):
@@ -130,9 +91,9 @@ HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[1
             q1[e] = w1;
             q2[e] = w2;
         }
-        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(0, r, c0 + half)]) = q0;
-        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(1, r, c0 + half)]) = q1;
-        *reinterpret_cast<u32x4*>(&planes[x6_chunk<ROWS>(2, r, c0 + half)]) = q2;
+        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(0, r, c0 + half)]) = q0;
+        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(1, r, c0 + half)]) = q1;
+        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(2, r, c0 + half)]) = q2;
     }
 }
 
@@ -212,9 +173,9 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
                 q2[e] = w2;
             }
             const int rn = (NP / 32) * lo + k;
-            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(0, rn, 2 * wave + hi)]) = q0;
-            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(1, rn, 2 * wave + hi)]) = q1;
-            *reinterpret_cast<u32x4*>(&sBt[x6_chunk<NP>(2, rn, 2 * wave + hi)]) = q2;
+            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(0, rn, 2 * wave + hi)]) = q0;
+            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(1, rn, 2 * wave + hi)]) = q1;
+            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(2, rn, 2 * wave + hi)]) = q2;
         }
 
         if (MODE != 2 && c > c_begin) {
@@ -252,15 +213,15 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 #pragma unroll
         for (int s = 0; s < HELIX_CS / 16; ++s) {
             const int cx = 2 * s + hi;
-            const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(0, pt * 32 + lo, cx)]);
-            const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(1, pt * 32 + lo, cx)]);
-            const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(&sXt[x6_chunk<HELIX_HD>(2, pt * 32 + lo, cx)]);
+            const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(0, pt * 32 + lo, cx)]);
+            const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(1, pt * 32 + lo, cx)]);
+            const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(2, pt * 32 + lo, cx)]);
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
                 const int rn = (nt0 + 2 * i) * 32 + lo;
-                const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(0, rn, cx)]);
-                const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(1, rn, cx)]);
-                const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(&sBt[x6_chunk<NP>(2, rn, cx)]);
+                const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(0, rn, cx)]);
+                const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(1, rn, cx)]);
+                const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(2, rn, cx)]);
                 acc[i] = mfma_bf16(b2, x0, acc[i]);
                 acc[i] = mfma_bf16(b1, x1, acc[i]);
                 acc[i] = mfma_bf16(b0, x2, acc[i]);

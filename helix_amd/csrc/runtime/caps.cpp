@@ -60,15 +60,18 @@ constexpr HelixMatmulTraits kBf16WalkTraits[] = {
      "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256, true},
 };
 
-// Pass A on bf16 MFMA with three-way operand splitting (pass_a_x6.hip):
-// fp32-equivalent state at 16x the fp32 matrix issue rate. The default on
-// every path; HELIX_PASSA=f32 selects the fp32-MFMA kernels above.
+// bf16x6 kernels: GEMMs on bf16 MFMA over operands split into three bf16
+// parts, fp32 accuracy at 16x the fp32 matrix issue rate. Pass A uses them on
+// every path (pass_a_x6.hip) and the fp32 path's Pass C for d_state <= 128
+// (pass_c_x6.hip; d_state 256 does not fit its LDS budget). The default;
+// HELIX_X6=0 selects the fp32-MFMA kernels above.
 constexpr const char* kX6StateF32[] = {"helix_chunk_state_x6f32_n64", "helix_chunk_state_x6f32_n128",
                                        "helix_chunk_state_x6f32_n256"};
 constexpr const char* kX6StateSbf[] = {"helix_chunk_state_x6sbf_n64", "helix_chunk_state_x6sbf_n128",
                                        "helix_chunk_state_x6sbf_n256"};
 constexpr const char* kX6StateAgg[] = {"helix_chunk_state_x6agg_n64", "helix_chunk_state_x6agg_n128",
                                        "helix_chunk_state_x6agg_n256"};
+constexpr const char* kX6OutF32[] = {"helix_chunk_out_x6_n64", "helix_chunk_out_x6_n128", nullptr};
 
 // The selectable trait sets: [family: fp32, bf16, bf16 walk][np index], with
 // Pass A on fp32 MFMA or bf16x6. Built once; names live as long as the process.
@@ -85,18 +88,24 @@ struct TraitSets {
                 v = base[fam][k];
                 std::string nm = v.name;
                 const size_t at = nm.find(" (d_state");
-                names[1][fam][k] = nm.substr(0, at) + ", pass A bf16x6" + nm.substr(at);
+                const bool x6c = fam == 0 && kX6OutF32[k] != nullptr;
+                names[1][fam][k] =
+                    nm.substr(0, at) + (x6c ? ", passes A and C bf16x6" : ", pass A bf16x6") + nm.substr(at);
                 v.name = names[1][fam][k].c_str();
                 v.k_chunk_state = x6[fam][k];
                 v.mfma_a = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
+                if (x6c) {
+                    v.k_chunk_out = kX6OutF32[k];
+                    v.mfma_c = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
+                }
             }
     }
 };
 
 const HelixMatmulTraits& pick_traits(int fam, int k) {
     static const TraitSets sets;
-    const char* v = std::getenv("HELIX_PASSA");
-    const int x6 = (v && v[0] == 'f') ? 0 : 1;
+    const char* v = std::getenv("HELIX_X6");
+    const int x6 = (v && v[0] == '0') ? 0 : 1;
     return sets.t[x6][fam][k];
 }
 
@@ -104,6 +113,7 @@ const char* const kKernelNames[] = {
     "helix_chunk_state_x6f32_n64", "helix_chunk_state_x6f32_n128", "helix_chunk_state_x6f32_n256",
     "helix_chunk_state_x6sbf_n64", "helix_chunk_state_x6sbf_n128", "helix_chunk_state_x6sbf_n256",
     "helix_chunk_state_x6agg_n64", "helix_chunk_state_x6agg_n128", "helix_chunk_state_x6agg_n256",
+    "helix_chunk_out_x6_n64",      "helix_chunk_out_x6_n128",
     "helix_chunk_state_f32_n64",  "helix_chunk_state_f32_n128", "helix_chunk_state_f32_n256",
     "helix_chunk_state_sbf_n64",  "helix_chunk_state_sbf_n128", "helix_chunk_state_sbf_n256",
     "helix_state_scan_f32",

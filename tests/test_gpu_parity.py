@@ -8,8 +8,8 @@ Mirrors the reference's tests/test_metal_parity.mm:
     (:163-166); s1 always held to the fp32 bound (:214-218).
 Both MI355X paths are exercised explicitly (SGMMA -> fp32 MFMA Pass C, MPP ->
 bf16 Pass C) because AUTO resolves to bf16 for every multipass shape here, and
-each with Pass A on its default bf16x6 split products and on fp32 MFMA
-(HELIX_PASSA=f32).
+each with its default bf16x6 split-product kernels and with the fp32-MFMA
+ones (HELIX_X6=0).
 The single-pass modes are absent: this build declines multipass=false.
 
 Then the BASELINE.json configurations at full size, gated on
@@ -68,11 +68,12 @@ MODES = [
     ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}),
     ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}),
     ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}),
-    # Pass A on fp32 MFMA instead of bf16x6 split products.
-    ("fp32/mmaA/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_PASSA": "f32"}),
-    ("bf16/mmaA/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA": "f32"}),
-    ("bf16walk/mmaA/long", HELIX_BACKEND_MPP, None, "long",
-     {"HELIX_PASSA": "f32", "HELIX_BF16_PASSC": "walk"}),
+    # fp32-MFMA kernels instead of bf16x6 split products.
+    ("fp32/mma/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_X6": "0"}),
+    ("fp32/mma", HELIX_BACKEND_SGMMA, None, "short", {"HELIX_X6": "0"}),
+    ("bf16/mma/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_X6": "0"}),
+    ("bf16walk/mma/long", HELIX_BACKEND_MPP, None, "long",
+     {"HELIX_X6": "0", "HELIX_BF16_PASSC": "walk"}),
 ]
 
 
@@ -125,7 +126,7 @@ def _baseline(name, memory):
 
 CASES = [(n, path, mem) for n, c in CONFIGS.items() for path in c.paths for mem in ("dist", "long")]
 CASES += [(n, "bf16walk", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
-CASES += [(n, path + "/mmaA", "long") for n, c in CONFIGS.items() for path in c.paths]
+CASES += [(n, path + "/mma", "long") for n, c in CONFIGS.items() for path in c.paths]
 
 
 @pytest.mark.parametrize("name,path,memory", CASES, ids=[f"{n}-{p}-{m}" for n, p, m in CASES])
@@ -136,7 +137,7 @@ def test_baseline_config(gpu, name, path, memory):
     d.multipass = True
     d.backend = HELIX_BACKEND_MPP if path.startswith("bf16") else HELIX_BACKEND_SGMMA
     with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None,
-             HELIX_PASSA="f32" if path.endswith("/mmaA") else None):
+             HELIX_X6="0" if path.endswith("/mma") else None):
         assert gpu.supported(d)
         assert (gpu.select_backend(d) == HELIX_BACKEND_MPP) == path.startswith("bf16")
         print(f"[{name} {path} {memory}] {gpu.backend_desc(d)}", flush=True)

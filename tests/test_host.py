@@ -170,16 +170,20 @@ def test_backend_selection(host):
     assert host.select_backend(mp(shape, HELIX_BACKEND_AUTO)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_SGMMA)) == HELIX_BACKEND_SGMMA
-    # Pass A runs on bf16x6 split products by default on every path.
-    assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32, pass A bf16x6 (d_state<=128)"
+    # bf16x6 split products by default: Pass A on every path, and the fp32
+    # path's Pass C up to d_state 128.
+    assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
+            == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
     assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C, pass A bf16x6 (d_state<=256)"
+    assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
+            == "mfma fp32, pass A bf16x6 (d_state<=256)")
     with env(HELIX_BF16_PASSC="walk"):
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
-            == "mfma fp32, pass A bf16x6 (d_state<=64)")
-    # HELIX_PASSA=f32 selects the fp32-MFMA Pass A.
-    with env(HELIX_PASSA="f32"):
+            == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
+    # HELIX_X6=0 selects the fp32-MFMA kernels.
+    with env(HELIX_X6="0"):
         assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
         with env(HELIX_BF16_PASSC="walk"):
