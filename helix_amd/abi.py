@@ -44,6 +44,9 @@ class HelixPlanInfo(ctypes.Structure):
         ("s_seg_bytes", c_uint64),
         ("launches", c_int32),
         ("np", c_int32),
+        ("kernel_a", ctypes.c_char_p),
+        ("kernel_b", ctypes.c_char_p),
+        ("kernel_c", ctypes.c_char_p),
     ]
 
 

@@ -216,5 +216,8 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->s_seg_bytes = pl.sg_elems * sizeof(float);
     out->launches = 3 * pl.n_groups;
     out->np = tr.np;
+    out->kernel_a = tr.k_chunk_state;
+    out->kernel_b = tr.k_state_scan;
+    out->kernel_c = tr.k_chunk_out;
     return HELIX_OK;
 }

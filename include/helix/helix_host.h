@@ -34,6 +34,9 @@ typedef struct {
     uint64_t s_seg_bytes;       /* segment aggregates / segment initial states   */
     int32_t  launches;          /* kernel launches per encode                    */
     int32_t  np;                /* d_state padding of the selected kernels       */
+    const char* kernel_a;       /* code-object names of the Pass A, B and C      */
+    const char* kernel_b;       /* kernels (static strings)                      */
+    const char* kernel_c;
 } helix_plan_info;
 
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */

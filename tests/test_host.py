@@ -182,6 +182,20 @@ def test_backend_selection(host):
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
+    # The plan names the kernels each pass launches.
+    k = host.plan_info(mp(shape))
+    assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
+        b"helix_chunk_state_x6sbf_n128", b"helix_state_scan_f32", b"helix_chunk_out_bf16_n128")
+    k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
+    assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n128", b"helix_chunk_out_x6_n128")
+    k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
+    assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
+    with env(HELIX_BF16_PASSC="walk"):
+        k = host.plan_info(mp(shape))
+        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk_bf16_n128")
+    with env(HELIX_X6="0"):
+        k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
+        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_f32_n128", b"helix_chunk_out_f32_n128")
     # HELIX_X6=0 selects the fp32-MFMA kernels.
     with env(HELIX_X6="0"):
         assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
