@@ -57,6 +57,10 @@
 #define HELIX_N_MAX 256
 /* Threads per workgroup: four wave64s, one per SIMD of a CU. */
 #define HELIX_WG 256
+/* Heads per workgroup of the chunk-walking Pass C (four waves per head):
+ * two up to d_state 128; one at 256, where a head's state needs the whole
+ * register budget of a wave. */
+#define HELIX_WALK_HPW(np) ((np) <= 128 ? 2 : 1)
 
 typedef struct HelixScanParams {
     int n_tok;

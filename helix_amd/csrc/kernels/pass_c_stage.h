@@ -88,14 +88,18 @@ __device__ __forceinline__ void load_cb_rows(float (&vc)[16][NP / 64], float (&v
 
 // Store one 32 x 32 output tile (t block tb, P block pb of the slab at p0) of
 // head h: lane (lo, hi), register r holds y[t = 32 tb + acc_row(r, hi)][32 pb + lo].
-// Rows past tlen and columns past the slab width are not written.
+// Rows past tlen and columns past the slab width are not written; with
+// tlen <= 0 nothing is (t0 must still address a row of y).
 __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanParams& p,
                                              const HelixScanBuffers& b, int seq, int h, int t0,
                                              int tlen, int p0, int pw, int tb, int pb, int lo, int hi) {
     const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
+    // tlen <= 0 stores nothing: the resource's range is empty, so the range
+    // check drops every store whatever its offset.
+    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u : 0u;
     const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
                                         (long long)p0 * p.s_y[2],
-                                    ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u);
+                                    bytes);
     const int pp = pb * 32 + lo;
     const int voff = (4 * hi * sy0 + pp * sy2) * 4;
 #pragma unroll

@@ -7,106 +7,123 @@
 //     y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C S_init)
 // with bf16 operands and fp32 accumulators.
 //
-// Here one workgroup owns (seq, segment, head, 64-wide P slab). It starts from
-// the segment's initial state S_seg(s) (fp32, from Pass B) and walks the
+// Here one workgroup owns (seq, segment, HELIX_WALK_HPW heads of one B/C
+// group, 64-wide P slab); the heads share the staging of B and C, four waves
+// per head. Each head starts from the segment's initial state S_seg(s)
+// (fp32, from Pass B) and walks the
 // segment's chunks in order, so the per-chunk initial state never touches
 // HBM: after producing y for chunk c it advances
 //     R <- exp(L_end_c) R + B_c^T . (decay . dt . x)_c          (G4)
 // in the same registers, on bf16 operands with fp32 accumulation. R only
-// feeds y here; the fp32-exact carried state and s1 come from Passes A and B.
+// feeds y here; the fp32-accurate carried state and s1 come from Passes A
+// and B (Pass A runs its aggregate-only variant).
 //
 // Wave w owns output tile (t block tb = w >> 1, P block pb = w & 1) and keeps
 // its own copy of R[:, pb block] (all N/32 state tiles) in MFMA result
-// layout: lane (lo, hi), register r holds R[8(r/4) + 4hi + r%4 + 32nt][lo].
-// That layout feeds G3 directly as the B operand: an MFMA's sixteen K slots
-// may hold any sixteen state indices as long as the A operand (C) uses the
-// same ones, and registers 0..7 of a tile give half hi the indices
-// {0-3, 8-11} + 4hi, registers 8..15 the same plus 16. The G1 result is kept
-// the same way (as C.B^T transposed, so the lane owns one output row t) and
-// feeds G2's A operand without an LDS round trip.
+// layout: lane (lo, hi), register r holds R[32nt + 8(r/4) + 4hi + r%4][lo].
+// Registers 8q .. 8q+7 of a tile therefore hold, for half hi, the state
+// indices 32nt + 16q + {0-3, 8-11} + 4hi. An MFMA's sixteen K slots may hold
+// any sixteen indices as long as both operands use the same ones, so every
+// k-contiguous operand in LDS is stored in that order: within each group of
+// 16, index i sits at position perm16(i) (bits 2 and 3 swapped), and a lane's
+// eight K values are one 16-byte read. R feeds G3 straight from registers;
+// the G1 result (C.B^T, kept transposed so the lane owns one output row t)
+// feeds G2 the same way.
+//
+// LDS (bf16, k-contiguous, perm16 order): C[t][n] and B[j][n] (G1, G3),
+// B^T[n][j] (G4), dtX^T[p][j] (G2) and dtXs^T[p][j] (G4); rows padded by 8.
 #include "helix_common.h"
 
-template <int NP>
+#include "pass_c_stage.h"
+
+// Position of index i inside its group of 16 (bits 2 and 3 swapped).
+HELIX_DEV int perm16(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// Per-chunk inputs prefetched a chunk ahead: dt for token `lane`, and x for
+// tokens 16 wave + i at channel p = lane.
 struct StageW {
     float dtraw;
     float x[16];
-    float b[16][NP / 64];
-    float c[16][NP / 64];
 };
 
-template <int NP>
-__device__ __forceinline__ void load_stage_w(StageW<NP>& st, const HelixScanParams& p,
+__device__ __forceinline__ void load_stage_w(StageW& st, const HelixScanParams& p,
                                              const float* __restrict__ dt_h,
-                                             const float* __restrict__ x_h,
-                                             const float* __restrict__ B_g,
-                                             const float* __restrict__ C_g, int c, int lane,
-                                             int wave, int pw, int N) {
+                                             const float* __restrict__ x_h, int c, int lane,
+                                             int wave, int pw) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
-    st.dtraw = dt_h[(long long)(t0 + min(lane, tlen - 1)) * p.s_dt[0]];
-    const long long xc = (long long)min(lane, pw - 1) * p.s_x[2];
+    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int jr = min(wave + 4 * i, tlen - 1);
-        st.x[i] = x_h[(long long)(t0 + jr) * p.s_x[0] + xc];
-        const float* brow = B_g + (long long)(t0 + jr) * p.s_b[0];
-        const float* crow = C_g + (long long)(t0 + jr) * p.s_c[0];
-#pragma unroll
-        for (int m = 0; m < NP / 64; ++m) {
-            const int nc = min(lane + 64 * m, N - 1);
-            st.b[i][m] = brow[nc];
-            st.c[i][m] = crow[nc];
-        }
-    }
+    for (int i = 0; i < 16; ++i) st.x[i] = buf_elem<float>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
 }
 
-// Eight bf16 K values from MFMA result registers r0..r0+7.
+// Eight bf16 K values from MFMA result registers r0 .. r0+7.
 HELIX_DEV bf16x8 pack8(const f32x16& v, int r0) {
     bf16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = to_bf16(v[r0 + e]);
+    for (int e = 0; e < 8; ++e) {
+        const float f = v[r0 + e];
+        o[e] = to_bf16(f);
+    }
     return o;
 }
 
-// Two 4-element bf16 runs from an LDS row: columns [c0, c0+4) and [c0+8, c0+12).
-HELIX_DEV bf16x8 lds_pair4(const __bf16* row, int c0) {
-    const bf16x4 a = *reinterpret_cast<const bf16x4*>(row + c0);
-    const bf16x4 b = *reinterpret_cast<const bf16x4*>(row + c0 + 8);
-    bf16x8 o;
-    o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
-    o[4] = b[0]; o[5] = b[1]; o[6] = b[2]; o[7] = b[3];
-    return o;
+// Sixteen consecutive tokens' values written as one perm16-ordered group.
+HELIX_DEV void store16_perm(__bf16* row, const float (&v)[16]) {
+    bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        a[e] = to_bf16(v[e]);          // positions 0..3   <- 0..3
+        a[4 + e] = to_bf16(v[8 + e]);  // positions 4..7   <- 8..11
+        b[e] = to_bf16(v[4 + e]);      // positions 8..11  <- 4..7
+        b[4 + e] = to_bf16(v[12 + e]); // positions 12..15 <- 12..15
+    }
+    *reinterpret_cast<bf16x8*>(row) = a;
+    *reinterpret_cast<bf16x8*>(row + 8) = b;
 }
 
 template <int NP>
 __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int HPW = HELIX_WALK_HPW(NP);   // heads per workgroup, four waves each
+    constexpr int NW  = 4 * HPW;          // waves per workgroup
     constexpr int NT  = NP / 32;          // state tiles per P block
     constexpr int RS  = NP + 8;           // bf16 row stride of C[t][n], B[j][n]
     constexpr int RSJ = HELIX_CS + 8;     // bf16 row stride of B^T[n][j], dtX^T[p][j], dtXs^T[p][j]
+    constexpr int NCH = NP / 8;           // 8-element runs per C / B row
 
     __shared__ __attribute__((aligned(16))) __bf16 sC[HELIX_CS * RS];
     __shared__ __attribute__((aligned(16))) __bf16 sB[HELIX_CS * RS];
     __shared__ __attribute__((aligned(16))) __bf16 sBt[NP * RSJ];
-    __shared__ __attribute__((aligned(16))) __bf16 sXt[HELIX_HD * RSJ];
-    __shared__ __attribute__((aligned(16))) __bf16 sXst[HELIX_HD * RSJ];
-    __shared__ __attribute__((aligned(16))) double sL[HELIX_CS];
-    __shared__ __attribute__((aligned(16))) float sE[HELIX_CS];
+    __shared__ __attribute__((aligned(16))) __bf16 sXt[HPW][HELIX_HD * RSJ];
+    __shared__ __attribute__((aligned(16))) __bf16 sXst[HPW][HELIX_HD * RSJ];
+    __shared__ __attribute__((aligned(16))) double sL[HPW][HELIX_CS];
+    __shared__ __attribute__((aligned(16))) float sE[HPW][HELIX_CS];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, lo = lane & 31, hi = lane >> 5;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
+    const int hw = wave >> 2, w4 = wave & 3;      // head slot in the workgroup, role within it
     const int N = p.d_state, P = p.head_dim;
     const int hpg = p.heads_per_group;
+    const int npair = (hpg + HPW - 1) / HPW;
 
-    // 1-D grid, heads of one B/C group consecutive in the logical order so
-    // they share an XCD (and the chunk's B and C in its L2).
-    const unsigned total = (unsigned)(p.n_seg * p.n_head * p.n_pslab * p.n_seq);
+    // 1-D grid, a group's head blocks consecutive in the logical order so they
+    // share an XCD (and the chunk's B and C in its L2).
+    const unsigned total = (unsigned)(p.n_seg * p.n_group * npair * p.n_pslab * p.n_seq);
     unsigned wid = xcd_logical_id(blockIdx.x, total);
-    const int hig = (int)(wid % (unsigned)hpg);      wid /= (unsigned)hpg;
-    const int seg = (int)(wid % (unsigned)p.n_seg);  wid /= (unsigned)p.n_seg;
-    const int g   = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
+    const int pair = (int)(wid % (unsigned)npair);   wid /= (unsigned)npair;
+    const int seg  = (int)(wid % (unsigned)p.n_seg); wid /= (unsigned)p.n_seg;
+    const int g    = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
     const int slab = (int)(wid % (unsigned)p.n_pslab);
     const int seq  = (int)(wid / (unsigned)p.n_pslab);
-    const int h  = g * hpg + hig;
+    // A workgroup of the last block may have fewer heads than HPW: its spare
+    // waves walk the block's last head again and store nothing.
+    const int hslot = HPW * pair + hw;
+    const bool head_ok = hslot < hpg;
+    const int h  = g * hpg + min(hslot, hpg - 1);
     const int p0 = slab * HELIX_HD;
     const int pw = min(HELIX_HD, P - p0);
 
@@ -120,7 +137,7 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
     const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
     const float* __restrict__ C_g  = b.C + seq * p.seq_c + g * p.s_c[1];
 
-    const int tb = wave >> 1, pb = wave & 1;
+    const int tb = w4 >> 1, pb = w4 & 1;
     const int pp = pb * 32 + lo;                  // this lane's P column in the slab
 
     // R[n][p] for p in this wave's P block: the slab tile of S_seg(s) is
@@ -140,117 +157,217 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
             }
     }
 
-    StageW<NP> st;
-    load_stage_w<NP>(st, p, dt_h, x_h, B_g, C_g, c_begin, lane, wave, pw, N);
+    // B and C are staged once for the workgroup's heads. All NW waves share
+    // the 64 rows, RPW each: lane (jj = lane % RPW, qq = lane / RPW) holds
+    // state indices 8q .. 8q+7, q = qq + (64/RPW) k, of row RPW wave + jj;
+    // RPW consecutive rows per lane group keep the B^T writes contiguous.
+    constexpr int RPW = HELIX_CS / NW;
+    constexpr int QPI = 64 / RPW;                 // runs per wave instruction
+    constexpr int KQ  = NCH / QPI;
+    const int jj = lane % RPW, qq = lane / RPW;
+    const int jrow = RPW * wave + jj;
+    const int jp = perm16(jrow);
+
+    StageW st;
+    load_stage_w(st, p, dt_h, x_h, c_begin, lane, w4, pw);
+
+    // The output tile of chunk c is stored after chunk c+1's B and C loads are
+    // issued: the vmcnt counter completes in order and counts stores, so a
+    // store issued first would be waited on together with those loads.
+    f32x16 y_prev = zero16();
 
     for (int c = c_begin; c < c_end; ++c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
 
-        const float dtv = lane < tlen ? helix_dt(p, st.dtraw) : 0.0f;
-        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
-        const double lend = __shfl(lcum, 63, 64);
-        const float sdec = lane < tlen ? exp_diff(lend, lcum) : 0.0f;
-
-        // ---- stage this chunk into LDS (bf16 operands) ----------------------
+        // ---- B and C of this chunk (mostly from L2: a group's heads share them)
+        {
+            const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
+            const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+            const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * 4u);
+            const int jr = min(jrow, tlen - 1);
+            float vb[KQ][8], vc[KQ][8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int j = wave + 4 * i;
-            const float dj = bcast(dtv, j);
-            const float sj = bcast(sdec, j);
-            const float xv = lane < pw ? st.x[i] : 0.0f;
-            sXt[lane * RSJ + j]  = to_bf16(dj * xv);
-            sXst[lane * RSJ + j] = to_bf16(sj * dj * xv);
+            for (int k = 0; k < KQ; ++k) {
+                const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
+                const u32x4 b0 = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4, 0, 0);
+                const u32x4 b1 = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4 + 16, 0, 0);
+                const u32x4 c0 = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4, 0, 0);
+                const u32x4 c1 = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4 + 16, 0, 0);
 #pragma unroll
-            for (int m = 0; m < NP / 64; ++m) {
-                const int n = lane + 64 * m;
-                const bool ok = j < tlen && n < N;
-                const __bf16 bv = to_bf16(ok ? st.b[i][m] : 0.0f);
-                sB[j * RS + n]   = bv;
-                sBt[n * RSJ + j] = bv;
-                sC[j * RS + n]   = to_bf16(ok ? st.c[i][m] : 0.0f);
+                for (int e = 0; e < 4; ++e) {
+                    vb[k][e] = as_f32(b0[e]);
+                    vb[k][4 + e] = as_f32(b1[e]);
+                    vc[k][e] = as_f32(c0[e]);
+                    vc[k][4 + e] = as_f32(c1[e]);
+                }
+            }
+            // Chunk c-1's tile (a full chunk: only the sequence's last chunk is
+            // ragged). Unconditional, so every path has the same counter
+            // state; on the first chunk no row is valid and the range check
+            // drops the stores.
+            const bool have_prev = c > c_begin;
+            store_y_tile(y_prev, p, b, seq, h, have_prev ? t0 - HELIX_CS : t0,
+                         (have_prev && head_ok) ? HELIX_CS : 0, p0, pw, tb, pb, lo, hi);
+            // C is zeroed past tlen and d_state; that is all G1 and G3 need
+            // (B rows past tlen only meet zero dtXs columns in G4).
+#pragma unroll
+            for (int k = 0; k < KQ; ++k) {
+                const int q = qq + QPI * k;
+                const int cpos = 16 * (q >> 1) + 4 * (q & 1);   // perm16 position of 8q; 8q+4 sits 8 further
+                const int j = jrow;
+                bf16x4 b_lo, b_hi, c_lo, c_hi;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    b_lo[e] = to_bf16(vb[k][e]);
+                    b_hi[e] = to_bf16(vb[k][4 + e]);
+                    c_lo[e] = to_bf16(keep_if_lt2(vc[k][e], j, tlen, 8 * q, N));
+                    c_hi[e] = to_bf16(keep_if_lt2(vc[k][4 + e], j, tlen, 8 * q, N));
+                }
+                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
+                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos + 8]) = b_hi;
+                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos]) = c_lo;
+                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos + 8]) = c_hi;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sBt[(8 * q + e) * RSJ + jp] = b_lo[e];
+                    sBt[(8 * q + 4 + e) * RSJ + jp] = b_hi[e];
+                }
             }
         }
-        if (wave == 0) {
-            sL[lane] = lcum;
-            sE[lane] = expf((float)lcum);
+
+        // ---- decay preamble, dtX^T and dtXs^T -----------------------------------
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lend = __shfl(lcum, 63, 64);
+        const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
+        {
+            float vx[16], vs[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float dx = bcast(dtv, 16 * w4 + i) * st.x[i];
+                vx[i] = dx;
+                vs[i] = bcast(sdec, 16 * w4 + i) * dx;
+            }
+            store16_perm(&sXt[hw][lane * RSJ + 16 * w4], vx);
+            store16_perm(&sXst[hw][lane * RSJ + 16 * w4], vs);
+        }
+        if (w4 == 0) {
+            sL[hw][lane] = lcum;
+            sE[hw][lane] = expf((float)lcum);
         }
         __syncthreads();
 
-        if (c + 1 < c_end) load_stage_w<NP>(st, p, dt_h, x_h, B_g, C_g, c + 1, lane, wave, pw, N);
+        if (c + 1 < c_end) load_stage_w(st, p, dt_h, x_h, c + 1, lane, w4, pw);
 
-        // ---- G1: CB^T tiles (jb, tb) for jb <= tb, kept as M^T -------------
-        // D'[j][t] = sum_n B[j][n] C[t][n]; lane owns column t = tb*32 + lo.
+        // ---- G1: CB^T tiles (jb, tb) for jb <= tb, kept as M^T ---------------
+        // D'[j][t] = sum_n B[j][n] C[t][n]; lane owns column t = tb*32 + lo,
+        // register r holds j = 32 jb + acc_row(r, hi).
         const int t_own = tb * 32 + lo;
-        const double l_t = sL[t_own];
+        const double l_t = sL[hw][t_own];
         bf16x8 mA[2][2];                        // [jb][half] A operands of G2
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
             if (jb > tb) break;
             f32x16 d = zero16();
-#pragma unroll 4
+            // Operands of step s+1 are read before step s's MFMA issues.
+            const __bf16* arow = &sB[(jb * 32 + lo) * RS + 8 * hi];
+            const __bf16* brow = &sC[t_own * RS + 8 * hi];
+            bf16x8 av = *reinterpret_cast<const bf16x8*>(arow);
+            bf16x8 bv = *reinterpret_cast<const bf16x8*>(brow);
+#pragma unroll
             for (int s = 0; s < NP / 16; ++s) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sB[(jb * 32 + lo) * RS + 16 * s + 8 * hi]);
-                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sC[t_own * RS + 16 * s + 8 * hi]);
+                bf16x8 an = av, bn = bv;
+                if (s + 1 < NP / 16) {
+                    an = *reinterpret_cast<const bf16x8*>(arow + 16 * (s + 1));
+                    bn = *reinterpret_cast<const bf16x8*>(brow + 16 * (s + 1));
+                }
                 d = mfma_bf16(av, bv, d);
+                av = an;
+                bv = bn;
             }
             // M[t][j] = CB[t][j] exp(Lcum_t - Lcum_j), zero above the diagonal.
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = jb * 32 + acc_row(r, hi);
-                d[r] = (j <= t_own) ? d[r] * expf((float)(l_t - sL[j])) : 0.0f;
+                const float v = d[r];
+                d[r] = keep_if_le(v * exp2_diff(l_t, sL[hw][j]), j, t_own);
             }
             mA[jb][0] = pack8(d, 0);
             mA[jb][1] = pack8(d, 8);
         }
 
-        // ---- G3: y = C . R (state before this chunk), row scale, G2 --------
+        // ---- G3: y = C . R (state before this chunk), row scale, G2. The
+        // tile is stored as coalesced 4-byte writes (a wave covers two
+        // 128-byte row runs per store); a transposed tile stored as 16-byte
+        // writes scatters each store over 64 rows and measured 3x slower. ----
         f32x16 acc = zero16();
-        const __bf16* crow = &sC[t_own * RS];
+        {
+            // All of this lane's C row operands first (NT x 2 reads), then the MFMAs.
+            bf16x8 ca[NT][2];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const bf16x8 av = lds_pair4(crow, nt * 32 + 16 * half + 4 * hi);
-                acc = mfma_bf16(av, pack8(R[nt], 8 * half), acc);
-            }
+                for (int half = 0; half < 2; ++half)
+                    ca[nt][half] = *reinterpret_cast<const bf16x8*>(&sC[t_own * RS + nt * 32 + 16 * half + 8 * hi]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) acc = mfma_bf16(ca[nt][half], pack8(R[nt], 8 * half), acc);
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] *= sE[tb * 32 + acc_row(r, hi)];
-        const __bf16* xrow = &sXt[pp * RSJ];
+        for (int r = 0; r < 16; ++r) acc[r] *= sE[hw][tb * 32 + acc_row(r, hi)];
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
             if (jb > tb) break;
 #pragma unroll
-            for (int half = 0; half < 2; ++half)
-                acc = mfma_bf16(mA[jb][half], lds_pair4(xrow, jb * 32 + 16 * half + 4 * hi), acc);
+            for (int half = 0; half < 2; ++half) {
+                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&sXt[hw][pp * RSJ + jb * 32 + 16 * half + 8 * hi]);
+                acc = mfma_bf16(mA[jb][half], bv, acc);
+            }
         }
-        float* yh = b.y + seq * p.seq_y + h * p.s_y[1] + p0 * p.s_y[2];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = tb * 32 + acc_row(r, hi);
-            if (t < tlen && pp < pw) yh[(long long)(t0 + t) * p.s_y[0] + pp * p.s_y[2]] = acc[r];
-        }
+        y_prev = acc;
 
-        // ---- G4: R <- exp(L_end) R + B^T . dtXs ----------------------------
+        // ---- G4: R <- exp(L_end) R + B^T . dtXs --------------------------------
         const float a_c = expf((float)lend);
-        const __bf16* xsrow = &sXst[pp * RSJ];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            R[nt] *= a_c;
+        for (int nt = 0; nt < NT; ++nt) R[nt] *= a_c;
+        {
+            // K step outermost: the NT tiles' MFMAs are independent, so each
+            // step's reads are issued while the previous step's MFMAs run.
+            bf16x8 xs = *reinterpret_cast<const bf16x8*>(&sXst[hw][pp * RSJ + 8 * hi]);
+            bf16x8 bt[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) bt[nt] = *reinterpret_cast<const bf16x8*>(&sBt[(nt * 32 + lo) * RSJ + 8 * hi]);
 #pragma unroll
             for (int s = 0; s < HELIX_CS / 16; ++s) {
-                const bf16x8 av = *reinterpret_cast<const bf16x8*>(&sBt[(nt * 32 + lo) * RSJ + 16 * s + 8 * hi]);
-                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(&xsrow[16 * s + 8 * hi]);
-                R[nt] = mfma_bf16(av, bv, R[nt]);
+                bf16x8 xn = xs, bn[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) bn[nt] = bt[nt];
+                if (s + 1 < HELIX_CS / 16) {
+                    xn = *reinterpret_cast<const bf16x8*>(&sXst[hw][pp * RSJ + 16 * (s + 1) + 8 * hi]);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        bn[nt] = *reinterpret_cast<const bf16x8*>(&sBt[(nt * 32 + lo) * RSJ + 16 * (s + 1) + 8 * hi]);
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) R[nt] = mfma_bf16(bt[nt], xs, R[nt]);
+                xs = xn;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) bt[nt] = bn[nt];
             }
         }
         __syncthreads();
     }
+    {
+        const int tl0  = (p.chunk_base + c_end - 1) * HELIX_CS;
+        store_y_tile(y_prev, p, b, seq, h, tl0, head_ok ? min(HELIX_CS, p.n_tok - tl0) : 0, p0, pw, tb, pb, lo,
+                     hi);
+    }
 }
 
 #define HELIX_PASS_C_WALK(NP)                                                                   \
-    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_walk_bf16_n##NP(           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK_HPW(NP)) void helix_scan_walk_bf16_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \
         scan_walk_bf16_impl<NP>(p, b);                                                          \
     }

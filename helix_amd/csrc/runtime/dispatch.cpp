@@ -12,7 +12,8 @@
 //   Pass B  grid (ceil(n_pslab*16*np/256), n_head, n_seq) x 256 threads
 //   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
 //           decoded XCD-aware in the kernel); the walking variant runs one
-//           workgroup per (segment, head, P slab, seq) instead
+//           workgroup of 256 * HELIX_WALK_HPW(np) threads per (segment,
+//           block of that many heads of a group, P slab, seq) instead
 // The ragged-tail padding and the bf16 staging of B and C that the reference
 // runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
 // staging here, so there is nothing to launch before the group loop.
@@ -159,10 +160,15 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c) {
+            const unsigned hpg = (unsigned)(d->n_head / d->n_group);
+            const unsigned hpw = HELIX_WALK_HPW(tr.np);
+            const unsigned pairs = (hpg + hpw - 1) / hpw;
             const unsigned n_wg = tr.walk
-                ? (unsigned)params.n_seg * (unsigned)d->n_head * (unsigned)params.n_pslab * (unsigned)d->n_seq
+                ? (unsigned)params.n_seg * (unsigned)d->n_group * pairs * (unsigned)params.n_pslab *
+                      (unsigned)d->n_seq
                 : (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) * (unsigned)d->n_seq;
-            e = hipModuleLaunchKernel(fC, n_wg, 1, 1, HELIX_WG, 1, 1, 0, stream, args, nullptr);
+            const unsigned threads = tr.walk ? HELIX_WG * hpw : HELIX_WG;
+            e = hipModuleLaunchKernel(fC, n_wg, 1, 1, threads, 1, 1, 0, stream, args, nullptr);
         }
         if (e != hipSuccess) {
             (void)hipGetLastError();
