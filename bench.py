@@ -227,8 +227,8 @@ def main():
                 Variant("fp32", ctx, HELIX_BACKEND_SGMMA, tensors)]
     if args.variants:
         # Alternative kernel choices, timed interleaved in the same process.
-        variants.append(Variant("bf16-walk", ctx, HELIX_BACKEND_MPP, tensors,
-                                env={"HELIX_BF16_PASSC": "walk"}))
+        variants.append(Variant("bf16-tile", ctx, HELIX_BACKEND_MPP, tensors,
+                                env={"HELIX_BF16_PASSC": "tile"}))
 
     # Warm-up: W steps each, then alternate until the wall clock has run
     # warmup_ms (the reference's protocol against clock ramps).

@@ -162,6 +162,10 @@ void set_error(const helix_ctx* ctx, const std::string& msg) {
     t_last_error = msg;
 }
 
+namespace {
+bool prefer_walk(const helix_scan_desc& d);
+}  // namespace
+
 const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d) {
     (void)ctx;
     const int k = np_index(d.d_state);
@@ -170,12 +174,14 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
         if (f[0] == 's') return pick_traits(0, k);
     const bool want_bf16 = d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP;
     if (want_bf16 && d.multipass) {
-        // HELIX_BF16_PASSC=walk selects the chunk-walking Pass C (state in
-        // registers, no per-chunk scratch); the chunk-parallel one is the
-        // default while it is the faster of the two.
-        if (const char* v = std::getenv("HELIX_BF16_PASSC"))
+        // HELIX_BF16_PASSC=walk|tile overrides the choice between the
+        // chunk-walking Pass C (state in registers, no per-chunk scratch) and
+        // the chunk-parallel one.
+        if (const char* v = std::getenv("HELIX_BF16_PASSC")) {
             if (v[0] == 'w') return pick_traits(2, k);
-        return pick_traits(1, k);
+            if (v[0] == 't') return pick_traits(1, k);
+        }
+        return pick_traits(prefer_walk(d) ? 2 : 1, k);
     }
     return pick_traits(0, k);
 }
@@ -190,7 +196,11 @@ namespace {
 
 // Chunks per segment for a group of `cpg` chunks: enough segments that Pass A
 // has ~kTargetWgA workgroups, and no more (a longer walk keeps more of the
-// chunk recurrence in registers and shortens Pass B).
+// chunk recurrence in registers and shortens Pass B), up to kMaxSegLen (past
+// that the walks get too long to fill the chip: at config 4a, 64-chunk
+// segments took 1.03 ms and 16-chunk ones 0.95 ms).
+constexpr long kMaxSegLen = 16;
+
 int choose_seg_len(const helix_scan_desc& d, int cpg) {
     if (const char* v = std::getenv("HELIX_SEG_LEN")) {
         const long x = std::strtol(v, nullptr, 10);
@@ -199,8 +209,21 @@ int choose_seg_len(const helix_scan_desc& d, int cpg) {
     const long n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
     const long items = (long)d.n_seq * d.n_head * n_pslab;
     const long segs = std::max<long>(1, (kTargetWgA + items - 1) / items);
-    const long len = (cpg + segs - 1) / segs;
+    const long len = std::min<long>((cpg + segs - 1) / segs, kMaxSegLen);
     return (int)std::max<long>(1, std::min<long>(len, cpg));
+}
+
+// The bf16 path walks segments in Pass C (no per-chunk state in scratch)
+// when the plan gives full-length segments, where its lower traffic pays
+// for the longer per-workgroup chains; with short segments the
+// chunk-parallel Pass C is faster. Measured at config 2: 0.205 vs 0.209 ms;
+// config 4a: 0.936 vs 0.949 ms; config 3 (8-chunk segments): 0.111 vs
+// 0.102 ms. d_state 256 keeps the chunk-parallel kernel (one head per
+// walking workgroup there).
+bool prefer_walk(const helix_scan_desc& d) {
+    if (d.d_state > 128) return false;
+    const long n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
+    return choose_seg_len(d, (int)std::min<long>(n_chunks, 1 << 30)) >= kMaxSegLen;
 }
 
 void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int np, int cpg, MultipassPlan* pl) {

@@ -174,7 +174,13 @@ def test_backend_selection(host):
     # path's Pass C up to d_state 128.
     assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
-    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
+    # The bf16 path walks segments in Pass C when the plan gives full-length
+    # segments (d_state <= 128), and runs chunk-parallel otherwise.
+    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
+    assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
+            == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)")
+    with env(HELIX_BF16_PASSC="tile"):
+        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C, pass A bf16x6 (d_state<=256)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
@@ -185,7 +191,11 @@ def test_backend_selection(host):
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x6sbf_n128", b"helix_state_scan_f32", b"helix_chunk_out_bf16_n128")
+        b"helix_chunk_state_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk_bf16_n128")
+    with env(HELIX_BF16_PASSC="tile"):
+        k = host.plan_info(mp(shape))
+        assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
+            b"helix_chunk_state_x6sbf_n128", b"helix_state_scan_f32", b"helix_chunk_out_bf16_n128")
     k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n128", b"helix_chunk_out_x6_n128")
     k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
@@ -199,9 +209,9 @@ def test_backend_selection(host):
     # HELIX_X6=0 selects the fp32-MFMA kernels.
     with env(HELIX_X6="0"):
         assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
-        with env(HELIX_BF16_PASSC="walk"):
-            assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk (d_state<=128)"
+        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk (d_state<=128)"
+        with env(HELIX_BF16_PASSC="tile"):
+            assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
     d = mp(shape)
     d.multipass = False
     assert host.backend_desc(d) == "declined (shape unsupported)"
@@ -240,7 +250,14 @@ def _plan_invariants(host, name, backend):
     assert info.np == (64 if N <= 64 else 128 if N <= 128 else 256)
     es = 2 if backend == HELIX_BACKEND_MPP else 4
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
-    walk = backend == HELIX_BACKEND_MPP and os.environ.get("HELIX_BF16_PASSC") == "walk"
+    # The walking Pass C keeps the chunk-local states in registers, so its
+    # plan holds no s_local region; it runs only on the bf16 path.
+    walk = b"walk" in info.kernel_c
+    assert not walk or backend == HELIX_BACKEND_MPP
+    if os.environ.get("HELIX_BF16_PASSC") == "walk" and backend == HELIX_BACKEND_MPP and N <= 128:
+        assert walk
+    if os.environ.get("HELIX_BF16_PASSC") == "tile":
+        assert not walk
     want_sl = state * info.chunks_per_group * es if (info.seg_len > 1 and not walk) else 0
     assert info.s_local_bytes == want_sl
     assert info.s_seg_bytes == state * info.segs_per_group * 4
