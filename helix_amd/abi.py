@@ -47,6 +47,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("kernel_a", ctypes.c_char_p),
         ("kernel_b", ctypes.c_char_p),
         ("kernel_c", ctypes.c_char_p),
+        ("kernel_1pass", ctypes.c_char_p),
     ]
 
 

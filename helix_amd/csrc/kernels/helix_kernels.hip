@@ -8,3 +8,4 @@
 #include "pass_c_bf16.hip"
 #include "pass_c_x6.hip"
 #include "pass_c_walk.hip"
+#include "pass_single.hip"

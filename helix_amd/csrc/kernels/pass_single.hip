@@ -1,0 +1,305 @@
+// pass_single.hip -- the single-pass scan (multipass = false): one launch, no
+// scratch.
+//
+// Reference counterpart: helix_scan_sgmma_f32 (src/kernels/
+// helix_scan_sgmma.metal:32-249). One workgroup per (P slab, head, seq) walks
+// every chunk of the sequence in order:
+//   y_t = sum_{j<=t} (C_t . B_j) exp(Lcum_t - Lcum_j) dt_j x_j     (G1, G2)
+//       + exp(Lcum_t) C_t . S                                     (G3)
+//   S  <- exp(L_end) S + sum_j B_j^T exp(L_end - Lcum_j) dt_j x_j   (G4)
+// The reference parks S in the caller's s1 buffer between chunks (a device
+// round trip per chunk). Here the state stays in the workgroup's MFMA
+// registers for the whole sequence: s0 is read once at the start and s1
+// written once at the end.
+//
+// MI355X layout: four waves on v_mfma_f32_16x16x4_f32, fp32 throughout.
+// Wave w owns the 16 channels p = 16w .. 16w+15 of the slab and every state
+// index n, so the y tile it produces (all 64 tokens of its channels) and the
+// state it advances are both its own: G3 takes its B operand straight from
+// the state registers, with no cross-wave reduction.
+//   16x16x4 layouts: A[i][k]: lane holds A[lane%16][lane/16];
+//                    B[k][j]: lane holds B[lane/16][lane%16];
+//                    D[i][j]: lane, reg r holds D[4*(lane/16) + r][lane%16].
+// The state tile nt is R[n][p] for n = 16 nt .. 16 nt + 15 (M = n, N = p).
+// K order: G1 and G3 step s of a 16-wide K block takes k = 4*(lane/16) + s,
+// so the A operand's four k of a block are one 16-byte LDS read and G3's B
+// operand at step s is state register s; G2 and G4 take token j = 4 s +
+// lane/16. Both operands of a product use the same order.
+//
+// LDS: C and B rows (fp32, 64 x (np+4)), dtX (64 x 80), the chunk's Lcum in
+// fp64 and two 64-vectors: 151 KiB at d_state 256. M reuses B's rows once
+// G1 and G4 are done with them.
+#include "helix_common.h"
+
+#include "pass_c_stage.h"
+
+HELIX_DEV f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+HELIX_DEV f32x4 zero4() {
+    f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    return z;
+}
+
+// One chunk's global inputs for this thread, loaded for chunk c+1 while chunk
+// c runs: dt of token `lane`, x of tokens 16 w + i at channel `lane`, and the
+// C and B rows wave + 4 i at columns lane + 64 m. Every address is clamped in
+// bounds; the masks are applied when the registers are staged into LDS.
+template <int NP>
+struct StageS {
+    float dtraw;
+    float x[16];
+    float c[16][NP / 64];
+    float b[16][NP / 64];
+};
+
+template <int NP>
+__device__ __forceinline__ void load_stage_s(StageS<NP>& st, const HelixScanParams& p,
+                                             const HelixScanBuffers& b, const float* __restrict__ dt_h,
+                                             const float* __restrict__ x_h, int seq, int g, int t0,
+                                             int tlen, int pw, int lane, int wave) {
+    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const helix_rsrc rx =
+        make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    const int xc = min(lane, pw - 1) * sx2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int jr = min(16 * wave + i, tlen - 1);
+        st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
+    }
+    load_cb_rows<NP>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
+}
+
+// G1 tile idx (0..9) of the causal 4 x 4 grid of 16 x 16 tiles, row-major
+// over the lower triangle: (0,0) (1,0) (1,1) (2,0) ... (3,3).
+HELIX_DEV int tri_tb(int idx) { return (idx >= 1) + (idx >= 3) + (idx >= 6); }
+HELIX_DEV int tri_jb(int idx) {
+    const int tb = tri_tb(idx);
+    return idx - tb * (tb + 1) / 2;
+}
+
+template <int NP>
+__device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int NT  = NP / 16;           // 16-row state tiles (all of them live in every wave)
+    constexpr int RSC = NP + 4;            // C and B rows
+    constexpr int RSM = HELIX_CS + 4;      // M rows, in B's region after G4
+    constexpr int RSX = HELIX_HD + 16;     // dtX rows
+    static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
+    __shared__ __attribute__((aligned(16))) float sC[HELIX_CS * RSC];
+    __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSC];
+    __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * RSX];
+    __shared__ double sL[HELIX_CS];        // Lcum_t (fp64)
+    __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
+    __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
+    float* const sM = sB;
+
+    const int lane = threadIdx.x & 63, wave = wave_uniform();
+    const int l16 = lane & 15, g4 = lane >> 4;
+
+    // 1-D grid, slab then head fastest in the logical order, so the heads of
+    // one B/C group (consecutive heads) share an XCD's L2.
+    const unsigned total = (unsigned)p.n_seq * (unsigned)p.n_head * (unsigned)p.n_pslab;
+    const unsigned wid = xcd_logical_id(blockIdx.x, total);
+    const int slab = (int)(wid % (unsigned)p.n_pslab);
+    const int h    = (int)((wid / (unsigned)p.n_pslab) % (unsigned)p.n_head);
+    const int seq  = (int)(wid / ((unsigned)p.n_pslab * (unsigned)p.n_head));
+    const int g  = h / p.heads_per_group;
+    const int N  = p.d_state;
+    const int p0 = slab * HELIX_HD;
+    const int pw = min(HELIX_HD, p.head_dim - p0);
+    const int pc = 16 * wave + l16;       // this lane's channel in the slab (result column)
+
+    const float A_h = b.A[(long long)h * p.s_a];
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + (long long)p0 * p.s_x[2];
+
+    // State entering the sequence, s0[ids[seq]] in the caller's [P][N] rows
+    // (s_s[1] == d_state): register r of tile nt holds n = 16 nt + 4 g4 + r,
+    // p = pc. Channels past the slab read 0 through the range check; n past
+    // d_state is masked (it would read the next row).
+    const int src = p.has_ids ? b.ids[seq] : seq;
+    f32x4 R[NT];
+    {
+        const helix_rsrc rs = make_rsrc(b.s0 + src * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
+                                        (unsigned)(pw * N) * 4u);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int n = 16 * nt + 4 * g4 + r;
+                R[nt][r] = keep_if_lt(buf_f32(rs, (pc * N + n) * 4, 0), n, N);
+            }
+    }
+
+    const int n_ch = (p.n_tok + HELIX_CS - 1) / HELIX_CS;
+    const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
+    StageS<NP> st;
+    load_stage_s<NP>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
+
+    for (int c = 0; c < n_ch; ++c) {
+        const int t0   = c * HELIX_CS;
+        const int tlen = min(HELIX_CS, p.n_tok - t0);
+
+        // ---- chunk preamble and staging ------------------------------------
+        // dt = 0 past tlen, so Lcum stays at Lcum[tlen-1] there and dtX rows
+        // past tlen are zero.
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lend = bcast(lcum, 63);
+        if (wave == 0) {
+            sL[lane]  = lcum;
+            sCs[lane] = exp_diff(lend, lcum);
+            sE[lane]  = expf((float)lcum);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int j = 16 * wave + i;
+            sX[j * RSX + lane] = keep_if_lt(bcast(dtv, j) * st.x[i], lane, pw);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int j = wave + 4 * i;
+#pragma unroll
+            for (int m = 0; m < NP / 64; ++m) {
+                const int n = lane + 64 * m;
+                sC[j * RSC + n] = keep_if_lt2(st.c[i][m], j, tlen, n, N);
+                sB[j * RSC + n] = keep_if_lt2(st.b[i][m], j, tlen, n, N);
+            }
+        }
+        __syncthreads();
+
+        // The next chunk's inputs travel while this one runs on the MFMA pipe.
+        if (c + 1 < n_ch)
+            load_stage_s<NP>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS, min(HELIX_CS, p.n_tok - t0 - HELIX_CS),
+                             pw, lane, wave);
+
+        // B operands of G2 (dtX) and G4 (dtX scaled by exp(L_end - Lcum_j)).
+        float xb[16], xs[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int j = 4 * s + g4;
+            xb[s] = sX[j * RSX + pc];
+            xs[s] = xb[s] * sCs[j];
+        }
+
+        // ---- G1: M = tril(C B^T) . exp(Lcum_t - Lcum_j), tiles wave + 4 q ----
+        f32x4 mt[3];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            mt[q] = zero4();
+            const int idx = wave + 4 * q;
+            if (idx < 10) {
+                const int tb = tri_tb(idx), jb = tri_jb(idx);
+                f32x4 acc = zero4();
+#pragma unroll 4
+                for (int kb = 0; kb < NP / 16; ++kb) {
+                    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * kb + 4 * g4]);
+                    const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sB[(16 * jb + l16) * RSC + 16 * kb + 4 * g4]);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc = mfma16(a4[s], b4[s], acc);
+                }
+                const int j = 16 * jb + l16;
+                const double lj = sL[j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tb + 4 * g4 + r;
+                    // j > t: exp of a positive difference may overflow; the
+                    // bitwise mask clears the product whatever it is.
+                    mt[q][r] = keep_if_le(acc[r] * exp_diff(sL[t], lj), j, t);
+                }
+            }
+        }
+
+        // ---- G3: y = exp(Lcum_t) . (C S), S from this wave's registers ------
+        f32x4 ya[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) ya[tb] = zero4();
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * nt + 4 * g4]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) ya[tb] = mfma16(a4[s], R[nt][s], ya[tb]);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ya[tb][r] *= sE[16 * tb + 4 * g4 + r];
+
+        // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x) -------------
+        const float a_c = expf((float)lend);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) R[nt] *= a_c;
+#pragma unroll 4
+        for (int s = 0; s < 16; ++s) {
+            const int j = 4 * s + g4;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) R[nt] = mfma16(sB[j * RSC + 16 * nt + l16], xs[s], R[nt]);
+        }
+        __syncthreads();   // every wave is done with the B rows: M takes them over
+
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+            const int idx = wave + 4 * q;
+            if (idx < 10) {
+                const int tb = tri_tb(idx), jb = tri_jb(idx);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sM[(16 * tb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
+            }
+        }
+        __syncthreads();
+
+        // ---- G2: y += M dtX over the causal K range of each t block ---------
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+            for (int s = 0; s < 4 * (tb + 1); ++s)
+                ya[tb] = mfma16(sM[(16 * tb + l16) * RSM + 4 * s + g4], xb[s], ya[tb]);
+        }
+
+        // ---- y rows t < tlen, channels < pw ---------------------------------
+        {
+            const unsigned bytes = ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u;
+            const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
+                                                (long long)p0 * p.s_y[2],
+                                            bytes);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tb + 4 * g4 + r;
+                    const float v = ya[tb][r];
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        as_u32(v), ry, store_off_if_lt((t * sy0 + pc * sy2) * 4, t, tlen, pc, pw), 0, 0);
+                }
+        }
+        __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX
+    }
+
+    // Final state to s1[seq], same register layout as the s0 read.
+    const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * N, (unsigned)(pw * N) * 4u);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = 16 * nt + 4 * g4 + r;
+            const float v = R[nt][r];
+            __builtin_amdgcn_raw_buffer_store_b32(as_u32(v), ro, store_off_if_lt((pc * N + n) * 4, n, N, pc, pw),
+                                                  0, 0);
+        }
+}
+
+#define HELIX_SCAN_1PASS(NP)                                                                    \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_f32_n##NP(           \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_1pass_impl<NP>(p, b);                                                              \
+    }
+
+HELIX_SCAN_1PASS(64)
+HELIX_SCAN_1PASS(128)
+HELIX_SCAN_1PASS(256)

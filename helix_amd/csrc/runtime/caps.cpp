@@ -60,6 +60,20 @@ constexpr HelixMatmulTraits kBf16WalkTraits[] = {
      "v_mfma_f32_32x32x2_f32", "v_mfma_f32_32x32x16_bf16", 256, true},
 };
 
+// The single-pass path (multipass = false, the descriptor default; reference
+// helix_scan_sgmma_f32): one launch per encode, one workgroup per (seq, head,
+// P slab) walking every chunk with the state in registers, fp32 MFMA
+// throughout, no scratch. AUTO and SGMMA both land here (the reference's MPP
+// traits exist only for multipass, caps.mm:66).
+constexpr HelixMatmulTraits kSingleTraits[] = {
+    {HELIX_BACKEND_SGMMA, "mfma fp32, single pass (d_state<=64)", nullptr, nullptr, nullptr, false,
+     "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 64, false, "helix_scan_1pass_f32_n64"},
+    {HELIX_BACKEND_SGMMA, "mfma fp32, single pass (d_state<=128)", nullptr, nullptr, nullptr, false,
+     "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 128, false, "helix_scan_1pass_f32_n128"},
+    {HELIX_BACKEND_SGMMA, "mfma fp32, single pass (d_state<=256)", nullptr, nullptr, nullptr, false,
+     "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 256, false, "helix_scan_1pass_f32_n256"},
+};
+
 // bf16x6 kernels: GEMMs on bf16 MFMA over operands split into three bf16
 // parts, fp32 accuracy at 16x the fp32 matrix issue rate. Pass A uses them on
 // every path (pass_a_x6.hip) and the fp32 path's Pass C for d_state <= 128
@@ -121,6 +135,7 @@ const char* const kKernelNames[] = {
     "helix_chunk_out_bf16_n64",   "helix_chunk_out_bf16_n128",  "helix_chunk_out_bf16_n256",
     "helix_chunk_state_agg_n64",  "helix_chunk_state_agg_n128", "helix_chunk_state_agg_n256",
     "helix_scan_walk_bf16_n64",   "helix_scan_walk_bf16_n128",  "helix_scan_walk_bf16_n256",
+    "helix_scan_1pass_f32_n64",   "helix_scan_1pass_f32_n128",  "helix_scan_1pass_f32_n256",
 };
 
 int np_index(int d_state) {
@@ -169,6 +184,7 @@ bool prefer_walk(const helix_scan_desc& d);
 const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d) {
     (void)ctx;
     const int k = np_index(d.d_state);
+    if (!d.multipass) return kSingleTraits[k];
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
         if (f[0] == 's') return pick_traits(0, k);
@@ -375,9 +391,9 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
     if (d->s_b[2] != 1 || d->s_c[2] != 1 || d->s_s[2] != 1) return false;
     if (d->s_s[1] != d->d_state) return false;
     if (d->chunk != 0 && d->chunk != HELIX_CS) return false;
-    // Only the three-pass path is built; a single-pass request is declined so
-    // the caller keeps its own kernel (helix.h: false => fall back).
-    if (!d->multipass) return false;
+    // An explicit bf16 (MPP) request must be serviceable, and the bf16 Pass C
+    // exists only in the multipass decomposition (reference caps.mm:66,145-147).
+    if (!d->multipass && d->backend == HELIX_BACKEND_MPP) return false;
     if (d->backend == HELIX_BACKEND_REF) return false;
     HelixScanParams unused;
     return helix::rt::build_params(*d, &unused, nullptr);

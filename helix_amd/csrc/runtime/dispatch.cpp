@@ -7,7 +7,10 @@
 // enqueued. Stream order sequences the passes; there are no barriers to
 // insert.
 //
-// Per super-chunk group, in stream order:
+// multipass = false: one launch of the single-pass kernel, grid
+// (n_seq * n_head * n_pslab) x 256 threads, no scratch.
+//
+// Otherwise, per super-chunk group, in stream order:
 //   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
 //   Pass B  grid (ceil(n_pslab*16*np/256), n_head, n_seq) x 256 threads
 //   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
@@ -59,6 +62,56 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     params.has_ids = ids.buf ? 1 : 0;
 
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    auto fn = [&](const char* name) -> hipFunction_t {
+        if (!name) return nullptr;
+        auto it = ctx->kernels.find(name);
+        return it == ctx->kernels.end() ? nullptr : it->second;
+    };
+
+    // Single pass (reference dispatch.mm:122-138): one launch, one workgroup
+    // per (seq, head, P slab), the state carried in registers; no scratch.
+    if (!d->multipass) {
+        hipFunction_t f1 = fn(tr.k_single);
+        if (!f1) {
+            set_error(ctx, "kernel not resolved in code object");
+            return HELIX_ERR_PIPELINE;
+        }
+        const long long n_wg = (long long)d->n_seq * d->n_head * params.n_pslab;
+        if (n_wg > 0xffffffffLL) {
+            set_error(ctx, "launch grid exceeds 2^32 workgroups (n_seq * n_head * n_pslab)");
+            return HELIX_ERR_INVALID_ARG;
+        }
+        params.np = tr.np;
+        HelixScanBuffers bufs;
+        std::memset(&bufs, 0, sizeof(bufs));
+        bufs.s0  = static_cast<const float*>(dptr(s0));
+        bufs.x   = static_cast<const float*>(dptr(x));
+        bufs.dt  = static_cast<const float*>(dptr(dt));
+        bufs.A   = static_cast<const float*>(dptr(A));
+        bufs.B   = static_cast<const float*>(dptr(B));
+        bufs.C   = static_cast<const float*>(dptr(C));
+        bufs.ids = static_cast<const int*>(dptr(ids));
+        bufs.y   = static_cast<float*>(dptr(y));
+        bufs.s1  = static_cast<float*>(dptr(s1));
+        int prev = -1;
+        (void)hipGetDevice(&prev);
+        if (prev != ctx->device && hipSetDevice(ctx->device) != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(ctx, "hipSetDevice failed");
+            return HELIX_ERR_NO_DEVICE;
+        }
+        void* args[] = {&params, &bufs};
+        const hipError_t e = hipModuleLaunchKernel(f1, (unsigned)n_wg, 1, 1, HELIX_WG, 1, 1, 0, stream, args,
+                                                   nullptr);
+        if (prev >= 0 && prev != ctx->device) (void)hipSetDevice(prev);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error(ctx, std::string("kernel launch failed: ") + hipGetErrorString(e));
+            return HELIX_ERR_PIPELINE;
+        }
+        return HELIX_OK;
+    }
+
     const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(*d, tr);
     if (plan.n_chunks <= 0) {
         set_error(ctx, "empty problem");
@@ -85,10 +138,6 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         }
     }
 
-    auto fn = [&](const char* name) -> hipFunction_t {
-        auto it = ctx->kernels.find(name);
-        return it == ctx->kernels.end() ? nullptr : it->second;
-    };
     hipFunction_t fA = fn(tr.k_chunk_state), fB = fn(tr.k_state_scan), fC = fn(tr.k_chunk_out);
     if (!fA || !fB || !fC) {
         set_error(ctx, "kernel not resolved in code object");
@@ -207,8 +256,21 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     if (!ctx || !d || !out) return HELIX_ERR_INVALID_ARG;
     if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
-    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr);
     std::memset(out, 0, sizeof(*out));
+    if (!d->multipass) {
+        out->n_chunks = (d->n_tok + HELIX_CS - 1) / HELIX_CS;
+        out->chunks_per_group = out->n_chunks;
+        out->n_groups = 1;
+        out->seg_len = out->n_chunks;
+        out->segs_per_group = 1;
+        out->hblk = 1;
+        out->n_hblk = d->n_head / d->n_group;
+        out->launches = 1;
+        out->np = tr.np;
+        out->kernel_1pass = tr.k_single;
+        return HELIX_OK;
+    }
+    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr);
     out->n_chunks = pl.n_chunks;
     out->chunks_per_group = pl.chunks_per_group;
     out->n_groups = pl.n_groups;

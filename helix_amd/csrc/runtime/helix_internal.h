@@ -41,6 +41,10 @@ struct HelixMatmulTraits {
     // (one workgroup per segment x head x P slab); Pass A then stores only the
     // segment aggregates and there is no per-chunk state in scratch.
     bool          walk;
+    // The single-pass kernel (multipass = false; reference k_single,
+    // caps.mm:18-25). Set only in the single-pass trait set, where the three
+    // pass names are null.
+    const char*   k_single;
 };
 
 namespace helix::rt {

@@ -19,7 +19,8 @@ extern "C" {
  * HELIX_ERR_NO_DEVICE without touching HIP. Free with helix_ctx_free. */
 helix_status helix_ctx_create_host(helix_ctx** out);
 
-/* The multipass plan helix_scan_encode would use for `d`. */
+/* The plan helix_scan_encode would use for `d`. With multipass = false it is
+ * one launch of kernel_1pass: one group, no scratch, kernel_a/b/c NULL. */
 typedef struct {
     int32_t  n_chunks;          /* ceil(n_tok / 64)                              */
     int32_t  chunks_per_group;  /* chunks per super-chunk group (scratch bound)  */
@@ -37,6 +38,7 @@ typedef struct {
     const char* kernel_a;       /* code-object names of the Pass A, B and C      */
     const char* kernel_b;       /* kernels (static strings)                      */
     const char* kernel_c;
+    const char* kernel_1pass;   /* the single-pass kernel, else NULL             */
 } helix_plan_info;
 
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */

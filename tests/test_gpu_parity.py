@@ -9,8 +9,8 @@ Mirrors the reference's tests/test_metal_parity.mm:
 Both MI355X paths are exercised explicitly (SGMMA -> fp32 MFMA Pass C, MPP ->
 bf16 Pass C) because AUTO resolves to bf16 for every multipass shape here, and
 each with its default bf16x6 split-product kernels and with the fp32-MFMA
-ones (HELIX_X6=0).
-The single-pass modes are absent: this build declines multipass=false.
+ones (HELIX_X6=0). The reference's single-pass modes (multipass=false, AUTO
+backend: the fp32 single-pass kernel) run in SHORT and LONG memory.
 
 Then the BASELINE.json configurations at full size, gated on
 max|dy|/max|y| <= 1e-4 (fp32) / 2e-2 (bf16) and likewise for s1, with the CPU
@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 
 from oracle import pyoracle as po
-from helix_amd.desc import HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA
+from helix_amd.desc import HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA
 from baseline_configs import CONFIGS
 from gpu_harness import (BF16_ABS, BF16_GATE, BF16_REL, F32_ABS, F32_GATE, F32_REL, env, run)
 
@@ -56,24 +56,26 @@ SHAPES = [
 ]
 
 MODES = [
-    # (label, backend, scratch_mb, memory, extra environment)
-    ("fp32", HELIX_BACKEND_SGMMA, None, "short", {}),
-    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", {}),
-    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}),
-    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {}),
-    ("bf16", HELIX_BACKEND_MPP, None, "short", {}),
-    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}),
-    ("bf16/long", HELIX_BACKEND_MPP, None, "long", {}),
-    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long", {}),
-    ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}),
-    ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}),
-    ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}),
+    # (label, backend, scratch_mb, memory, extra environment, multipass)
+    ("1pass", HELIX_BACKEND_AUTO, None, "short", {}, False),
+    ("1pass/long", HELIX_BACKEND_AUTO, None, "long", {}, False),
+    ("fp32", HELIX_BACKEND_SGMMA, None, "short", {}, True),
+    ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", {}, True),
+    ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}, True),
+    ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {}, True),
+    ("bf16", HELIX_BACKEND_MPP, None, "short", {}, True),
+    ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}, True),
+    ("bf16/long", HELIX_BACKEND_MPP, None, "long", {}, True),
+    ("bf16/sm/long", HELIX_BACKEND_MPP, 1, "long", {}, True),
+    ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}, True),
+    ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}, True),
+    ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}, True),
     # fp32-MFMA kernels instead of bf16x6 split products.
-    ("fp32/mma/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_X6": "0"}),
-    ("fp32/mma", HELIX_BACKEND_SGMMA, None, "short", {"HELIX_X6": "0"}),
-    ("bf16/mma/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_X6": "0"}),
+    ("fp32/mma/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_X6": "0"}, True),
+    ("fp32/mma", HELIX_BACKEND_SGMMA, None, "short", {"HELIX_X6": "0"}, True),
+    ("bf16/mma/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_X6": "0"}, True),
     ("bf16walk/mma/long", HELIX_BACKEND_MPP, None, "long",
-     {"HELIX_X6": "0", "HELIX_BF16_PASSC": "walk"}),
+     {"HELIX_X6": "0", "HELIX_BF16_PASSC": "walk"}, True),
 ]
 
 
@@ -88,10 +90,10 @@ def _reference(shape, memory):
 @pytest.mark.parametrize("mode", MODES, ids=[m[0] for m in MODES])
 @pytest.mark.parametrize("shape", SHAPES, ids=[s[-1] for s in SHAPES])
 def test_shape_matrix(gpu, shape, mode):
-    label, backend, scratch_mb, memory, extra = mode
+    label, backend, scratch_mb, memory, extra, multipass = mode
     p, y_ref, s_ref = _reference(shape, memory)
     d = p.d.copy()
-    d.multipass = True
+    d.multipass = multipass
     d.backend = backend
     with env(HELIX_SCRATCH_MB=scratch_mb, **extra):
         assert gpu.supported(d), gpu.backend_desc(d)
@@ -127,6 +129,7 @@ def _baseline(name, memory):
 CASES = [(n, path, mem) for n, c in CONFIGS.items() for path in c.paths for mem in ("dist", "long")]
 CASES += [(n, "bf16walk", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
 CASES += [(n, path + "/mma", "long") for n, c in CONFIGS.items() for path in c.paths]
+CASES += [(n, "1pass", mem) for n in CONFIGS for mem in ("dist", "long")]
 
 
 @pytest.mark.parametrize("name,path,memory", CASES, ids=[f"{n}-{p}-{m}" for n, p, m in CASES])
@@ -134,8 +137,9 @@ def test_baseline_config(gpu, name, path, memory):
     c = CONFIGS[name]
     p, y_ref, s_ref = _baseline(name, memory)
     d = p.d.copy()
-    d.multipass = True
-    d.backend = HELIX_BACKEND_MPP if path.startswith("bf16") else HELIX_BACKEND_SGMMA
+    d.multipass = path != "1pass"
+    d.backend = (HELIX_BACKEND_MPP if path.startswith("bf16")
+                 else HELIX_BACKEND_AUTO if path == "1pass" else HELIX_BACKEND_SGMMA)
     with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None,
              HELIX_X6="0" if path.endswith("/mma") else None):
         assert gpu.supported(d)

@@ -133,7 +133,8 @@ def _declined(host, mutate):
     ("strided s state", lambda d: d.s_s.__setitem__(2, 2)),
     ("s rows not d_state apart", lambda d: d.s_s.__setitem__(1, 256)),
     ("chunk 32", lambda d: setattr(d, "chunk", 32)),
-    ("single pass", lambda d: setattr(d, "multipass", False)),
+    ("single pass with explicit MPP",
+     lambda d: (setattr(d, "multipass", False), setattr(d, "backend", HELIX_BACKEND_MPP))),
     ("REF backend", lambda d: setattr(d, "backend", HELIX_BACKEND_REF)),
     ("grid z overflow", lambda d: setattr(d, "n_seq", 70000)),
 ])
@@ -212,9 +213,25 @@ def test_backend_selection(host):
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk (d_state<=128)"
         with env(HELIX_BF16_PASSC="tile"):
             assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
+    # multipass=false (the descriptor default) runs the fp32 single-pass
+    # kernel under AUTO and SGMMA; an explicit MPP request is declined there
+    # (reference caps.mm:66,145-147).
     d = mp(shape)
     d.multipass = False
+    assert host.backend_desc(d) == "mfma fp32, single pass (d_state<=128)"
+    assert host.select_backend(d) == HELIX_BACKEND_SGMMA
+    d.backend = HELIX_BACKEND_SGMMA
+    assert host.backend_desc(d) == "mfma fp32, single pass (d_state<=128)"
+    d.backend = HELIX_BACKEND_MPP
     assert host.backend_desc(d) == "declined (shape unsupported)"
+    for n, want in ((64, 64), (40, 64), (96, 128), (256, 256)):
+        d = mp((100, 1, 2, 64, n, 1))
+        d.multipass = False
+        k = host.plan_info(d)
+        assert (k.np, k.launches, k.total_bytes, k.n_groups) == (want, 1, 0, 1)
+        assert k.kernel_1pass == b"helix_scan_1pass_f32_n%d" % want
+        assert k.kernel_a is None and k.kernel_b is None and k.kernel_c is None
+    assert host.plan_info(mp(shape)).kernel_1pass is None
     with env(HELIX_FORCE_BACKEND="sgmma"):
         assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_SGMMA
 
