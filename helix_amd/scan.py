@@ -83,13 +83,16 @@ def make_desc(x: torch.Tensor, dt: torch.Tensor, B: torch.Tensor, C: torch.Tenso
 def ssd_scan(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
              s0: torch.Tensor | None = None, ids: torch.Tensor | None = None, *,
              backend: str = "auto", dt_min: float = 0.0, dt_max: float = math.inf,
+             multipass: bool = True,
              y: torch.Tensor | None = None, s1: torch.Tensor | None = None,
              scratch: torch.Tensor | None = None, stream: torch.cuda.Stream | None = None):
     """Chunked SSD prefill scan on the MI355X kernels. Returns (y, s1).
 
     x [S,L,H,P], dt [S,L,H] (pre-softplus), A [H], B/C [S,L,G,N], s0 [S,H,P,N]
     (zeros when None), ids int32 [S] (source state row per sequence). All fp32
-    on one gfx950 device. Raises HelixError when the shape is declined.
+    on one gfx950 device. multipass=False runs the single-pass kernel (fp32,
+    no scratch; backend "bf16" is then declined). Raises HelixError when the
+    shape is declined.
     """
     dev = x.device
     if dev.type != "cuda":
@@ -107,7 +110,8 @@ def ssd_scan(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: torch.Tensor
         s1 = torch.empty((S, H, P, N), dtype=torch.float32, device=dev)
     if ids is not None and (ids.dtype != torch.int32 or not ids.is_contiguous()):
         raise ValueError("ids must be a contiguous int32 tensor")
-    d = make_desc(x, dt, B, C, s0, y, A, backend=backend, dt_min=dt_min, dt_max=dt_max)
+    d = make_desc(x, dt, B, C, s0, y, A, backend=backend, multipass=multipass, dt_min=dt_min,
+                  dt_max=dt_max)
     if tuple(s1.stride()) != tuple(s0.stride()):
         raise ValueError("s0 and s1 must share strides")
     ctx = context(dev.index if dev.index is not None else torch.cuda.current_device())

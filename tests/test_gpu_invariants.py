@@ -1,0 +1,320 @@
+"""GPU tests beyond the shape matrix: invariants at realistic sizes and the
+boundary cases a real caller produces, on every path (multipass fp32,
+multipass bf16 with the chunk-walking and the chunk-parallel Pass C, single
+pass).
+
+* State splitting, the property that pins the carried state (Pass B, the
+  cross-group carry, the single-pass register state):
+  scan(L1 + L2) == scan(L2, s0 = scan(L1).s1), split at ragged and at chunk
+  boundaries, in LONG memory where the carry is numerically visible.
+* ids: a permutation of the source state rows (reference
+  src/kernels/helix_scan_multipass.metal:178-185, helix_scan_sgmma.metal:82-83).
+* Strided views: the element strides ggml's nb[] produce (padded token rows,
+  group, head and sequence strides, A with a stride), against the oracle fed
+  the same padded buffers.
+* Determinism: two encodes of the same inputs are bitwise equal.
+* Errors found before anything is enqueued leave the outputs untouched
+  (reference dispatch.mm:55-153); encode_into is the same call.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pyoracle as po
+from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA,
+                            HELIX_ERR_INVALID_ARG, HELIX_ERR_SCRATCH_TOO_SMALL,
+                            HELIX_ERR_UNSUPPORTED_SHAPE, HELIX_OK, HELIX_TENSOR_NULL, HelixTensor,
+                            desc_init)
+from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, T, env, run, upload
+
+pytestmark = pytest.mark.gpu
+
+# (label, backend, multipass, environment)
+PATHS = [
+    ("fp32", HELIX_BACKEND_SGMMA, True, {}),
+    ("bf16", HELIX_BACKEND_MPP, True, {}),
+    ("bf16tile", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "tile"}),
+    ("bf16walk", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk"}),
+    ("1pass", HELIX_BACKEND_AUTO, False, {}),
+]
+PATH_IDS = [p[0] for p in PATHS]
+
+
+def _gate(label):
+    return BF16_GATE if label.startswith("bf16") else F32_GATE
+
+
+def _desc(p, backend, multipass):
+    d = p.d.copy()
+    d.backend = backend
+    d.multipass = multipass
+    return d
+
+
+def _sub(p: po.Problem, t0: int, t1: int, s0=None) -> po.Problem:
+    """Tokens [t0, t1) of a dense Problem as a Problem of its own."""
+    L, S, H, P, N, G = p.shape
+    d = desc_init(t1 - t0, S, H, P, N, G)
+    d.dt_min, d.dt_max = p.d.dt_min, p.d.dt_max
+    cut = lambda a: np.ascontiguousarray(a[:, t0:t1])
+    return po.Problem(d, p.s0.copy() if s0 is None else s0, cut(p.x), cut(p.dt), p.A.copy(),
+                      cut(p.B), cut(p.C), p.ids)
+
+
+def _rel(a, b):
+    return po.max_rel_err(a, b)
+
+
+# ---------------------------------------------------------------------------
+# State splitting
+# ---------------------------------------------------------------------------
+
+SPLIT_SHAPE = (2048, 2, 8, 64, 128, 2)
+
+
+@pytest.fixture(scope="module")
+def split_problem():
+    p = po.problem_harness(*SPLIT_SHAPE, 31337, "long")
+    y, s1 = po.scan(p, threads=0)
+    return p, y, s1
+
+
+@pytest.mark.parametrize("split", [64, 1000, 1984])
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_state_splitting(gpu, split_problem, path, split):
+    label, backend, multipass, extra = path
+    p, y_ref, s_ref = split_problem
+    first, second = _sub(p, 0, split), _sub(p, split, p.d.n_tok)
+    with env(**extra):
+        s_mid = torch.full(first.s_shape(), float("nan"), device="cuda")
+        _, y1, _ = run(gpu, first, desc=_desc(first, backend, multipass), s1_gpu=s_mid)
+        _, y2, s1 = run(gpu, second, desc=_desc(second, backend, multipass), s0_gpu=s_mid)
+        _, y_full, s1_full = run(gpu, p, desc=_desc(p, backend, multipass))
+    y_split = np.concatenate([y1, y2], axis=1)
+    gate = _gate(label)
+    e_ref, es_ref = _rel(y_split, y_ref), _rel(s1, s_ref)
+    e_self = _rel(y_split, y_full)
+    print(f"{label} split {split}: vs oracle {e_ref:.2e} (s1 {es_ref:.2e}), vs unsplit {e_self:.2e}",
+          flush=True)
+    assert np.all(np.isfinite(y_split)) and np.all(np.isfinite(s1))
+    assert e_ref <= gate and e_self <= gate
+    # The carried state never passes through bf16 on any path.
+    assert es_ref <= F32_GATE and _rel(s1, s1_full) <= F32_GATE
+    assert po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0
+
+
+# ---------------------------------------------------------------------------
+# ids: source state rows permuted
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_ids_permutation(gpu, path):
+    label, backend, multipass, extra = path
+    p = po.problem_harness(300, 4, 4, 64, 128, 2, 2718, "long")
+    rng = np.random.default_rng(5)
+    p.s0 = rng.standard_normal(p.s0.shape).astype(np.float32) * 0.3
+    p.ids = np.array([2, 0, 3, 1], np.int32)
+    y_ref, s_ref = po.scan(p, use_ids=True)
+    y_plain, _ = po.scan(p, use_ids=False)
+    assert _rel(y_plain, y_ref) > 1e-2      # the permutation is visible in y
+    with env(**extra):
+        _, y, s1 = run(gpu, p, desc=_desc(p, backend, multipass), use_ids=True)
+    ey, es = _rel(y, y_ref), _rel(s1, s_ref)
+    print(f"{label} ids {p.ids.tolist()}: y {ey:.2e} s1 {es:.2e}", flush=True)
+    assert ey <= _gate(label) and es <= F32_GATE
+
+
+# ---------------------------------------------------------------------------
+# Strided views (what a ggml caller passes)
+# ---------------------------------------------------------------------------
+
+def _strided_problem(L, S, H, P, N, G, seed):
+    """A dense harness problem re-laid into padded buffers, with the strides
+    in the descriptor; the oracle reads the same buffers through them."""
+    base = po.problem_harness(L, S, H, P, N, G, seed, "long")
+    rng = np.random.default_rng(seed)
+    base.s0 = rng.standard_normal(base.s0.shape).astype(np.float32) * 0.2
+    d = desc_init(L, S, H, P, N, G)
+
+    def place(dense, strides, seq_stride, fill=np.nan):
+        """dense [S, a, b, c] (or [S, a, b]) into a flat buffer at the given strides."""
+        total = seq_stride * dense.shape[0]
+        buf = np.full(total + 64, fill, np.float32)
+        idx = np.zeros(dense.shape, np.int64)
+        for ax, st in enumerate((seq_stride,) + tuple(strides)):
+            shape = [1] * dense.ndim
+            shape[ax] = dense.shape[ax]
+            idx = idx + (np.arange(dense.shape[ax]) * st).reshape(shape)
+        assert idx.max() < total
+        buf[idx] = dense
+        return buf
+
+    # x: padded token rows and head stride; y: different padding.
+    sx = (H * (P + 8) + 16, P + 8, 1)
+    sy = (H * P + 32, P, 1)
+    sb = (G * (N + 8) + 8, N + 8, 1)
+    sc = (G * N + 24, N, 1)
+    sdt = (H + 3, 1)
+    ss = (P * N + 64, N, 1)
+    seq = lambda st, Lr: st[0] * Lr + 40
+    x = place(base.x, sx, seq(sx, L))
+    B = place(base.B, sb, seq(sb, L))
+    C = place(base.C, sc, seq(sc, L))
+    dt = place(base.dt, sdt, seq(sdt, L))
+    s0 = place(base.s0, ss, H * ss[0] + 128, 0.0)
+    A = np.full(2 * H, np.nan, np.float32)
+    A[::2] = base.A
+    for name, st, sq in (("s_x", sx, seq(sx, L)), ("s_b", sb, seq(sb, L)), ("s_c", sc, seq(sc, L))):
+        arr = getattr(d, name)
+        arr[0], arr[1], arr[2] = st
+        setattr(d, "seq_" + name[2:], sq)
+    d.s_y[0], d.s_y[1], d.s_y[2], d.seq_y = sy[0], sy[1], sy[2], seq(sy, L)
+    d.s_dt[0], d.s_dt[1], d.seq_dt = sdt[0], sdt[1], seq(sdt, L)
+    d.s_s[0], d.s_s[1], d.s_s[2], d.seq_s = ss[0], ss[1], ss[2], H * ss[0] + 128
+    d.s_a = 2
+    p = po.Problem(d, s0, x, dt, A, B, C, None, label="strided")
+    y_len = d.seq_y * S + 64
+    s_len = d.seq_s * S + 64
+    return p, base, y_len, s_len
+
+
+def _dense_y(p, buf):
+    d = p.d
+    S, L, H, P = d.n_seq, d.n_tok, d.n_head, d.head_dim
+    i = (np.arange(S)[:, None, None, None] * d.seq_y + np.arange(L)[None, :, None, None] * d.s_y[0]
+         + np.arange(H)[None, None, :, None] * d.s_y[1] + np.arange(P)[None, None, None, :] * d.s_y[2])
+    return buf[i]
+
+
+def _dense_s(p, buf):
+    d = p.d
+    S, H, P, N = d.n_seq, d.n_head, d.head_dim, d.d_state
+    i = (np.arange(S)[:, None, None, None] * d.seq_s + np.arange(H)[None, :, None, None] * d.s_s[0]
+         + np.arange(P)[None, None, :, None] * d.s_s[1] + np.arange(N)[None, None, None, :])
+    return buf[i]
+
+
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_strided_views(gpu, path):
+    label, backend, multipass, extra = path
+    p, base, y_len, s_len = _strided_problem(200, 2, 4, 64, 128, 2, 77)
+    d = _desc(p, backend, multipass)
+    # Oracle on the padded buffers through the strides, and on the dense copy.
+    y_buf = np.zeros(y_len, np.float32)
+    s_buf = np.zeros(s_len, np.float32)
+    po.lib().oracle_scan(ctypes.byref(p.d), po._f(p.s0), po._f(p.x), po._f(p.dt), po._f(p.A),
+                         po._f(p.B), po._f(p.C), None, po._f(y_buf), po._f(s_buf), None)
+    y_ref, s_ref = _dense_y(p, y_buf), _dense_s(p, s_buf)
+    y_dense, s_dense = po.scan(base, use_ids=False)
+    assert _rel(y_ref, y_dense) < 1e-6 and _rel(s_ref, s_dense) < 1e-6
+    with env(**extra):
+        assert gpu.supported(d), gpu.backend_desc(d)
+        dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+        y_gpu = torch.full((y_len,), float("nan"), device="cuda")
+        s_gpu = torch.full((s_len,), float("nan"), device="cuda")
+        nbytes = gpu.scratch_size(d)
+        scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+        rc = gpu.encode(torch.cuda.current_stream().cuda_stream, d, T(dev["s0"]), T(dev["x"]),
+                        T(dev["dt"]), T(dev["A"]), T(dev["B"]), T(dev["C"]), HELIX_TENSOR_NULL,
+                        T(y_gpu), T(s_gpu), T(scratch))
+        assert rc == HELIX_OK, gpu.last_error()
+        torch.cuda.synchronize()
+    y_out, s_out = y_gpu.cpu().numpy(), s_gpu.cpu().numpy()
+    y, s1 = _dense_y(p, y_out), _dense_s(p, s_out)
+    ey, es = _rel(y, y_ref), _rel(s1, s_ref)
+    print(f"{label} strided: y {ey:.2e} s1 {es:.2e}", flush=True)
+    assert ey <= _gate(label) and es <= F32_GATE
+    # Nothing outside the views was written: padding keeps its NaN fill.
+    mask_y = np.ones(y_len, bool)
+    mask_y[_dense_y(p, np.arange(y_len))] = False
+    mask_s = np.ones(s_len, bool)
+    mask_s[_dense_s(p, np.arange(s_len))] = False
+    assert np.all(np.isnan(y_out[mask_y])) and np.all(np.isnan(s_out[mask_s]))
+
+
+# ---------------------------------------------------------------------------
+# Determinism, encode_into, error paths
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", PATHS, ids=PATH_IDS)
+def test_deterministic_and_encode_into(gpu, path):
+    label, backend, multipass, extra = path
+    p = po.problem_harness(700, 2, 8, 64, 128, 2, 99, "long")
+    d = _desc(p, backend, multipass)
+    with env(**extra):
+        _, y1, s1a = run(gpu, p, desc=d)
+        _, y2, s1b = run(gpu, p, desc=d, into=True)
+    assert y1.tobytes() == y2.tobytes() and s1a.tobytes() == s1b.tobytes(), label
+
+
+def _address_range(ptr: int):
+    """(base, size) of the HIP allocation containing device pointer ptr."""
+    # The runtime already in the process (torch's, which libhelix.so binds to
+    # by soname): RTLD_NOLOAD never loads a second copy.
+    hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | os.RTLD_LAZY)
+    base, size = ctypes.c_void_p(), ctypes.c_size_t()
+    rc = hip.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ctypes.c_void_p(ptr))
+    assert rc == 0, f"hipMemGetAddressRange failed: {rc}"
+    return base.value, size.value
+
+
+def test_errors_enqueue_nothing(gpu):
+    p = po.problem_harness(300, 1, 4, 64, 128, 1, 7, "short")
+    d = _desc(p, HELIX_BACKEND_MPP, True)
+    need = gpu.scratch_size(d)
+    assert need > 0
+    dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+    y = torch.full(p.y_shape(), float("nan"), device="cuda")
+    s1 = torch.full(p.s_shape(), float("nan"), device="cuda")
+    # The size check sees the HIP allocation that contains the scratch
+    # pointer (a device pointer carries no length): place the pointer
+    # need/2 bytes before the end of its allocation, confirmed here with the
+    # same query, so the scan cannot fit and the encode must refuse it.
+    pool = torch.empty(4 * need, dtype=torch.uint8, device="cuda")
+    base, size = _address_range(pool.data_ptr())
+    end = base + size
+    small = HelixTensor(end - need // 2, 0)
+    assert end - small.buf < need and small.buf >= pool.data_ptr()
+    stream = torch.cuda.current_stream().cuda_stream
+    args = [T(dev[k]) for k in ("s0", "x", "dt", "A", "B", "C")]
+    rc = gpu.encode(stream, d, *args, HELIX_TENSOR_NULL, T(y), T(s1), small)
+    assert rc == HELIX_ERR_SCRATCH_TOO_SMALL, gpu.last_error()
+    rc = gpu.encode(stream, d, *args, HELIX_TENSOR_NULL, T(y), T(s1), HELIX_TENSOR_NULL)
+    assert rc == HELIX_ERR_SCRATCH_TOO_SMALL
+    ok_scratch = T(torch.empty(need, dtype=torch.uint8, device="cuda"))
+    rc = gpu.encode(stream, d, *args[:5], HELIX_TENSOR_NULL, HELIX_TENSOR_NULL, T(y), T(s1), ok_scratch)
+    assert rc == HELIX_ERR_INVALID_ARG
+    bad = d.copy()
+    bad.d_state = 260
+    rc = gpu.encode(stream, bad, *args, HELIX_TENSOR_NULL, T(y), T(s1), ok_scratch)
+    assert rc == HELIX_ERR_UNSUPPORTED_SHAPE
+    # An explicit bf16 request is declined on the single-pass path.
+    one = d.copy()
+    one.multipass = False
+    rc = gpu.encode(stream, one, *args, HELIX_TENSOR_NULL, T(y), T(s1), HELIX_TENSOR_NULL)
+    assert rc == HELIX_ERR_UNSUPPORTED_SHAPE
+    torch.cuda.synchronize()
+    assert torch.isnan(y).all() and torch.isnan(s1).all()
+    # The single pass needs no scratch at all.
+    one.backend = HELIX_BACKEND_AUTO
+    assert gpu.scratch_size(one) == 0
+    rc = gpu.encode(stream, one, *args, HELIX_TENSOR_NULL, T(y), T(s1), HELIX_TENSOR_NULL)
+    assert rc == HELIX_OK
+    torch.cuda.synchronize()
+    y_ref, s_ref = po.scan(p)
+    assert _rel(y.cpu().numpy(), y_ref) <= F32_GATE
+
+
+def test_side_stream(gpu):
+    """Encoding onto a non-default stream orders with that stream only."""
+    p = po.problem_harness(500, 1, 4, 64, 128, 2, 11, "long")
+    y_ref, s_ref = po.scan(p)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        _, y, s1 = run(gpu, p, desc=_desc(p, HELIX_BACKEND_MPP, True), stream=side)
+    assert _rel(y, y_ref) <= BF16_GATE and _rel(s1, s_ref) <= F32_GATE
