@@ -26,7 +26,7 @@ sys.path.insert(0, ROOT)
 import torch  # noqa: E402
 
 from helix_amd.abi import Context  # noqa: E402
-from helix_amd.desc import (HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_OK,  # noqa: E402
+from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_OK,  # noqa: E402
                             algorithmic_bytes, algorithmic_flops)
 from helix_amd.scan import make_desc, tensor_arg  # noqa: E402
 
@@ -58,15 +58,16 @@ def make_inputs(seed: int, dev):
 
 
 class Variant:
-    def __init__(self, name, ctx, backend, tensors, env=None):
+    def __init__(self, name, ctx, backend, tensors, env=None, multipass=True):
         self.name = name
         self.ctx = ctx
         self.env = env or {}
+        self.multipass = multipass
         saved = self._push()
         x, dt, A, B, C, s0 = tensors
         self.y = torch.empty_like(x)
         self.s1 = torch.empty_like(s0)
-        self.d = make_desc(x, dt, B, C, s0, self.y, A, multipass=True)
+        self.d = make_desc(x, dt, B, C, s0, self.y, A, multipass=multipass)
         self.d.backend = backend
         assert ctx.supported(self.d), ctx.backend_desc(self.d)
         self.kernel = ctx.backend_desc(self.d)
@@ -229,6 +230,7 @@ def main():
         # Alternative kernel choices, timed interleaved in the same process.
         variants.append(Variant("bf16-tile", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_BF16_PASSC": "tile"}))
+        variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
 
     # Warm-up: W steps each, then alternate until the wall clock has run
     # warmup_ms (the reference's protocol against clock ramps).
@@ -256,7 +258,9 @@ def main():
         ts = time_variant(v, args.steps, stream)
         torch.cuda.synchronize()
         wall = (time.perf_counter() - w0) / args.steps * 1e3
-        passes = {k: dist(time_variant(v, args.steps, stream, only=k)) for k in "ABC"}
+        # Per-pass split (HELIX_ONLY_PASS) exists only for the multipass path.
+        passes = ({k: dist(time_variant(v, args.steps, stream, only=k)) for k in "ABC"}
+                  if v.multipass else None)
         d = dist(ts)
         ms = statistics.fmean(ts)
         peak_c = PEAK_BF16_MFMA if v.name == "bf16" else PEAK_FP32_MFMA
@@ -327,9 +331,13 @@ def main():
     }
     extra = [v for v in variants if v.name not in ("bf16", "fp32")]
     if extra:
-        out["variants"] = {v.name: {"ms_per_step": results[v.name]["ms"], "kernel": results[v.name]["kernel"],
-                                    "passes_ms_median": {k: results[v.name]["passes"][k]["median"] for k in "ABC"}}
-                           for v in extra}
+        out["variants"] = {}
+        for v in extra:
+            rv = results[v.name]
+            e = {"ms_per_step": rv["ms"], "kernel": rv["kernel"]}
+            if rv["passes"]:
+                e["passes_ms_median"] = {k: rv["passes"][k]["median"] for k in "ABC"}
+            out["variants"][v.name] = e
     if args.calib_copy:
         n = args.calib_copy * (1 << 20) // 4
         src = torch.randn(n, device=dev)
