@@ -81,20 +81,29 @@ HELIX_DEV int tri_jb(int idx) {
     return idx - tb * (tb + 1) / 2;
 }
 
-template <int NP>
+// DIAG: A is one decay per (head, state index), A[h][n] (reference
+// scan_ref.cpp:26-29). Then M[t][j] = sum_n C_t[n] B_j[n] exp(A_n (cs_t -
+// cs_j)), with cs the chunk-local prefix of dt, is no longer a product of
+// matrices; it is summed on the VALU (exp2 of a pre-scaled A), and the rest
+// stays on MFMA after folding every other decay into factors that never
+// exceed 1: C rows by exp(A_n cs_t) (G3), B rows by exp(A_n (cs_end - cs_j))
+// (G4), and the carried state by exp(A_n cs_end) per state index.
+template <int NP, bool DIAG>
 __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int NT  = NP / 16;           // 16-row state tiles (all of them live in every wave)
     constexpr int RSC = NP + 4;            // C and B rows
-    constexpr int RSM = HELIX_CS + 4;      // M rows, in B's region after G4
+    constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
     constexpr int RSX = HELIX_HD + 16;     // dtX rows
     static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
     __shared__ __attribute__((aligned(16))) float sC[HELIX_CS * RSC];
     __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSC];
     __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * RSX];
-    __shared__ double sL[HELIX_CS];        // Lcum_t (fp64)
+    __shared__ double sL[HELIX_CS];        // Lcum_t (scalar A) or cs_t (DIAG), fp64
     __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
     __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
-    float* const sM = sB;
+    __shared__ double sA2[DIAG ? NP : 2];        // A_n log2(e) in fp64, 0 past d_state
+    __shared__ __attribute__((aligned(16))) float sMd[DIAG ? HELIX_CS * RSM : 4];
+    float* const sM = DIAG ? sMd : sB;
 
     const int lane = threadIdx.x & 63, wave = wave_uniform();
     const int l16 = lane & 15, g4 = lane >> 4;
@@ -112,7 +121,11 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     const int pw = min(HELIX_HD, p.head_dim - p0);
     const int pc = 16 * wave + l16;       // this lane's channel in the slab (result column)
 
-    const float A_h = b.A[(long long)h * p.s_a];
+    const float A_h = DIAG ? 0.0f : b.A[(long long)h * p.s_a];
+    if constexpr (DIAG) {
+        for (int n = threadIdx.x; n < NP; n += HELIX_WG)
+            sA2[n] = n < N ? (double)b.A[(long long)h * p.s_a + n] * 1.4426950408889634074 : 0.0;
+    }
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
     const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + (long long)p0 * p.s_x[2];
 
@@ -147,12 +160,14 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         // dt = 0 past tlen, so Lcum stays at Lcum[tlen-1] there and dtX rows
         // past tlen are zero.
         const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
-        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lcum = wave_incl_sum(DIAG ? (double)dtv : (double)A_h * (double)dtv);
         const double lend = bcast(lcum, 63);
         if (wave == 0) {
-            sL[lane]  = lcum;
-            sCs[lane] = exp_diff(lend, lcum);
-            sE[lane]  = expf((float)lcum);
+            sL[lane] = lcum;
+            if constexpr (!DIAG) {
+                sCs[lane] = exp_diff(lend, lcum);
+                sE[lane]  = expf((float)lcum);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -176,22 +191,68 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             load_stage_s<NP>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS, min(HELIX_CS, p.n_tok - t0 - HELIX_CS),
                              pw, lane, wave);
 
-        // B operands of G2 (dtX) and G4 (dtX scaled by exp(L_end - Lcum_j)).
+        // B operands of G2 (dtX) and G4 (dtX scaled by exp(L_end - Lcum_j); with
+        // DIAG that decay goes into the B rows instead).
         float xb[16], xs[16];
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const int j = 4 * s + g4;
             xb[s] = sX[j * RSX + pc];
-            xs[s] = xb[s] * sCs[j];
+            xs[s] = DIAG ? xb[s] : xb[s] * sCs[j];
         }
 
         // ---- G1: M = tril(C B^T) . exp(Lcum_t - Lcum_j), tiles wave + 4 q ----
         f32x4 mt[3];
+        if constexpr (DIAG) {
+            // M on the VALU. Thread: row t = tid / 4, columns j = 16 q + i
+            // (q = tid % 4); a group wholly above the diagonal skips the sum.
+            // Past d_state C and B are zero, so n runs to d_state only. Each
+            // exponent is formed in fp64 and rounded once, as the scalar
+            // path's exp(Lcum_t - Lcum_j) is.
+            const int t = threadIdx.x >> 2, q = threadIdx.x & 3;
+            const double ct = sL[t];
+            double dcs[16];
+            float acc[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                dcs[i] = ct - sL[16 * q + i];
+                acc[i] = 0.0f;
+            }
+            if (16 * q <= t) {
+                for (int n = 0; n < N; n += 4) {
+                    const f32x4 c4 = *reinterpret_cast<const f32x4*>(&sC[t * RSC + n]);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const double a = sA2[n + k];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            acc[i] = fmaf(c4[k] * __builtin_amdgcn_exp2f((float)(a * dcs[i])),
+                                          sB[(16 * q + i) * RSC + n + k], acc[i]);
+                    }
+                }
+            }
+            // j > t: the exponent is positive and may overflow; the bitwise
+            // mask clears whatever the sum holds.
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sM[t * RSM + 16 * q + i] = keep_if_le(acc[i], 16 * q + i, t);
+            __syncthreads();   // M is summed from the unscaled rows
+            // C rows by exp(A_n cs_t), B rows by exp(A_n (cs_end - cs_j)).
+#pragma unroll 4
+            for (int i = 0; i < HELIX_CS * NP / HELIX_WG; ++i) {
+                const int idx = (int)threadIdx.x + HELIX_WG * i;
+                const int row = idx / NP, n = idx % NP;
+                const double cr = sL[row];
+                const double a = sA2[n];
+                sC[row * RSC + n] *= __builtin_amdgcn_exp2f((float)(a * cr));
+                sB[row * RSC + n] *= __builtin_amdgcn_exp2f((float)(a * (lend - cr)));
+            }
+            __syncthreads();
+        }
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
             mt[q] = zero4();
             const int idx = wave + 4 * q;
-            if (idx < 10) {
+            if (!DIAG && idx < 10) {
                 const int tb = tri_tb(idx), jb = tri_jb(idx);
                 f32x4 acc = zero4();
 #pragma unroll 4
@@ -226,33 +287,45 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 for (int s = 0; s < 4; ++s) ya[tb] = mfma16(a4[s], R[nt][s], ya[tb]);
             }
         }
+        if constexpr (!DIAG) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
+            for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ya[tb][r] *= sE[16 * tb + 4 * g4 + r];
+                for (int r = 0; r < 4; ++r) ya[tb][r] *= sE[16 * tb + 4 * g4 + r];
+        }
 
         // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x) -------------
-        const float a_c = expf((float)lend);
+        if constexpr (DIAG) {
+            // Per state index: register r of tile nt holds n = 16 nt + 4 g4 + r.
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) R[nt] *= a_c;
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    R[nt][r] *= __builtin_amdgcn_exp2f((float)(sA2[16 * nt + 4 * g4 + r] * lend));
+        } else {
+            const float a_c = expf((float)lend);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) R[nt] *= a_c;
+        }
 #pragma unroll 4
         for (int s = 0; s < 16; ++s) {
             const int j = 4 * s + g4;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) R[nt] = mfma16(sB[j * RSC + 16 * nt + l16], xs[s], R[nt]);
         }
-        __syncthreads();   // every wave is done with the B rows: M takes them over
-
+        if constexpr (!DIAG) {
+            __syncthreads();   // every wave is done with the B rows: M takes them over
 #pragma unroll
-        for (int q = 0; q < 3; ++q) {
-            const int idx = wave + 4 * q;
-            if (idx < 10) {
-                const int tb = tri_tb(idx), jb = tri_jb(idx);
+            for (int q = 0; q < 3; ++q) {
+                const int idx = wave + 4 * q;
+                if (idx < 10) {
+                    const int tb = tri_tb(idx), jb = tri_jb(idx);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sM[(16 * tb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
+                    for (int r = 0; r < 4; ++r) sM[(16 * tb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
 
         // ---- G2: y += M dtX over the causal K range of each t block ---------
 #pragma unroll
@@ -297,9 +370,18 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #define HELIX_SCAN_1PASS(NP)                                                                    \
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_f32_n##NP(           \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        scan_1pass_impl<NP>(p, b);                                                              \
+        scan_1pass_impl<NP, false>(p, b);                                                       \
+    }
+
+#define HELIX_SCAN_1PASS_DIAG(NP)                                                               \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_diag_f32_n##NP(      \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_1pass_impl<NP, true>(p, b);                                                        \
     }
 
 HELIX_SCAN_1PASS(64)
 HELIX_SCAN_1PASS(128)
 HELIX_SCAN_1PASS(256)
+// d_state <= 128: the diagonal form keeps M in rows of its own.
+HELIX_SCAN_1PASS_DIAG(64)
+HELIX_SCAN_1PASS_DIAG(128)

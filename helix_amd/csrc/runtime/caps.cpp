@@ -74,6 +74,19 @@ constexpr HelixMatmulTraits kSingleTraits[] = {
      "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 256, false, "helix_scan_1pass_f32_n256"},
 };
 
+// Diagonal A (A[h][n], HELIX_A_DIAG_PER_CHANNEL): the reference declines it
+// (caps.mm:121-123) because its chunked factorization needs one decay per
+// (head, token); here the single-pass walk serves it, with M summed on the
+// VALU and the other decays folded into row scales (pass_single.hip). It runs
+// for either value of `multipass` (there is no three-pass form) and needs no
+// scratch. d_state <= 128.
+constexpr HelixMatmulTraits kDiagTraits[] = {
+    {HELIX_BACKEND_SGMMA, "mfma fp32, single pass, diagonal A (d_state<=64)", nullptr, nullptr, nullptr, false,
+     "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 64, false, "helix_scan_1pass_diag_f32_n64"},
+    {HELIX_BACKEND_SGMMA, "mfma fp32, single pass, diagonal A (d_state<=128)", nullptr, nullptr, nullptr, false,
+     "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", 128, false, "helix_scan_1pass_diag_f32_n128"},
+};
+
 // bf16x6 kernels: GEMMs on bf16 MFMA over operands split into three bf16
 // parts, fp32 accuracy at 16x the fp32 matrix issue rate. Pass A uses them on
 // every path (pass_a_x6.hip) and the fp32 path's Pass C for d_state <= 128
@@ -136,6 +149,7 @@ const char* const kKernelNames[] = {
     "helix_chunk_state_agg_n64",  "helix_chunk_state_agg_n128", "helix_chunk_state_agg_n256",
     "helix_scan_walk_bf16_n64",   "helix_scan_walk_bf16_n128",  "helix_scan_walk_bf16_n256",
     "helix_scan_1pass_f32_n64",   "helix_scan_1pass_f32_n128",  "helix_scan_1pass_f32_n256",
+    "helix_scan_1pass_diag_f32_n64", "helix_scan_1pass_diag_f32_n128",
 };
 
 int np_index(int d_state) {
@@ -184,6 +198,7 @@ bool prefer_walk(const helix_scan_desc& d);
 const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d) {
     (void)ctx;
     const int k = np_index(d.d_state);
+    if (d.a_form == HELIX_A_DIAG_PER_CHANNEL) return kDiagTraits[k < 1 ? k : 1];
     if (!d.multipass) return kSingleTraits[k];
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
@@ -381,8 +396,14 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
         d->d_state <= 0 || d->n_group <= 0)
         return false;
     if (d->n_head % d->n_group != 0) return false;
-    // The chunked reassociation needs one decay scalar per (head, token).
-    if (d->a_form != HELIX_A_SCALAR_PER_HEAD) return false;
+    // Scalar A runs on every path; diagonal A (one decay per state index) on
+    // the fp32 single-pass walk only, up to d_state 128 (an explicit bf16
+    // request for it is declined, as the reference declines diagonal A).
+    if (d->a_form == HELIX_A_DIAG_PER_CHANNEL) {
+        if (d->d_state > 128 || d->backend == HELIX_BACKEND_MPP) return false;
+    } else if (d->a_form != HELIX_A_SCALAR_PER_HEAD) {
+        return false;
+    }
     // fp16/bf16 storage is not served; bf16 compute is chosen by backend.
     if (d->io_dtype != HELIX_F32 || d->compute_dtype != HELIX_F32) return false;
     if (d->d_state % 8 != 0 || d->head_dim % 8 != 0) return false;
@@ -400,7 +421,8 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
 }
 
 extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
-    if (!d || !d->multipass) return 0;
+    // The single-pass walks (multipass = false, and diagonal A) use none.
+    if (!d || !d->multipass || d->a_form == HELIX_A_DIAG_PER_CHANNEL) return 0;
     return helix::rt::plan_multipass(*d, helix::rt::select_traits(ctx, *d)).total_bytes;
 }
 

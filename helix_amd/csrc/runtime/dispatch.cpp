@@ -7,7 +7,7 @@
 // enqueued. Stream order sequences the passes; there are no barriers to
 // insert.
 //
-// multipass = false: one launch of the single-pass kernel, grid
+// multipass = false, or a diagonal A: one launch of the single-pass kernel, grid
 // (n_seq * n_head * n_pslab) x 256 threads, no scratch.
 //
 // Otherwise, per super-chunk group, in stream order:
@@ -70,7 +70,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
 
     // Single pass (reference dispatch.mm:122-138): one launch, one workgroup
     // per (seq, head, P slab), the state carried in registers; no scratch.
-    if (!d->multipass) {
+    // Diagonal A always takes this path.
+    if (tr.k_single) {
         hipFunction_t f1 = fn(tr.k_single);
         if (!f1) {
             set_error(ctx, "kernel not resolved in code object");
@@ -257,7 +258,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     std::memset(out, 0, sizeof(*out));
-    if (!d->multipass) {
+    if (tr.k_single) {
         out->n_chunks = (d->n_tok + HELIX_CS - 1) / HELIX_CS;
         out->chunks_per_group = out->n_chunks;
         out->n_groups = 1;

@@ -19,8 +19,9 @@ extern "C" {
  * HELIX_ERR_NO_DEVICE without touching HIP. Free with helix_ctx_free. */
 helix_status helix_ctx_create_host(helix_ctx** out);
 
-/* The plan helix_scan_encode would use for `d`. With multipass = false it is
- * one launch of kernel_1pass: one group, no scratch, kernel_a/b/c NULL. */
+/* The plan helix_scan_encode would use for `d`. With multipass = false, or a
+ * diagonal A, it is one launch of kernel_1pass: one group, no scratch,
+ * kernel_a/b/c NULL. */
 typedef struct {
     int32_t  n_chunks;          /* ceil(n_tok / 64)                              */
     int32_t  chunks_per_group;  /* chunks per super-chunk group (scratch bound)  */

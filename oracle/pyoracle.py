@@ -133,6 +133,21 @@ def problem_harness(L, S, H, P, N, G, seed, memory="short", chunk=0) -> Problem:
     return Problem(d, s0, x, dt, A, B, C, ids, label=f"harness seed={seed} {memory}")
 
 
+def problem_diag(L, S, H, P, N, G, seed, memory="long") -> Problem:
+    """A harness problem with a diagonal A (A[h][n], helix.h HELIX_A_DIAG_PER_CHANNEL,
+    reference scan_ref.cpp:26-29): per-(head, state) decays drawn like the
+    harness draws the scalar ones, A = -exp(U(-0.5, 1)) for LONG memory and
+    A = -exp(U(0, ln 16)) for SHORT, from numpy's generator seeded with `seed`."""
+    p = problem_harness(L, S, H, P, N, G, seed, memory)
+    rng = np.random.default_rng(seed)
+    lo, hi = (-0.5, 1.0) if memory == "long" else (0.0, float(np.log(16.0)))
+    p.A = (-np.exp(rng.uniform(lo, hi, (H, N)))).astype(np.float32).ravel()
+    p.d.a_form = 1          # HELIX_A_DIAG_PER_CHANNEL
+    p.d.s_a = N
+    p.label = f"diag-A harness seed={seed} {memory}"
+    return p
+
+
 def problem_gauss(L, S, H, P, N, G, seed, s0_sigma=0.0, dt_mu=-1.0, dt_sigma=0.5,
                   a_lo=1.0, a_hi=16.0) -> Problem:
     """The BASELINE.json generator (Gaussian; see helix_oracle.h)."""

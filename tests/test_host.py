@@ -122,7 +122,12 @@ def _declined(host, mutate):
     ("zero tokens", lambda d: setattr(d, "n_tok", 0)),
     ("negative heads", lambda d: setattr(d, "n_head", -4)),
     ("heads not a multiple of groups", lambda d: setattr(d, "n_group", 3)),
-    ("diagonal A", lambda d: setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL)),
+    ("diagonal A with explicit MPP",
+     lambda d: (setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL), setattr(d, "backend", HELIX_BACKEND_MPP))),
+    ("diagonal A at d_state 256",
+     lambda d: (setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL), setattr(d, "d_state", 256),
+                d.s_s.__setitem__(1, 256))),
+    ("unknown A form", lambda d: setattr(d, "a_form", 7)),
     ("bf16 storage", lambda d: setattr(d, "io_dtype", HELIX_BF16)),
     ("bf16 compute dtype", lambda d: setattr(d, "compute_dtype", HELIX_BF16)),
     ("d_state not a multiple of 8", lambda d: setattr(d, "d_state", 60)),
@@ -151,6 +156,25 @@ def test_gate_accepts_ragged_strided_and_odd_shapes(host):
     d.s_y[2] = 1
     d.chunk = 64
     assert host.supported(d)
+
+
+def test_diagonal_a_runs_the_single_pass_walk(host):
+    # Diagonal A: one launch of the diagonal single-pass kernel for either
+    # value of multipass, AUTO or SGMMA, no scratch.
+    for multipass in (True, False):
+        for backend in (HELIX_BACKEND_AUTO, HELIX_BACKEND_SGMMA):
+            for n, want in ((16, 64), (64, 64), (128, 128)):
+                d = mp((300, 2, 4, 64, n, 2), backend)
+                d.multipass = multipass
+                d.a_form = HELIX_A_DIAG_PER_CHANNEL
+                d.s_a = n
+                assert host.supported(d)
+                assert host.select_backend(d) == HELIX_BACKEND_SGMMA
+                assert host.backend_desc(d) == f"mfma fp32, single pass, diagonal A (d_state<={want})"
+                assert host.scratch_size(d) == 0
+                k = host.plan_info(d)
+                assert k.kernel_1pass == b"helix_scan_1pass_diag_f32_n%d" % want
+                assert (k.launches, k.total_bytes, k.kernel_a) == (1, 0, None)
 
 
 def test_null_context_and_desc():

@@ -216,9 +216,10 @@ def _brute(p):
                 for t in range(L):
                     v = float(p.dt[s, t, h])
                     dt = v if v > 20 else math.log1p(math.exp(v))
-                    a = math.exp(float(p.A[h]) * dt)
                     acc = 0.0
                     for n in range(N):
+                        a_hn = p.A[h * p.d.s_a + (n if p.d.a_form == 1 else 0)]
+                        a = math.exp(float(a_hn) * dt)
                         st[n] = a * st[n] + dt * float(p.B[s, t, g, n]) * float(p.x[s, t, h, q])
                         acc += float(p.C[s, t, g, n]) * st[n]
                     y[s, t, h, q] = acc
@@ -340,3 +341,39 @@ def test_gauss_generator_moments():
     assert np.all(p.A <= -1.0) and np.all(p.A >= -16.0)
     z = po.problem_gauss(16, 1, 2, 8, 8, 1, 1, s0_sigma=0.0)
     assert not np.any(z.s0)
+
+
+# ---------------------------------------------------------------------------
+# Diagonal A (A[h][n]; reference scan_ref.cpp:26-29, helix.h HELIX_A_DIAG_PER_CHANNEL)
+# ---------------------------------------------------------------------------
+
+@needs_ref
+@pytest.mark.parametrize("memory", ["short", "long"])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 8, 8, 1), (130, 2, 4, 64, 64, 2), (300, 1, 2, 64, 128, 1)])
+def test_diag_bitexact_vs_reference(shape, memory):
+    p = po.problem_diag(*shape, 404, memory)
+    p.ids = np.arange(p.d.n_seq, dtype=np.int32)[::-1].copy()
+    y, s1 = po.scan(p)
+    yr, sr = po.ref_scan(p)
+    assert np.array_equal(bits(y), bits(yr)) and np.array_equal(bits(s1), bits(sr))
+
+
+def test_diag_with_equal_rows_is_the_scalar_form():
+    # Every state row of a head decaying at A_h is exactly the scalar-A scan.
+    p = po.problem_diag(200, 2, 4, 16, 24, 2, 8, "long")
+    q = po.problem_harness(200, 2, 4, 16, 24, 2, 8, "long")
+    A = np.repeat(q.A[:, None], 24, axis=1).astype(np.float32)
+    p.A = A.ravel()
+    y, s1 = po.scan(p)
+    yq, sq = po.scan(q)
+    assert np.array_equal(bits(y), bits(yq)) and np.array_equal(bits(s1), bits(sq))
+
+
+@pytest.mark.parametrize("shape", [(9, 1, 1, 1, 3, 1), (12, 2, 4, 3, 2, 2)])
+def test_diag_brute_force_small(shape):
+    p = po.problem_diag(*shape, 33, "long")
+    assert len(set(p.A.tolist())) == p.A.size        # the rows really differ
+    y, s1 = po.scan(p)
+    yb, sb = _brute(p)
+    np.testing.assert_allclose(y, yb, rtol=1e-6, atol=1e-12)
+    np.testing.assert_allclose(s1, sb, rtol=1e-6, atol=1e-12)
