@@ -100,8 +100,9 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
     __shared__ __attribute__((aligned(16))) __bf16 sBt[NP * RSJ];
     __shared__ __attribute__((aligned(16))) __bf16 sXt[HPW][HELIX_HD * RSJ];
     __shared__ __attribute__((aligned(16))) __bf16 sXst[HPW][HELIX_HD * RSJ];
-    __shared__ __attribute__((aligned(16))) double sL[HPW][HELIX_CS];
+    __shared__ __attribute__((aligned(16))) float sL2[HPW][HELIX_CS];   // Lcum_t log2(e), fp32
     __shared__ __attribute__((aligned(16))) float sE[HPW][HELIX_CS];
+    __shared__ __attribute__((aligned(16))) float sDt[NW][2][HELIX_CS];  // per wave: dt_j, decay_j
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
@@ -237,23 +238,37 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         }
 
         // ---- decay preamble, dtX^T and dtXs^T -----------------------------------
+        // The prefix itself is summed in fp64; the decays that only feed bf16
+        // operands (M, dtXs) are formed in fp32 from Lcum log2(e): an fp32
+        // difference of two prefixes is good to ~2^-24 of their magnitude,
+        // far inside the 2^-9 of a bf16 operand.
         const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
         const double lcum = wave_incl_sum((double)A_h * (double)dtv);
         const double lend = __shfl(lcum, 63, 64);
         const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
         {
+            // dt and the decay of this wave's 16 tokens, through the wave's own
+            // LDS row (one write, four broadcast reads each; the wave's LDS
+            // accesses complete in order).
+            sDt[wave][0][lane] = dtv;
+            sDt[wave][1][lane] = sdec;
             float vx[16], vs[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float dx = bcast(dtv, 16 * w4 + i) * st.x[i];
-                vx[i] = dx;
-                vs[i] = bcast(sdec, 16 * w4 + i) * dx;
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sDt[wave][0][16 * w4 + 4 * i4]);
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sDt[wave][1][16 * w4 + 4 * i4]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float dx = d4[k] * st.x[4 * i4 + k];
+                    vx[4 * i4 + k] = dx;
+                    vs[4 * i4 + k] = s4[k] * dx;
+                }
             }
             store16_perm(&sXt[hw][lane * RSJ + 16 * w4], vx);
             store16_perm(&sXst[hw][lane * RSJ + 16 * w4], vs);
         }
         if (w4 == 0) {
-            sL[hw][lane] = lcum;
+            sL2[hw][lane] = (float)(lcum * 1.4426950408889634074);
             sE[hw][lane] = expf((float)lcum);
         }
         __syncthreads();
@@ -264,7 +279,7 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         // D'[j][t] = sum_n B[j][n] C[t][n]; lane owns column t = tb*32 + lo,
         // register r holds j = 32 jb + acc_row(r, hi).
         const int t_own = tb * 32 + lo;
-        const double l_t = sL[hw][t_own];
+        const float l_t = sL2[hw][t_own];
         bf16x8 mA[2][2];                        // [jb][half] A operands of G2
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
@@ -286,12 +301,17 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
                 av = an;
                 bv = bn;
             }
-            // M[t][j] = CB[t][j] exp(Lcum_t - Lcum_j), zero above the diagonal.
+            // M[t][j] = CB[t][j] exp(Lcum_t - Lcum_j), zero above the diagonal;
+            // registers 4q .. 4q+3 are rows j0 .. j0+3, one 16-byte read.
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int j = jb * 32 + acc_row(r, hi);
-                const float v = d[r];
-                d[r] = keep_if_le(v * exp2_diff(l_t, sL[hw][j]), j, t_own);
+            for (int q = 0; q < 4; ++q) {
+                const int j0 = jb * 32 + 8 * q + 4 * hi;
+                const f32x4 lj = *reinterpret_cast<const f32x4*>(&sL2[hw][j0]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float v = d[4 * q + k];
+                    d[4 * q + k] = keep_if_le(v * __builtin_amdgcn_exp2f(l_t - lj[k]), j0 + k, t_own);
+                }
             }
             mA[jb][0] = pack8(d, 0);
             mA[jb][1] = pack8(d, 8);
