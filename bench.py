@@ -57,6 +57,12 @@ def make_inputs(seed: int, dev):
     return x, dt, A, B, C, s0
 
 
+def as_storage(tensors, dtype):
+    """x, B and C rounded to a 16-bit storage type (io_dtype); dt, A, s0 stay fp32."""
+    x, dt, A, B, C, s0 = tensors
+    return x.to(dtype), dt, A, B.to(dtype), C.to(dtype), s0
+
+
 class Variant:
     def __init__(self, name, ctx, backend, tensors, env=None, multipass=True):
         self.name = name
@@ -231,6 +237,7 @@ def main():
         variants.append(Variant("bf16-tile", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_BF16_PASSC": "tile"}))
         variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
+        variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
 
     # Warm-up: W steps each, then alternate until the wall clock has run
     # warmup_ms (the reference's protocol against clock ramps).

@@ -358,6 +358,80 @@ HELIX_DEV typename RawReg<T>::type buf_raw(helix_rsrc r, int vidx, int sidx) {
 HELIX_DEV float raw_to_f32(float v) { return v; }
 HELIX_DEV float raw_to_f32(unsigned bits) { return __builtin_bit_cast(float, bits << 16); }
 
+// ---- caller storage types (helix_scan_desc.io_dtype) --------------------------
+// x, B, C and y are stored as IO = float, __bf16 or _Float16; dt, A and the
+// states are always fp32. Loads widen to fp32 exactly; stores round to
+// nearest even. Offsets are in elements.
+template <typename IO>
+HELIX_DEV float io_f32(unsigned short bits) {
+    if constexpr (__is_same(IO, __bf16))
+        return __builtin_bit_cast(float, (unsigned)bits << 16);
+    else
+        return (float)__builtin_bit_cast(_Float16, bits);
+}
+template <typename IO>
+HELIX_DEV float io_load(helix_rsrc r, int vidx, int sidx) {
+    if constexpr (sizeof(IO) == 4)
+        return buf_f32(r, vidx * 4, sidx * 4);
+    else
+        return io_f32<IO>(__builtin_bit_cast(unsigned short,
+                                             __builtin_amdgcn_raw_buffer_load_b16(r, vidx * 2, sidx * 2, 0)));
+}
+// An element kept in its storage form from its load to its use: fp32 stays a
+// float, a 16-bit type stays its loaded bits until io_widen. A loader that
+// widened at the load would make each load's consumer the next instruction,
+// and the loads would wait for each other one by one.
+template <typename IO> struct IoWord { typedef float type; };
+template <> struct IoWord<__bf16> { typedef unsigned type; };
+template <> struct IoWord<_Float16> { typedef unsigned type; };
+template <typename IO>
+HELIX_DEV typename IoWord<IO>::type io_load_word(helix_rsrc r, int vidx, int sidx) {
+    if constexpr (sizeof(IO) == 4)
+        return buf_f32(r, vidx * 4, sidx * 4);
+    else
+        return (unsigned)__builtin_bit_cast(unsigned short,
+                                            __builtin_amdgcn_raw_buffer_load_b16(r, vidx * 2, sidx * 2, 0));
+}
+template <typename IO>
+HELIX_DEV float io_widen(typename IoWord<IO>::type w) {
+    if constexpr (sizeof(IO) == 4)
+        return w;
+    else
+        return io_f32<IO>((unsigned short)w);
+}
+template <typename IO>
+HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
+    if constexpr (sizeof(IO) == 4) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff_bytes, soff_bytes, 0);
+    } else {
+        const IO h = (IO)v;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, h), r, voff_bytes, soff_bytes,
+                                              0);
+    }
+}
+// Eight consecutive elements starting at byte offset voff, widened to fp32:
+// two 16-byte loads for fp32, one for 16-bit storage.
+template <typename IO>
+HELIX_DEV void io_load8(helix_rsrc r, int voff, float (&o)[8]) {
+    if constexpr (sizeof(IO) == 4) {
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o[e] = as_f32(a[e]);
+            o[4 + e] = as_f32(b[e]);
+        }
+    } else {
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const unsigned w = a[e];
+            o[2 * e] = io_f32<IO>((unsigned short)(w & 0xffffu));
+            o[2 * e + 1] = io_f32<IO>((unsigned short)(w >> 16));
+        }
+    }
+}
+
 // Element store of v, as T (float, or rounded to __bf16); offsets in elements.
 template <typename T>
 HELIX_DEV void buf_store_elem(helix_rsrc r, float v, int vidx, int sidx) {

@@ -24,53 +24,76 @@
 //   x   tokens 16 wave + i (i < 16), channel p = lane
 //   B   tokens 16 wave + 8 hi + e (e < 8), state indices NB lo .. NB lo + NB-1,
 //       one 8/16/32-byte load per token (NB = NP/32 consecutive floats)
-template <int NP>
+// x and B stay in storage form until they are split (x6_b): the words of a
+// B run are kept as loaded, fp32 bits or two 16-bit values per word.
+template <int NP, typename IO>
 struct StageX6 {
+    static constexpr int BW = sizeof(IO) == 4 ? NP / 32 : NP / 64;   // words per B run
     float dtraw;
-    float x[16];
-    float b[8][NP / 32];
+    typename IoWord<IO>::type x[16];
+    unsigned b[8][BW];
 };
+
+// State index k of token e's B run, widened to fp32.
+template <int NP, typename IO>
+HELIX_DEV float x6_b(const StageX6<NP, IO>& st, int e, int k) {
+    if constexpr (sizeof(IO) == 4) {
+        return as_f32(st.b[e][k]);
+    } else {
+        const unsigned w = st.b[e][k >> 1];
+        return io_f32<IO>((unsigned short)((k & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+}
 
 // Rows are clamped to the last valid token, channels to the slab and state
 // indices to d_state, so every load is in bounds; nothing is masked (see the
 // staging comment in the kernel).
-template <int NP>
-__device__ __forceinline__ void load_stage_x6(StageX6<NP>& st, const HelixScanParams& p,
+// IO: the caller's storage type of x and B. A lane's run of NB state
+// indices is one 8/16/32-byte load in fp32 and one 4/8/16-byte load in 16-bit
+// storage.
+template <int NP, typename IO>
+__device__ __forceinline__ void load_stage_x6(StageX6<NP, IO>& st, const HelixScanParams& p,
                                               const float* __restrict__ dt_h,
-                                              const float* __restrict__ x_h,
-                                              const float* __restrict__ B_g, int c, int lane,
+                                              const IO* __restrict__ x_h,
+                                              const IO* __restrict__ B_g, int c, int lane,
                                               int wave, int pw, int N) {
+    constexpr int ES = (int)sizeof(IO);
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
     const int sb0 = sgpr_fresh((int)p.s_b[0]);
     const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
-    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
-    const helix_rsrc rb  = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0],
+                                     ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)ES);
+    const helix_rsrc rb  = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
     st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int jr = min(16 * wave + i, tlen - 1);
-        st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
+        st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
     }
     constexpr int NB = NP / 32;
     const int lo = lane & 31, hi = lane >> 5;
-    const int nb = min(NB * lo, N - NB) * 4;            // byte offset of the lane's run
+    const int nb = min(NB * lo, N - NB) * ES;           // byte offset of the lane's run
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int jr = min(16 * wave + 8 * hi + e, tlen - 1);
-        const int off = nb + jr * sb0 * 4;
-        if constexpr (NB == 2) {
+        const int off = nb + jr * sb0 * ES;
+        // The run's BW words: 4, 8, 16 or 32 bytes, in 16-byte loads at most.
+        constexpr int BW = StageX6<NP, IO>::BW;
+        if constexpr (BW == 1) {
+            st.b[e][0] = __builtin_amdgcn_raw_buffer_load_b32(rb, off, 0, 0);
+        } else if constexpr (BW == 2) {
             const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rb, off, 0, 0);
-            st.b[e][0] = as_f32(w[0]);
-            st.b[e][1] = as_f32(w[1]);
+            st.b[e][0] = w[0];
+            st.b[e][1] = w[1];
         } else {
 #pragma unroll
-            for (int q = 0; q < NB / 4; ++q) {
+            for (int q = 0; q < BW / 4; ++q) {
                 const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 16 * q, 0, 0);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) st.b[e][4 * q + k] = as_f32(w[k]);
+                for (int k = 0; k < 4; ++k) st.b[e][4 * q + k] = w[k];
             }
         }
     }
@@ -98,7 +121,8 @@ HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[1
 }
 
 // MODE as in pass_a.hip: 0 store R_c fp32, 1 store R_c bf16, 2 aggregates only.
-template <int NP, int MODE>
+// IO: the caller's storage type of x and B.
+template <int NP, int MODE, typename IO = float>
 __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr bool SBF = MODE == 1;
     constexpr int NTW = NP / 64;      // N tiles per wave
@@ -123,8 +147,8 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 
     const float A_h = b.A[(long long)h * p.s_a];
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
-    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
-    const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
+    const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
 
     const long long tile_off = state_tile_off(p, h, slab);
     const unsigned tile_elems = 64u * NP;
@@ -139,7 +163,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 
     // Two register stages in turn: the loads of chunk c+2 are issued while
     // chunks c and c+1 are processed (a copy between stages would wait on them).
-    auto step = [&](StageX6<NP>& st, int c) {
+    auto step = [&](StageX6<NP, IO>& st, int c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
 
@@ -157,7 +181,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         {
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bcast(cf, 16 * wave + i) * st.x[i];
+            for (int i = 0; i < 16; ++i) v[i] = bcast(cf, 16 * wave + i) * io_widen<IO>(st.x[i]);
             stage_split_row<HELIX_HD>(sXt, lane, 2 * wave, v);
         }
         // B^T rows NB lo + k, chunk 2 wave + hi (tokens 16 wave + 8 hi + e).
@@ -167,7 +191,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 unsigned w0, w1, w2;
-                split3_pair(st.b[2 * e][k], st.b[2 * e + 1][k], w0, w1, w2);
+                split3_pair(x6_b(st, 2 * e, k), x6_b(st, 2 * e + 1, k), w0, w1, w2);
                 q0[e] = w0;
                 q1[e] = w1;
                 q2[e] = w2;
@@ -203,7 +227,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 
         // This register stage is free again: chunk c+2's inputs travel while
         // this chunk's and the next one's GEMMs run.
-        if (c + 2 < c_end) load_stage_x6<NP>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
+        if (c + 2 < c_end) load_stage_x6<NP, IO>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
 
         const float a_c = expf((float)lend);
 #pragma unroll
@@ -233,9 +257,9 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         lam += (float)lend;
         __syncthreads();
     };
-    StageX6<NP> sa, sb;
-    load_stage_x6<NP>(sa, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
-    if (c_begin + 1 < c_end) load_stage_x6<NP>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
+    StageX6<NP, IO> sa, sb;
+    load_stage_x6<NP, IO>(sa, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
+    if (c_begin + 1 < c_end) load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
     for (int c = c_begin; c < c_end; c += 2) {
         step(sa, c);
         if (c + 1 < c_end) step(sb, c + 1);
@@ -269,6 +293,21 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         chunk_state_x6_impl<NP, 2>(p, b);                                                       \
     }
 
+// Aggregates from 16-bit storage of x and B (io_dtype BF16 / F16), for the
+// chunk-walking Pass C.
+#define HELIX_PASS_A_X6_IO(NP)                                                                  \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, __bf16>(p, b);                                               \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_f16io_n##NP(  \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, _Float16>(p, b);                                             \
+    }
+
 HELIX_PASS_A_X6(64)
 HELIX_PASS_A_X6(128)
 HELIX_PASS_A_X6(256)
+HELIX_PASS_A_X6_IO(64)
+HELIX_PASS_A_X6_IO(128)
+HELIX_PASS_A_X6_IO(256)

@@ -64,24 +64,29 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
 
 // Rows of C and B of one (seq, chunk, group) for this thread: row
 // wave + 4 i, columns lane + 64 m, clamped in bounds (masked when staged).
-template <int NP>
-__device__ __forceinline__ void load_cb_rows(float (&vc)[16][NP / 64], float (&vb)[16][NP / 64],
+// IO is the caller's storage type of B and C; the values stay in storage
+// form (io_widen at the use).
+template <int NP, typename IO = float>
+__device__ __forceinline__ void load_cb_rows(typename IoWord<IO>::type (&vc)[16][NP / 64],
+                                             typename IoWord<IO>::type (&vb)[16][NP / 64],
                                              const HelixScanParams& p, const HelixScanBuffers& b,
                                              int seq, int g, int t0, int tlen, int lane, int wave) {
     const int N = p.d_state;
     const int sc0 = (int)p.s_c[0], sb0 = (int)p.s_b[0];
-    const helix_rsrc rc = make_rsrc(b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0],
-                                    ((tlen - 1) * sc0 + N) * 4u);
-    const helix_rsrc rb = make_rsrc(b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0],
-                                    ((tlen - 1) * sb0 + N) * 4u);
+    const IO* C = reinterpret_cast<const IO*>(b.C);
+    const IO* B = reinterpret_cast<const IO*>(b.B);
+    const helix_rsrc rc = make_rsrc(C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0],
+                                    ((tlen - 1) * sc0 + N) * (unsigned)sizeof(IO));
+    const helix_rsrc rb = make_rsrc(B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0],
+                                    ((tlen - 1) * sb0 + N) * (unsigned)sizeof(IO));
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int jr = min(wave + 4 * i, tlen - 1);
 #pragma unroll
         for (int m = 0; m < NP / 64; ++m) {
             const int nc = min(lane + 64 * m, N - 1);
-            vc[i][m] = buf_elem<float>(rc, nc, jr * sc0);
-            vb[i][m] = buf_elem<float>(rb, nc, jr * sb0);
+            vc[i][m] = io_load_word<IO>(rc, nc, jr * sc0);
+            vb[i][m] = io_load_word<IO>(rb, nc, jr * sb0);
         }
     }
 }
@@ -89,28 +94,29 @@ __device__ __forceinline__ void load_cb_rows(float (&vc)[16][NP / 64], float (&v
 // Store one 32 x 32 output tile (t block tb, P block pb of the slab at p0) of
 // head h: lane (lo, hi), register r holds y[t = 32 tb + acc_row(r, hi)][32 pb + lo].
 // Rows past tlen and columns past the slab width are not written; with
-// tlen <= 0 nothing is (t0 must still address a row of y).
+// tlen <= 0 nothing is (t0 must still address a row of y). IO is the
+// caller's storage type of y.
+template <typename IO = float>
 __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanParams& p,
                                              const HelixScanBuffers& b, int seq, int h, int t0,
                                              int tlen, int p0, int pw, int tb, int pb, int lo, int hi) {
+    constexpr int ES = (int)sizeof(IO);
     const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
     // tlen <= 0 stores nothing: the resource's range is empty, so the range
     // check drops every store whatever its offset.
-    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u : 0u;
-    const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
-                                        (long long)p0 * p.s_y[2],
+    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * (unsigned)ES : 0u;
+    const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
+                                        (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                     bytes);
     const int pp = pb * 32 + lo;
-    const int voff = (4 * hi * sy0 + pp * sy2) * 4;
+    const int voff = (4 * hi * sy0 + pp * sy2) * ES;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int t = tb * 32 + acc_row(r, hi);
         // The element goes through a float value: a bit cast applied to a
         // vector element in place reads element 0 with this compiler.
         const float v = acc[r];
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ry,
-                                              store_off_if_lt(voff, t, tlen, pp, pw),
-                                              (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * 4, 0);
+        io_store<IO>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * ES);
     }
 }
 

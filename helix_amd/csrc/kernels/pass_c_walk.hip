@@ -41,24 +41,27 @@ HELIX_DEV int perm16(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1)
 
 // Per-chunk inputs prefetched a chunk ahead: dt for token `lane`, and x for
 // tokens 16 wave + i at channel p = lane.
+template <typename IO>
 struct StageW {
     float dtraw;
-    float x[16];
+    typename IoWord<IO>::type x[16];    // storage form
 };
 
-__device__ __forceinline__ void load_stage_w(StageW& st, const HelixScanParams& p,
+template <typename IO>
+__device__ __forceinline__ void load_stage_w(StageW<IO>& st, const HelixScanParams& p,
                                              const float* __restrict__ dt_h,
-                                             const float* __restrict__ x_h, int c, int lane,
+                                             const IO* __restrict__ x_h, int c, int lane,
                                              int wave, int pw) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
     const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
-    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0],
+                                     ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
     st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) st.x[i] = buf_elem<float>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
+    for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
 }
 
 // Eight bf16 K values from MFMA result registers r0 .. r0+7.
@@ -86,7 +89,8 @@ HELIX_DEV void store16_perm(__bf16* row, const float (&v)[16]) {
     *reinterpret_cast<bf16x8*>(row + 8) = b;
 }
 
-template <int NP>
+// IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
+template <int NP, typename IO = float>
 __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int HPW = HELIX_WALK_HPW(NP);   // heads per workgroup, four waves each
     constexpr int NW  = 4 * HPW;          // waves per workgroup
@@ -134,9 +138,10 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
 
     const float A_h = b.A[(long long)h * p.s_a];
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
-    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
-    const float* __restrict__ B_g  = b.B + seq * p.seq_b + g * p.s_b[1];
-    const float* __restrict__ C_g  = b.C + seq * p.seq_c + g * p.s_c[1];
+    constexpr int ES = (int)sizeof(IO);
+    const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
+    const IO* __restrict__ C_g = reinterpret_cast<const IO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
 
     const int tb = w4 >> 1, pb = w4 & 1;
     const int pp = pb * 32 + lo;                  // this lane's P column in the slab
@@ -169,8 +174,8 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
     const int jrow = RPW * wave + jj;
     const int jp = perm16(jrow);
 
-    StageW st;
-    load_stage_w(st, p, dt_h, x_h, c_begin, lane, w4, pw);
+    StageW<IO> st;
+    load_stage_w<IO>(st, p, dt_h, x_h, c_begin, lane, w4, pw);
 
     // The output tile of chunk c is stored after chunk c+1's B and C loads are
     // issued: the vmcnt counter completes in order and counts stores, so a
@@ -184,23 +189,24 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         // ---- B and C of this chunk (mostly from L2: a group's heads share them)
         {
             const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
-            const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
-            const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * 4u);
+            const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
+            const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * (unsigned)ES);
             const int jr = min(jrow, tlen - 1);
-            float vb[KQ][8], vc[KQ][8];
+            // bf16 storage: a run's eight elements are already MFMA operands
+            // and move to LDS as raw words; other types are widened to fp32
+            // and rounded to bf16 once.
+            constexpr bool RAW = __is_same(IO, __bf16);
+            float vb[RAW ? 1 : KQ][8], vc[RAW ? 1 : KQ][8];
+            u32x4 wb[RAW ? KQ : 1], wc[RAW ? KQ : 1];
 #pragma unroll
             for (int k = 0; k < KQ; ++k) {
                 const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
-                const u32x4 b0 = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4, 0, 0);
-                const u32x4 b1 = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4 + 16, 0, 0);
-                const u32x4 c0 = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4, 0, 0);
-                const u32x4 c1 = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4 + 16, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    vb[k][e] = as_f32(b0[e]);
-                    vb[k][4 + e] = as_f32(b1[e]);
-                    vc[k][e] = as_f32(c0[e]);
-                    vc[k][4 + e] = as_f32(c1[e]);
+                if constexpr (RAW) {
+                    wb[k] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * ES, 0, 0);
+                    wc[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * ES, 0, 0);
+                } else {
+                    io_load8<IO>(rb, (n0 + jr * sb0) * ES, vb[k]);
+                    io_load8<IO>(rc, (n0 + jr * sc0) * ES, vc[k]);
                 }
             }
             // Chunk c-1's tile (a full chunk: only the sequence's last chunk is
@@ -208,7 +214,7 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
             // state; on the first chunk no row is valid and the range check
             // drops the stores.
             const bool have_prev = c > c_begin;
-            store_y_tile(y_prev, p, b, seq, h, have_prev ? t0 - HELIX_CS : t0,
+            store_y_tile<IO>(y_prev, p, b, seq, h, have_prev ? t0 - HELIX_CS : t0,
                          (have_prev && head_ok) ? HELIX_CS : 0, p0, pw, tb, pb, lo, hi);
             // C is zeroed past tlen and d_state; that is all G1 and G3 need
             // (B rows past tlen only meet zero dtXs columns in G4).
@@ -218,12 +224,20 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
                 const int cpos = 16 * (q >> 1) + 4 * (q & 1);   // perm16 position of 8q; 8q+4 sits 8 further
                 const int j = jrow;
                 bf16x4 b_lo, b_hi, c_lo, c_hi;
+                if constexpr (RAW) {
+                    const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * q)) >> 31);
+                    b_lo = __builtin_bit_cast(bf16x4, u32x2{wb[k][0], wb[k][1]});
+                    b_hi = __builtin_bit_cast(bf16x4, u32x2{wb[k][2], wb[k][3]});
+                    c_lo = __builtin_bit_cast(bf16x4, u32x2{wc[k][0] & keep, wc[k][1] & keep});
+                    c_hi = __builtin_bit_cast(bf16x4, u32x2{wc[k][2] & keep, wc[k][3] & keep});
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    b_lo[e] = to_bf16(vb[k][e]);
-                    b_hi[e] = to_bf16(vb[k][4 + e]);
-                    c_lo[e] = to_bf16(keep_if_lt2(vc[k][e], j, tlen, 8 * q, N));
-                    c_hi[e] = to_bf16(keep_if_lt2(vc[k][4 + e], j, tlen, 8 * q, N));
+                    for (int e = 0; e < 4; ++e) {
+                        b_lo[e] = to_bf16(vb[k][e]);
+                        b_hi[e] = to_bf16(vb[k][4 + e]);
+                        c_lo[e] = to_bf16(keep_if_lt2(vc[k][e], j, tlen, 8 * q, N));
+                        c_hi[e] = to_bf16(keep_if_lt2(vc[k][4 + e], j, tlen, 8 * q, N));
+                    }
                 }
                 *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
                 *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos + 8]) = b_hi;
@@ -259,7 +273,7 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
                 const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sDt[wave][1][16 * w4 + 4 * i4]);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const float dx = d4[k] * st.x[4 * i4 + k];
+                    const float dx = d4[k] * io_widen<IO>(st.x[4 * i4 + k]);
                     vx[4 * i4 + k] = dx;
                     vs[4 * i4 + k] = s4[k] * dx;
                 }
@@ -273,7 +287,7 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         }
         __syncthreads();
 
-        if (c + 1 < c_end) load_stage_w(st, p, dt_h, x_h, c + 1, lane, w4, pw);
+        if (c + 1 < c_end) load_stage_w<IO>(st, p, dt_h, x_h, c + 1, lane, w4, pw);
 
         // ---- G1: CB^T tiles (jb, tb) for jb <= tb, kept as M^T ---------------
         // D'[j][t] = sum_n B[j][n] C[t][n]; lane owns column t = tb*32 + lo,
@@ -381,8 +395,8 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
     }
     {
         const int tl0  = (p.chunk_base + c_end - 1) * HELIX_CS;
-        store_y_tile(y_prev, p, b, seq, h, tl0, head_ok ? min(HELIX_CS, p.n_tok - tl0) : 0, p0, pw, tb, pb, lo,
-                     hi);
+        store_y_tile<IO>(y_prev, p, b, seq, h, tl0, head_ok ? min(HELIX_CS, p.n_tok - tl0) : 0, p0, pw, tb, pb,
+                         lo, hi);
     }
 }
 
@@ -392,6 +406,20 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         scan_walk_bf16_impl<NP>(p, b);                                                          \
     }
 
+// 16-bit storage of x, B, C and y (io_dtype BF16 / F16).
+#define HELIX_PASS_C_WALK_IO(NP)                                                                \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK_HPW(NP)) void helix_scan_walk_bf16_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk_bf16_impl<NP, __bf16>(p, b);                                                  \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK_HPW(NP)) void helix_scan_walk_bf16_f16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk_bf16_impl<NP, _Float16>(p, b);                                                \
+    }
+
 HELIX_PASS_C_WALK(64)
 HELIX_PASS_C_WALK(128)
 HELIX_PASS_C_WALK(256)
+HELIX_PASS_C_WALK_IO(64)
+HELIX_PASS_C_WALK_IO(128)
+HELIX_PASS_C_WALK_IO(256)

@@ -46,31 +46,32 @@ HELIX_DEV f32x4 zero4() {
 // c runs: dt of token `lane`, x of tokens 16 w + i at channel `lane`, and the
 // C and B rows wave + 4 i at columns lane + 64 m. Every address is clamped in
 // bounds; the masks are applied when the registers are staged into LDS.
-template <int NP>
+template <int NP, typename IO>
 struct StageS {
+    typedef typename IoWord<IO>::type W;    // x, C, B in storage form
     float dtraw;
-    float x[16];
-    float c[16][NP / 64];
-    float b[16][NP / 64];
+    W x[16];
+    W c[16][NP / 64];
+    W b[16][NP / 64];
 };
 
-template <int NP>
-__device__ __forceinline__ void load_stage_s(StageS<NP>& st, const HelixScanParams& p,
+template <int NP, typename IO>
+__device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScanParams& p,
                                              const HelixScanBuffers& b, const float* __restrict__ dt_h,
-                                             const float* __restrict__ x_h, int seq, int g, int t0,
+                                             const IO* __restrict__ x_h, int seq, int g, int t0,
                                              int tlen, int pw, int lane, int wave) {
     const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
     const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
-    const helix_rsrc rx =
-        make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    const helix_rsrc rx = make_rsrc(x_h + (long long)t0 * p.s_x[0],
+                                    ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
     st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int jr = min(16 * wave + i, tlen - 1);
-        st.x[i] = buf_elem<float>(rx, xc, jr * sx0);
+        st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
     }
-    load_cb_rows<NP>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
+    load_cb_rows<NP, IO>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
 }
 
 // G1 tile idx (0..9) of the causal 4 x 4 grid of 16 x 16 tiles, row-major
@@ -88,7 +89,8 @@ HELIX_DEV int tri_jb(int idx) {
 // stays on MFMA after folding every other decay into factors that never
 // exceed 1: C rows by exp(A_n cs_t) (G3), B rows by exp(A_n (cs_end - cs_j))
 // (G4), and the carried state by exp(A_n cs_end) per state index.
-template <int NP, bool DIAG>
+// IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
+template <int NP, bool DIAG, typename IO = float>
 __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int NT  = NP / 16;           // 16-row state tiles (all of them live in every wave)
     constexpr int RSC = NP + 4;            // C and B rows
@@ -127,7 +129,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             sA2[n] = n < N ? (double)b.A[(long long)h * p.s_a + n] * 1.4426950408889634074 : 0.0;
     }
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
-    const float* __restrict__ x_h  = b.x + seq * p.seq_x + h * p.s_x[1] + (long long)p0 * p.s_x[2];
+    const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] +
+                                 (long long)p0 * p.s_x[2];
 
     // State entering the sequence, s0[ids[seq]] in the caller's [P][N] rows
     // (s_s[1] == d_state): register r of tile nt holds n = 16 nt + 4 g4 + r,
@@ -149,8 +152,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
     const int n_ch = (p.n_tok + HELIX_CS - 1) / HELIX_CS;
     const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
-    StageS<NP> st;
-    load_stage_s<NP>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
+    StageS<NP, IO> st;
+    load_stage_s<NP, IO>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
 
     for (int c = 0; c < n_ch; ++c) {
         const int t0   = c * HELIX_CS;
@@ -172,7 +175,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int j = 16 * wave + i;
-            sX[j * RSX + lane] = keep_if_lt(bcast(dtv, j) * st.x[i], lane, pw);
+            sX[j * RSX + lane] = keep_if_lt(bcast(dtv, j) * io_widen<IO>(st.x[i]), lane, pw);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -180,16 +183,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
             for (int m = 0; m < NP / 64; ++m) {
                 const int n = lane + 64 * m;
-                sC[j * RSC + n] = keep_if_lt2(st.c[i][m], j, tlen, n, N);
-                sB[j * RSC + n] = keep_if_lt2(st.b[i][m], j, tlen, n, N);
+                sC[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.c[i][m]), j, tlen, n, N);
+                sB[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.b[i][m]), j, tlen, n, N);
             }
         }
         __syncthreads();
 
         // The next chunk's inputs travel while this one runs on the MFMA pipe.
         if (c + 1 < n_ch)
-            load_stage_s<NP>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS, min(HELIX_CS, p.n_tok - t0 - HELIX_CS),
-                             pw, lane, wave);
+            load_stage_s<NP, IO>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
+                                 min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
 
         // B operands of G2 (dtX) and G4 (dtX scaled by exp(L_end - Lcum_j); with
         // DIAG that decay goes into the B rows instead).
@@ -337,9 +340,10 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
         // ---- y rows t < tlen, channels < pw ---------------------------------
         {
-            const unsigned bytes = ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u;
-            const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
-                                                (long long)p0 * p.s_y[2],
+            constexpr int ES = (int)sizeof(IO);
+            const unsigned bytes = ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * (unsigned)ES;
+            const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
+                                                (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                             bytes);
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb)
@@ -347,8 +351,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 for (int r = 0; r < 4; ++r) {
                     const int t = 16 * tb + 4 * g4 + r;
                     const float v = ya[tb][r];
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        as_u32(v), ry, store_off_if_lt((t * sy0 + pc * sy2) * 4, t, tlen, pc, pw), 0, 0);
+                    io_store<IO>(ry, v, store_off_if_lt((t * sy0 + pc * sy2) * ES, t, tlen, pc, pw), 0);
                 }
         }
         __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX
@@ -373,6 +376,17 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         scan_1pass_impl<NP, false>(p, b);                                                       \
     }
 
+// 16-bit storage of x, B, C and y (io_dtype BF16 / F16), fp32 compute.
+#define HELIX_SCAN_1PASS_IO(NP)                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_bf16io_n##NP(        \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_1pass_impl<NP, false, __bf16>(p, b);                                               \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_f16io_n##NP(         \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_1pass_impl<NP, false, _Float16>(p, b);                                             \
+    }
+
 #define HELIX_SCAN_1PASS_DIAG(NP)                                                               \
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_diag_f32_n##NP(      \
         HelixScanParams p, HelixScanBuffers b) {                                                \
@@ -382,6 +396,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 HELIX_SCAN_1PASS(64)
 HELIX_SCAN_1PASS(128)
 HELIX_SCAN_1PASS(256)
+HELIX_SCAN_1PASS_IO(64)
+HELIX_SCAN_1PASS_IO(128)
+HELIX_SCAN_1PASS_IO(256)
 // d_state <= 128: the diagonal form keeps M in rows of its own.
 HELIX_SCAN_1PASS_DIAG(64)
 HELIX_SCAN_1PASS_DIAG(128)

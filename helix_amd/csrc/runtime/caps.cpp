@@ -136,6 +136,40 @@ const HelixMatmulTraits& pick_traits(int fam, int k) {
     return sets.t[x6][fam][k];
 }
 
+// 16-bit storage of x, B, C and y (io_dtype F16 or BF16; dt, A and the states
+// stay fp32). A bf16 multipass request walks segments in Pass C with Pass A's
+// aggregate kernel reading the 16-bit operands; every other request runs the
+// single-pass kernel with fp32 compute. [io: 0 bf16, 1 f16][0 walk, 1 single][np]
+struct IoTraitSets {
+    HelixMatmulTraits t[2][2][3];
+    std::string names[2][2][3], ka[2][3], kc[2][3], k1[2][3];
+    IoTraitSets() {
+        const char* io[2] = {"bf16", "f16"};
+        const int nps[3] = {64, 128, 256};
+        for (int i = 0; i < 2; ++i)
+            for (int k = 0; k < 3; ++k) {
+                const std::string np = std::to_string(nps[k]);
+                ka[i][k] = std::string("helix_chunk_state_x6agg_") + io[i] + "io_n" + np;
+                kc[i][k] = std::string("helix_scan_walk_bf16_") + io[i] + "io_n" + np;
+                k1[i][k] = std::string("helix_scan_1pass_") + io[i] + "io_n" + np;
+                names[i][0][k] = std::string("mfma bf16 pass C, chunk walk, pass A bf16x6, ") + io[i] +
+                                 " storage (d_state<=" + np + ")";
+                names[i][1][k] = std::string("mfma fp32, single pass, ") + io[i] + " storage (d_state<=" + np + ")";
+                t[i][0][k] = {HELIX_BACKEND_MPP, names[i][0][k].c_str(), ka[i][k].c_str(), "helix_state_scan_f32",
+                              kc[i][k].c_str(), true, "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)",
+                              "v_mfma_f32_32x32x16_bf16", nps[k], true, nullptr};
+                t[i][1][k] = {HELIX_BACKEND_SGMMA, names[i][1][k].c_str(), nullptr, nullptr, nullptr, false,
+                              "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", nps[k], false,
+                              k1[i][k].c_str()};
+            }
+    }
+};
+
+const HelixMatmulTraits& io_traits(helix_dtype io, bool walk, int k) {
+    static const IoTraitSets sets;
+    return sets.t[io == HELIX_F16 ? 1 : 0][walk ? 0 : 1][k];
+}
+
 const char* const kKernelNames[] = {
     "helix_chunk_state_x6f32_n64", "helix_chunk_state_x6f32_n128", "helix_chunk_state_x6f32_n256",
     "helix_chunk_state_x6sbf_n64", "helix_chunk_state_x6sbf_n128", "helix_chunk_state_x6sbf_n256",
@@ -150,6 +184,12 @@ const char* const kKernelNames[] = {
     "helix_scan_walk_bf16_n64",   "helix_scan_walk_bf16_n128",  "helix_scan_walk_bf16_n256",
     "helix_scan_1pass_f32_n64",   "helix_scan_1pass_f32_n128",  "helix_scan_1pass_f32_n256",
     "helix_scan_1pass_diag_f32_n64", "helix_scan_1pass_diag_f32_n128",
+    "helix_chunk_state_x6agg_bf16io_n64", "helix_chunk_state_x6agg_bf16io_n128", "helix_chunk_state_x6agg_bf16io_n256",
+    "helix_chunk_state_x6agg_f16io_n64",  "helix_chunk_state_x6agg_f16io_n128",  "helix_chunk_state_x6agg_f16io_n256",
+    "helix_scan_walk_bf16_bf16io_n64",    "helix_scan_walk_bf16_bf16io_n128",    "helix_scan_walk_bf16_bf16io_n256",
+    "helix_scan_walk_bf16_f16io_n64",     "helix_scan_walk_bf16_f16io_n128",     "helix_scan_walk_bf16_f16io_n256",
+    "helix_scan_1pass_bf16io_n64",        "helix_scan_1pass_bf16io_n128",        "helix_scan_1pass_bf16io_n256",
+    "helix_scan_1pass_f16io_n64",         "helix_scan_1pass_f16io_n128",         "helix_scan_1pass_f16io_n256",
 };
 
 int np_index(int d_state) {
@@ -199,6 +239,12 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
     (void)ctx;
     const int k = np_index(d.d_state);
     if (d.a_form == HELIX_A_DIAG_PER_CHANNEL) return kDiagTraits[k < 1 ? k : 1];
+    if (d.io_dtype != HELIX_F32) {
+        const char* f = std::getenv("HELIX_FORCE_BACKEND");
+        const bool bf16 = (d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP) &&
+                          !(f && f[0] == 's');
+        return io_traits(d.io_dtype, bf16 && d.multipass, k);
+    }
     if (!d.multipass) return kSingleTraits[k];
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
@@ -404,8 +450,16 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
     } else if (d->a_form != HELIX_A_SCALAR_PER_HEAD) {
         return false;
     }
-    // fp16/bf16 storage is not served; bf16 compute is chosen by backend.
-    if (d->io_dtype != HELIX_F32 || d->compute_dtype != HELIX_F32) return false;
+    // Storage of x/B/C/y in F32, F16 or BF16; compute_dtype stays F32 (the
+    // bf16 compute path is chosen by backend, reference caps.mm:126).
+    if (d->compute_dtype != HELIX_F32) return false;
+    if (d->io_dtype != HELIX_F32) {
+        if (d->io_dtype != HELIX_F16 && d->io_dtype != HELIX_BF16) return false;
+        // 16-bit storage with scalar A only; B and C rows are read as runs of
+        // eight elements, kept 4-byte aligned by even element strides.
+        if (d->a_form != HELIX_A_SCALAR_PER_HEAD) return false;
+        if ((d->s_b[0] | d->s_b[1] | d->seq_b | d->s_c[0] | d->s_c[1] | d->seq_c) & 1) return false;
+    }
     if (d->d_state % 8 != 0 || d->head_dim % 8 != 0) return false;
     if (d->d_state > HELIX_N_MAX) return false;
     // B, C rows and state rows are staged as contiguous d_state vectors.
@@ -421,8 +475,10 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
 }
 
 extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
-    // The single-pass walks (multipass = false, and diagonal A) use none.
-    if (!d || !d->multipass || d->a_form == HELIX_A_DIAG_PER_CHANNEL) return 0;
+    // The single-pass walks (multipass = false, diagonal A, 16-bit storage off
+    // the bf16 path) use none.
+    if (!d || !d->multipass) return 0;
+    if (helix::rt::select_traits(ctx, *d).k_single) return 0;
     return helix::rt::plan_multipass(*d, helix::rt::select_traits(ctx, *d)).total_bytes;
 }
 

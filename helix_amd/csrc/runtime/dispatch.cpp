@@ -21,6 +21,7 @@
 // runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
 // staging here, so there is nothing to launch before the group loop.
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -60,6 +61,15 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_ERR_INVALID_ARG;
     }
     params.has_ids = ids.buf ? 1 : 0;
+
+    // 16-bit storage: B and C rows are read as 16-byte runs of eight
+    // elements, which needs their bases 4-byte aligned (the gate keeps the
+    // strides even).
+    if (d->io_dtype != HELIX_F32 &&
+        ((reinterpret_cast<uintptr_t>(dptr(B)) | reinterpret_cast<uintptr_t>(dptr(C))) & 3)) {
+        set_error(ctx, "B and C must be 4-byte aligned with 16-bit storage");
+        return HELIX_ERR_INVALID_ARG;
+    }
 
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     auto fn = [&](const char* name) -> hipFunction_t {

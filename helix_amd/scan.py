@@ -14,11 +14,13 @@ import threading
 import torch
 
 from .abi import Context, HelixError
-from .desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_OK,
-                   HELIX_TENSOR_NULL, HelixScanDesc, HelixTensor)
+from .desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_F16,
+                   HELIX_F32, HELIX_OK, HELIX_TENSOR_NULL, HelixScanDesc, HelixTensor)
 
 BACKENDS = {"auto": HELIX_BACKEND_AUTO, "fp32": HELIX_BACKEND_SGMMA, "sgmma": HELIX_BACKEND_SGMMA,
             "bf16": HELIX_BACKEND_MPP, "mpp": HELIX_BACKEND_MPP}
+# Storage type of x, B, C and y (helix_scan_desc.io_dtype).
+IO_DTYPES = {torch.float32: HELIX_F32, torch.bfloat16: HELIX_BF16, torch.float16: HELIX_F16}
 
 _ctx_lock = threading.Lock()
 _contexts: dict[int, Context] = {}
@@ -72,6 +74,7 @@ def make_desc(x: torch.Tensor, dt: torch.Tensor, B: torch.Tensor, C: torch.Tenso
     d.s_dt[0], d.s_dt[1], d.seq_dt = sdt[1], sdt[2], sdt[0]
     d.s_s[0], d.s_s[1], d.s_s[2], d.seq_s = ss[1], ss[2], ss[3], ss[0]
     d.s_a = A.stride(0)
+    d.io_dtype = IO_DTYPES[x.dtype]
     d.chunk = 0
     d.backend = BACKENDS[backend]
     d.multipass = multipass
@@ -89,23 +92,31 @@ def ssd_scan(x: torch.Tensor, dt: torch.Tensor, A: torch.Tensor, B: torch.Tensor
     """Chunked SSD prefill scan on the MI355X kernels. Returns (y, s1).
 
     x [S,L,H,P], dt [S,L,H] (pre-softplus), A [H], B/C [S,L,G,N], s0 [S,H,P,N]
-    (zeros when None), ids int32 [S] (source state row per sequence). All fp32
-    on one gfx950 device. multipass=False runs the single-pass kernel (fp32,
+    (zeros when None), ids int32 [S] (source state row per sequence), on one
+    gfx950 device. x, B, C and y are float32, bfloat16 or float16 (one type);
+    dt, A and the states are float32. multipass=False runs the single-pass kernel (fp32,
     no scratch; backend "bf16" is then declined). Raises HelixError when the
     shape is declined.
     """
     dev = x.device
     if dev.type != "cuda":
         raise ValueError("ssd_scan runs on a HIP device; got " + str(dev))
-    for name, t in (("x", x), ("dt", dt), ("A", A), ("B", B), ("C", C)):
-        if t.dtype != torch.float32 or t.device != dev:
-            raise ValueError(f"{name} must be float32 on {dev}")
+    # x, B, C (and y) share one storage type: float32, bfloat16 or float16;
+    # dt, A and the states are float32.
+    if x.dtype not in IO_DTYPES:
+        raise ValueError(f"x must be float32, bfloat16 or float16; got {x.dtype}")
+    for name, t, want in (("x", x, x.dtype), ("dt", dt, torch.float32), ("A", A, torch.float32),
+                          ("B", B, x.dtype), ("C", C, x.dtype)):
+        if t.dtype != want or t.device != dev:
+            raise ValueError(f"{name} must be {want} on {dev}")
     S, L, H, P = x.shape
     G, N = B.shape[2], B.shape[3]
     if s0 is None:
         s0 = torch.zeros((S, H, P, N), dtype=torch.float32, device=dev)
     if y is None:
-        y = torch.empty((S, L, H, P), dtype=torch.float32, device=dev)
+        y = torch.empty((S, L, H, P), dtype=x.dtype, device=dev)
+    elif y.dtype != x.dtype:
+        raise ValueError(f"y must be {x.dtype}")
     if s1 is None:
         s1 = torch.empty((S, H, P, N), dtype=torch.float32, device=dev)
     if ids is not None and (ids.dtype != torch.int32 or not ids.is_contiguous()):

@@ -139,7 +139,7 @@ typedef struct {
 
     int32_t       chunk;          /* 0 => library chooses (64); else must be 64 */
     helix_a_form  a_form;
-    helix_dtype   io_dtype;       /* storage of x/B/C/y; F32 only               */
+    helix_dtype   io_dtype;       /* storage of x/B/C/y: F32, F16 or BF16       */
     helix_dtype   compute_dtype;  /* must stay F32; bf16 is chosen by backend   */
     helix_backend backend;
     bool          multipass;      /* 3-pass chunk-parallel decomposition        */

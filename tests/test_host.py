@@ -19,7 +19,7 @@ import pytest
 
 from helix_amd import abi
 from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_REF,
-                            HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_ERR_INVALID_ARG,
+                            HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_F16, HELIX_ERR_INVALID_ARG,
                             HELIX_ERR_NO_DEVICE, HELIX_ERR_SCRATCH_TOO_SMALL,
                             HELIX_ERR_UNSUPPORTED_SHAPE, HELIX_A_DIAG_PER_CHANNEL,
                             HELIX_TENSOR_NULL, HelixScanDesc, HelixTensor, algorithmic_bytes,
@@ -128,7 +128,11 @@ def _declined(host, mutate):
      lambda d: (setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL), setattr(d, "d_state", 256),
                 d.s_s.__setitem__(1, 256))),
     ("unknown A form", lambda d: setattr(d, "a_form", 7)),
-    ("bf16 storage", lambda d: setattr(d, "io_dtype", HELIX_BF16)),
+    ("bf16 storage with diagonal A",
+     lambda d: (setattr(d, "io_dtype", HELIX_BF16), setattr(d, "a_form", HELIX_A_DIAG_PER_CHANNEL))),
+    ("bf16 storage with an odd B row stride",
+     lambda d: (setattr(d, "io_dtype", HELIX_BF16), d.s_b.__setitem__(0, 2 * 128 + 1))),
+    ("unknown storage type", lambda d: setattr(d, "io_dtype", 5)),
     ("bf16 compute dtype", lambda d: setattr(d, "compute_dtype", HELIX_BF16)),
     ("d_state not a multiple of 8", lambda d: setattr(d, "d_state", 60)),
     ("head_dim not a multiple of 8", lambda d: setattr(d, "head_dim", 60)),
@@ -175,6 +179,38 @@ def test_diagonal_a_runs_the_single_pass_walk(host):
                 k = host.plan_info(d)
                 assert k.kernel_1pass == b"helix_scan_1pass_diag_f32_n%d" % want
                 assert (k.launches, k.total_bytes, k.kernel_a) == (1, 0, None)
+
+
+@pytest.mark.parametrize("io,name", [(HELIX_BF16, "bf16"), (HELIX_F16, "f16")])
+def test_16bit_storage_selection(host, io, name):
+    # 16-bit x/B/C/y: a bf16 multipass request walks segments (Pass A's
+    # aggregate and the walking Pass C read 16-bit operands); everything else
+    # runs the single pass with fp32 compute and no scratch.
+    shape = CONFIG_SHAPES["cfg2"]
+    d = mp(shape)
+    d.io_dtype = io
+    assert host.supported(d)
+    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
+    k = host.plan_info(d)
+    assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
+        f"helix_chunk_state_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_scan_walk_bf16_{name}io_n128".encode())
+    assert k.total_bytes == host.scratch_size(d) > 0 and k.s_local_bytes == 0
+    with env(HELIX_BF16_PASSC="tile"):     # only the walk reads 16-bit operands
+        assert host.plan_info(d).kernel_c == f"helix_scan_walk_bf16_{name}io_n128".encode()
+    for backend, multipass in ((HELIX_BACKEND_SGMMA, True), (HELIX_BACKEND_AUTO, False),
+                               (HELIX_BACKEND_SGMMA, False)):
+        d = mp((300, 2, 4, 64, 256, 2), backend)
+        d.multipass = multipass
+        d.io_dtype = io
+        assert host.supported(d)
+        assert host.backend_desc(d) == f"mfma fp32, single pass, {name} storage (d_state<=256)"
+        assert host.scratch_size(d) == 0
+        assert host.plan_info(d).kernel_1pass == f"helix_scan_1pass_{name}io_n256".encode()
+    with env(HELIX_FORCE_BACKEND="sgmma"):
+        d = mp(shape)
+        d.io_dtype = io
+        assert host.plan_info(d).kernel_1pass == f"helix_scan_1pass_{name}io_n128".encode()
 
 
 def test_null_context_and_desc():
