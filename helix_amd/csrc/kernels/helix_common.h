@@ -399,14 +399,20 @@ HELIX_DEV float io_widen(typename IoWord<IO>::type w) {
     else
         return io_f32<IO>((unsigned short)w);
 }
-template <typename IO>
+// Cache policy of a buffer access (the instruction's aux operand): 0 is the
+// default; HELIX_NT marks it non-temporal. y is written once and never read
+// back by the scan: storing it non-temporal keeps it from displacing the
+// inputs still being read, which measured 15-25% faster on the walking
+// Pass C at config 2.
+#define HELIX_NT 2
+template <typename IO, int AUX = 0>
 HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
     if constexpr (sizeof(IO) == 4) {
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff_bytes, soff_bytes, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff_bytes, soff_bytes, AUX);
     } else {
         const IO h = (IO)v;
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, h), r, voff_bytes, soff_bytes,
-                                              0);
+                                              AUX);
     }
 }
 // Eight consecutive elements starting at byte offset voff, widened to fp32:

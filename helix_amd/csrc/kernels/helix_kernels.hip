@@ -8,4 +8,5 @@
 #include "pass_c_bf16.hip"
 #include "pass_c_x6.hip"
 #include "pass_c_walk.hip"
+#include "pass_c_walk16.hip"
 #include "pass_single.hip"

@@ -61,6 +61,10 @@
  * two up to d_state 128; one at 256, where a head's state needs the whole
  * register budget of a wave. */
 #define HELIX_WALK_HPW(np) ((np) <= 128 ? 2 : 1)
+/* Heads per workgroup of the 16 x 16 tile walk: as for the 32 x 32 walk (one
+ * head per workgroup, two workgroups per CU, measured slower at config 2:
+ * the B and C staging is then done for every head). */
+#define HELIX_WALK16_HPW(np) HELIX_WALK_HPW(np)
 
 typedef struct HelixScanParams {
     int n_tok;

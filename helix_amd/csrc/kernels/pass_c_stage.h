@@ -95,7 +95,7 @@ __device__ __forceinline__ void load_cb_rows(typename IoWord<IO>::type (&vc)[16]
 // head h: lane (lo, hi), register r holds y[t = 32 tb + acc_row(r, hi)][32 pb + lo].
 // Rows past tlen and columns past the slab width are not written; with
 // tlen <= 0 nothing is (t0 must still address a row of y). IO is the
-// caller's storage type of y.
+// caller's storage type of y; the stores are non-temporal.
 template <typename IO = float>
 __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanParams& p,
                                              const HelixScanBuffers& b, int seq, int h, int t0,
@@ -116,7 +116,7 @@ __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanP
         // The element goes through a float value: a bit cast applied to a
         // vector element in place reads element 0 with this compiler.
         const float v = acc[r];
-        io_store<IO>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * ES);
+        io_store<IO, HELIX_NT>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * ES);
     }
 }
 

@@ -64,6 +64,48 @@ __device__ __forceinline__ void load_stage_w(StageW<IO>& st, const HelixScanPara
     for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
 }
 
+// This lane's B and C runs of one chunk, as loaded: KQ runs of eight state
+// indices of row jrow, each two 16-byte words in fp32 storage or one in
+// 16-bit storage. Loaded a chunk ahead and widened only when staged.
+template <int KQ, typename IO>
+struct RunsW {
+    static constexpr int WPR = sizeof(IO) == 4 ? 2 : 1;
+    u32x4 b[KQ][WPR], c[KQ][WPR];
+};
+
+template <int KQ, int QPI, typename IO>
+__device__ __forceinline__ void load_runs_w(RunsW<KQ, IO>& r, const HelixScanParams& p,
+                                            const IO* __restrict__ B_g, const IO* __restrict__ C_g,
+                                            int c, int N, int jrow, int qq) {
+    constexpr int ES = (int)sizeof(IO);
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
+    const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
+    const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * (unsigned)ES);
+    const int jr = min(jrow, tlen - 1);
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+        const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
+#pragma unroll
+        for (int w = 0; w < RunsW<KQ, IO>::WPR; ++w) {
+            r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * ES + 16 * w, 0, 0);
+            r.c[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * ES + 16 * w, 0, 0);
+        }
+    }
+}
+
+// Element e (0..7) of a run, widened to fp32.
+template <typename IO, int WPR>
+HELIX_DEV float run_elem(const u32x4 (&w)[WPR], int e) {
+    if constexpr (sizeof(IO) == 4) {
+        return as_f32(w[e >> 2][e & 3]);
+    } else {
+        const unsigned v = w[0][e >> 1];
+        return io_f32<IO>((unsigned short)((e & 1) ? (v >> 16) : (v & 0xffffu)));
+    }
+}
+
 // Eight bf16 K values from MFMA result registers r0 .. r0+7.
 HELIX_DEV bf16x8 pack8(const f32x16& v, int r0) {
     bf16x8 o;
@@ -176,6 +218,8 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
 
     StageW<IO> st;
     load_stage_w<IO>(st, p, dt_h, x_h, c_begin, lane, w4, pw);
+    RunsW<KQ, IO> runs;
+    load_runs_w<KQ, QPI, IO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
 
     // The output tile of chunk c is stored after chunk c+1's B and C loads are
     // issued: the vmcnt counter completes in order and counts stores, so a
@@ -186,57 +230,40 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
 
-        // ---- B and C of this chunk (mostly from L2: a group's heads share them)
+        // ---- B and C of this chunk, loaded during the previous one ---------
         {
-            const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
-            const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
-            const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * (unsigned)ES);
-            const int jr = min(jrow, tlen - 1);
-            // bf16 storage: a run's eight elements are already MFMA operands
-            // and move to LDS as raw words; other types are widened to fp32
-            // and rounded to bf16 once.
-            constexpr bool RAW = __is_same(IO, __bf16);
-            float vb[RAW ? 1 : KQ][8], vc[RAW ? 1 : KQ][8];
-            u32x4 wb[RAW ? KQ : 1], wc[RAW ? KQ : 1];
-#pragma unroll
-            for (int k = 0; k < KQ; ++k) {
-                const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
-                if constexpr (RAW) {
-                    wb[k] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * ES, 0, 0);
-                    wc[k] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * ES, 0, 0);
-                } else {
-                    io_load8<IO>(rb, (n0 + jr * sb0) * ES, vb[k]);
-                    io_load8<IO>(rc, (n0 + jr * sc0) * ES, vc[k]);
-                }
-            }
             // Chunk c-1's tile (a full chunk: only the sequence's last chunk is
             // ragged). Unconditional, so every path has the same counter
             // state; on the first chunk no row is valid and the range check
-            // drops the stores.
+            // drops the stores. The runs were loaded before these stores, so
+            // waiting for them does not wait for the stores.
             const bool have_prev = c > c_begin;
             store_y_tile<IO>(y_prev, p, b, seq, h, have_prev ? t0 - HELIX_CS : t0,
                          (have_prev && head_ok) ? HELIX_CS : 0, p0, pw, tb, pb, lo, hi);
             // C is zeroed past tlen and d_state; that is all G1 and G3 need
-            // (B rows past tlen only meet zero dtXs columns in G4).
+            // (B rows past tlen only meet zero dtXs columns in G4). With bf16
+            // storage a run's elements are already MFMA operands.
+            constexpr bool RAW = __is_same(IO, __bf16);
 #pragma unroll
             for (int k = 0; k < KQ; ++k) {
                 const int q = qq + QPI * k;
                 const int cpos = 16 * (q >> 1) + 4 * (q & 1);   // perm16 position of 8q; 8q+4 sits 8 further
                 const int j = jrow;
+                const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * q)) >> 31);
                 bf16x4 b_lo, b_hi, c_lo, c_hi;
                 if constexpr (RAW) {
-                    const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * q)) >> 31);
-                    b_lo = __builtin_bit_cast(bf16x4, u32x2{wb[k][0], wb[k][1]});
-                    b_hi = __builtin_bit_cast(bf16x4, u32x2{wb[k][2], wb[k][3]});
-                    c_lo = __builtin_bit_cast(bf16x4, u32x2{wc[k][0] & keep, wc[k][1] & keep});
-                    c_hi = __builtin_bit_cast(bf16x4, u32x2{wc[k][2] & keep, wc[k][3] & keep});
+                    b_lo = __builtin_bit_cast(bf16x4, u32x2{runs.b[k][0][0], runs.b[k][0][1]});
+                    b_hi = __builtin_bit_cast(bf16x4, u32x2{runs.b[k][0][2], runs.b[k][0][3]});
+                    c_lo = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][0] & keep, runs.c[k][0][1] & keep});
+                    c_hi = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][2] & keep, runs.c[k][0][3] & keep});
                 } else {
+                    constexpr int WPR = RunsW<KQ, IO>::WPR;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        b_lo[e] = to_bf16(vb[k][e]);
-                        b_hi[e] = to_bf16(vb[k][4 + e]);
-                        c_lo[e] = to_bf16(keep_if_lt2(vc[k][e], j, tlen, 8 * q, N));
-                        c_hi[e] = to_bf16(keep_if_lt2(vc[k][4 + e], j, tlen, 8 * q, N));
+                        b_lo[e] = to_bf16(run_elem<IO, WPR>(runs.b[k], e));
+                        b_hi[e] = to_bf16(run_elem<IO, WPR>(runs.b[k], 4 + e));
+                        c_lo[e] = to_bf16(as_f32(as_u32(run_elem<IO, WPR>(runs.c[k], e)) & keep));
+                        c_hi[e] = to_bf16(as_f32(as_u32(run_elem<IO, WPR>(runs.c[k], 4 + e)) & keep));
                     }
                 }
                 *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
@@ -287,7 +314,13 @@ __device__ __forceinline__ void scan_walk_bf16_impl(const HelixScanParams& p, co
         }
         __syncthreads();
 
-        if (c + 1 < c_end) load_stage_w<IO>(st, p, dt_h, x_h, c + 1, lane, w4, pw);
+        // The next chunk's inputs travel while this one computes. On the last
+        // chunk the same chunk is loaded again, so the loop has no branch.
+        {
+            const int cn = min(c + 1, c_end - 1);
+            load_stage_w<IO>(st, p, dt_h, x_h, cn, lane, w4, pw);
+            load_runs_w<KQ, QPI, IO>(runs, p, B_g, C_g, cn, N, jrow, qq);
+        }
 
         // ---- G1: CB^T tiles (jb, tb) for jb <= tb, kept as M^T ---------------
         // D'[j][t] = sum_n B[j][n] C[t][n]; lane owns column t = tb*32 + lo,

@@ -1,0 +1,467 @@
+// pass_c_walk16.hip -- the chunk-walking bf16 Pass C on 16 x 16 x 32 MFMA tiles.
+//
+// Same contract as the 32 x 32 walk (pass_c_walk.hip): one workgroup owns
+// (seq, segment, HELIX_WALK_HPW heads of one B/C group, 64-wide P slab),
+// starts each head from S_seg (fp32, Pass B) and walks the segment's chunks,
+// producing per chunk
+//     y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C R)        (G1, G2, G3)
+//     R <- exp(L_end) R + B^T . (decay . dt . x)                  (G4)
+// on bf16 operands with fp32 accumulation (reference counterpart:
+// helix_chunk_out_mpp_impl, src/kernels/mpp/helix_scan_mpp.metal:54-232).
+//
+// Work split. The four waves of a head each own a 16-column P block
+// (p = 16 w4 + lane%16) for all 64 tokens, so no product is computed twice:
+//   - R[n][p] for the wave's 16 columns lives in registers, NP/16 result tiles
+//     of v_mfma_f32_16x16x32_bf16: register r of tile nb holds
+//     R[16 nb + 4 (lane/16) + r][p];
+//   - G3 (C R) and G4 (B^T dtXs) run on those tiles; G2 (M dtX) on the
+//     wave's columns;
+//   - G1 (C B^T and its decay mask) is split over the head's waves by 16 x 16
+//     block (ten blocks on or below the diagonal) and shared through LDS as
+//     M[t][j] in bf16.
+// An MFMA's 32 K slots may hold any 32 indices as long as both operands use
+// the same ones. A lane of the 16x16x32 layout supplies K slots 8 (lane/16)
+// .. +7; R's result registers give lane q state rows 4q .. 4q+3 of two
+// consecutive tiles, so within each group of 32 state indices, index
+// 16 h + 4 q + r sits at K position 8 q + 4 h + r (perm32) in every
+// n-contiguous operand (C and B rows in LDS), and R feeds G3 straight from
+// its registers.
+//
+// LDS (bf16, rows padded by 8): C[t][n], B[j][n] (perm32 order), B^T[n][j],
+// and per head dtX^T[p][j] (two buffers, by chunk parity), dtXs^T[p][j] and
+// M[t][j] (natural j order).
+#include "helix_common.h"
+
+#include "pass_c_stage.h"
+
+HELIX_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// K position of state index i inside its group of 32: 16 h + 4 q + r -> 8 q + 4 h + r.
+HELIX_DEV int perm32(int i) {
+    return (i & ~31) | (8 * ((i >> 2) & 3) + 4 * ((i >> 4) & 1) + (i & 3));
+}
+
+// G1 block idx (0..9) of the lower triangle of the 4 x 4 grid of 16 x 16
+// blocks, in the order (jb, tb) = (0,0) (0,1) (1,1) (0,2) (1,2) (2,2) (0,3) ...
+HELIX_DEV int g1_tb(int idx) { return (idx >= 1) + (idx >= 3) + (idx >= 6); }
+HELIX_DEV int g1_jb(int idx) {
+    const int tb = g1_tb(idx);
+    return idx - tb * (tb + 1) / 2;
+}
+
+// x of tokens 16 wave + i at channel p = lane and dt of token lane, prefetched
+// a chunk ahead in storage form.
+template <typename IO>
+struct StageW16 {
+    float dtraw;
+    typename IoWord<IO>::type x[16];
+};
+
+template <typename IO>
+__device__ __forceinline__ void load_stage_w16(StageW16<IO>& st, const HelixScanParams& p,
+                                               const float* __restrict__ dt_h,
+                                               const IO* __restrict__ x_h, int c, int lane,
+                                               int wave, int pw) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0],
+                                     ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
+    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    const int xc = min(lane, pw - 1) * sx2;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
+}
+
+// This lane's B and C runs of one chunk, as loaded: KQ runs of eight state
+// indices of row jrow, two 16-byte words each in fp32 storage, one in 16-bit.
+template <int KQ, typename IO>
+struct RunsW16 {
+    static constexpr int WPR = sizeof(IO) == 4 ? 2 : 1;
+    u32x4 b[KQ][WPR], c[KQ][WPR];
+};
+
+template <int KQ, int QPI, typename IO>
+__device__ __forceinline__ void load_runs_w16(RunsW16<KQ, IO>& r, const HelixScanParams& p,
+                                              const IO* __restrict__ B_g, const IO* __restrict__ C_g,
+                                              int c, int N, int jrow, int qq) {
+    constexpr int ES = (int)sizeof(IO);
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
+    const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
+    const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * (unsigned)ES);
+    const int jr = min(jrow, tlen - 1);
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+        const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
+#pragma unroll
+        for (int w = 0; w < RunsW16<KQ, IO>::WPR; ++w) {
+            r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * ES + 16 * w, 0, 0);
+            r.c[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * ES + 16 * w, 0, 0);
+        }
+    }
+}
+
+// Element e (0..7) of a run, widened to fp32.
+template <typename IO, int WPR>
+HELIX_DEV float run16_elem(const u32x4 (&w)[WPR], int e) {
+    if constexpr (sizeof(IO) == 4) {
+        return as_f32(w[e >> 2][e & 3]);
+    } else {
+        const unsigned v = w[0][e >> 1];
+        return io_f32<IO>((unsigned short)((e & 1) ? (v >> 16) : (v & 0xffffu)));
+    }
+}
+
+// Sixteen consecutive tokens' values of one row, in natural order.
+HELIX_DEV void store16_nat(__bf16* row, const float (&v)[16]) {
+    bf16x8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[e] = to_bf16(v[e]);
+        b[e] = to_bf16(v[8 + e]);
+    }
+    *reinterpret_cast<bf16x8*>(row) = a;
+    *reinterpret_cast<bf16x8*>(row + 8) = b;
+}
+
+// Store the wave's y tile of one chunk: acc[tb] register r holds
+// y[t = 16 tb + 4 q + r][pp]. Rows past tlen and columns past the slab width
+// are dropped by the range check; with tlen <= 0 nothing is stored.
+template <typename IO>
+__device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScanParams& p,
+                                          const HelixScanBuffers& b, int seq, int h, int t0, int tlen,
+                                          int p0, int pw, int pp, int q) {
+    constexpr int ES = (int)sizeof(IO);
+    const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
+    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * (unsigned)ES : 0u;
+    const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
+                                        (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
+                                    bytes);
+    const int voff = (4 * q * sy0 + pp * sy2) * ES;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * q + r;
+            const float v = acc[tb][r];
+            io_store<IO, HELIX_NT>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (16 * tb + r) * sy0 * ES);
+        }
+}
+
+// IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
+template <int NP, int HPW, typename IO = float>
+__device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    constexpr int NW  = 4 * HPW;              // HPW heads per workgroup, four waves each
+    constexpr int NB  = NP / 16;              // 16-row state tiles of R
+    constexpr int KS  = NP / 32;              // K steps over the state
+    constexpr int NT32 = NP / 32;             // 32 x 32 tiles of the slab tile layout
+    constexpr int RS  = NP + 8;               // bf16 row stride of C[t][n], B[j][n]
+    constexpr int RSJ = HELIX_CS + 8;         // bf16 row stride of B^T, dtX^T, dtXs^T, M
+    constexpr int NCH = NP / 8;               // 8-element runs per C / B row
+
+    // M takes the place of B's rows when they fit (B is dead once G1 has read
+    // it): G1 then keeps its blocks in registers until every wave is past
+    // its B reads.
+    constexpr bool M_IN_B = HPW * HELIX_CS * RSJ <= HELIX_CS * RS;
+    constexpr int MB = M_IN_B ? 0 : HPW * HELIX_CS * RSJ;
+    __shared__ __attribute__((aligned(16))) __bf16 sC[HELIX_CS * RS];
+    __shared__ __attribute__((aligned(16))) __bf16 sB[HELIX_CS * RS];
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[NP * RSJ];
+    __shared__ __attribute__((aligned(16))) __bf16 sXt[2][HPW][HELIX_HD * RSJ];   // by chunk parity
+    __shared__ __attribute__((aligned(16))) __bf16 sXst[HPW][HELIX_HD * RSJ];
+    __shared__ __attribute__((aligned(16))) __bf16 sMown[MB > 0 ? MB : 8];
+    __bf16* const sM = M_IN_B ? sB : sMown;      // head slot hw at sM + hw * HELIX_CS * RSJ
+    __shared__ __attribute__((aligned(16))) float sL2[HPW][HELIX_CS];   // Lcum_t log2(e)
+    __shared__ __attribute__((aligned(16))) float sE[HPW][HELIX_CS];    // exp(Lcum_t)
+    __shared__ __attribute__((aligned(16))) float sDt[NW][2][HELIX_CS];  // per wave: dt_j, decay_j
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = wave_uniform();
+    const int c16 = lane & 15, q = lane >> 4;
+    const int hw = wave >> 2, w4 = wave & 3;      // head slot in the workgroup, P block within it
+    const int N = p.d_state, P = p.head_dim;
+    const int hpg = p.heads_per_group;
+    const int npair = (hpg + HPW - 1) / HPW;
+
+    // 1-D grid, a group's head blocks consecutive in the logical order so they
+    // share an XCD (and the chunk's B and C in its L2).
+    const unsigned total = (unsigned)(p.n_seg * p.n_group * npair * p.n_pslab * p.n_seq);
+    unsigned wid = xcd_logical_id(blockIdx.x, total);
+    const int pair = (int)(wid % (unsigned)npair);   wid /= (unsigned)npair;
+    const int seg  = (int)(wid % (unsigned)p.n_seg); wid /= (unsigned)p.n_seg;
+    const int g    = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
+    const int slab = (int)(wid % (unsigned)p.n_pslab);
+    const int seq  = (int)(wid / (unsigned)p.n_pslab);
+    // A workgroup of the last block may have fewer heads than HPW: its spare
+    // waves walk the block's last head again and store nothing.
+    const int hslot = HPW * pair + hw;
+    const bool head_ok = hslot < hpg;
+    const int h  = g * hpg + min(hslot, hpg - 1);
+    const int p0 = slab * HELIX_HD;
+    const int pw = min(HELIX_HD, P - p0);
+
+    const int c_begin = seg * p.seg_len;
+    const int c_end   = min(c_begin + p.seg_len, p.n_cg);
+    if (c_begin >= c_end) return;
+
+    const float A_h = b.A[(long long)h * p.s_a];
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
+    const IO* __restrict__ C_g = reinterpret_cast<const IO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
+
+    const int pp = 16 * w4 + c16;                 // this lane's P column in the slab
+
+    // R[n][pp], n = 16 nb + 4 q + r, from the slab tile of S_seg(s): in the
+    // tile's unit layout that is unit ((pt NT32 + nb/2) 4 + r4) 64 + lane'
+    // with pt = w4/2, r4 = 2 (nb%2) + q/2, lane' = 32 (q%2) + 16 (w4%2) + c16.
+    f32x4 R[NB];
+    {
+        const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + state_tile_off(p, h, slab);
+        const helix_rsrc rg = make_rsrc(sg, 64u * NP * sizeof(float));
+        const int vunit = 64 * (q >> 1) + 32 * (q & 1) + 16 * (w4 & 1) + c16;
+        const int pt = w4 >> 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            R[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
+    }
+
+    __bf16* const sMh = sM + hw * (HELIX_CS * RSJ);
+    // M blocks (jb, tb) = (1, 0) and (3, 2) lie above the diagonal but inside
+    // the 32-wide K steps G2 reads: zero. Written once, or with every chunk's
+    // M when M shares B's rows.
+    const int zoff = [&] {
+        const int e2 = 2 * (64 * w4 + lane);      // 0 .. 510: 32 rows x 16 columns
+        const int row = e2 >> 4, col = e2 & 15;
+        const int t = row < 16 ? row : row + 16;
+        const int j = row < 16 ? 16 + col : 48 + col;
+        return t * RSJ + j;
+    }();
+    if constexpr (!M_IN_B) *reinterpret_cast<unsigned*>(&sMh[zoff]) = 0u;
+
+    // B and C are staged once for the workgroup's heads. All NW waves share
+    // the 64 rows, RPW each: lane (jj = lane % RPW, qq = lane / RPW) holds
+    // state indices 8u .. 8u+7, u = qq + (64/RPW) k, of row RPW wave + jj.
+    constexpr int RPW = HELIX_CS / NW;
+    constexpr int QPI = 64 / RPW;                 // runs per wave instruction
+    constexpr int KQ  = NCH / QPI;
+    const int jj = lane % RPW, qq = lane / RPW;
+    const int jrow = RPW * wave + jj;
+
+    // Issued in the loop's order (runs, then x and dt): the counter state at
+    // the loop head is then the same on entry as around the loop, and the
+    // wait for the runs never covers the previous chunk's y stores.
+    RunsW16<KQ, IO> runs;
+    load_runs_w16<KQ, QPI, IO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
+    StageW16<IO> st;
+    load_stage_w16<IO>(st, p, dt_h, x_h, c_begin, lane, w4, pw);
+
+    // Two barriers per chunk: (1) after staging, (2) after G1 has written M.
+    // Whatever a wave stages for chunk c+1 was last read before barrier (2)
+    // of chunk c, except dtX^T, which G2 reads after it: dtX^T alternates
+    // between two buffers. (With M in B's rows, B's staging must also wait
+    // for G2: a third barrier ends the chunk.)
+    for (int c = c_begin; c < c_end; ++c) {
+        const int t0   = (p.chunk_base + c) * HELIX_CS;
+        const int tlen = min(HELIX_CS, p.n_tok - t0);
+        const int par  = (c - c_begin) & 1;
+        // The next chunk's inputs are loaded as soon as this chunk's copy is
+        // consumed; on the last chunk the same chunk is loaded again, so the
+        // loop has no branch.
+        const int cn = min(c + 1, c_end - 1);
+
+        // ---- B and C of this chunk (loaded during the previous one) -------
+        {
+            // C is zeroed past tlen and d_state; that is all G1 and G3 need
+            // (B rows past tlen only meet zero dtXs columns in G4). With bf16
+            // storage a run's elements are already MFMA operands.
+            constexpr bool RAW = __is_same(IO, __bf16);
+#pragma unroll
+            for (int k = 0; k < KQ; ++k) {
+                const int u = qq + QPI * k;
+                const int cpos = perm32(8 * u);           // elements 8u+4 .. 8u+7 sit 8 further
+                const int j = jrow;
+                const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * u)) >> 31);
+                bf16x4 b_lo, b_hi, c_lo, c_hi;
+                if constexpr (RAW) {
+                    b_lo = __builtin_bit_cast(bf16x4, u32x2{runs.b[k][0][0], runs.b[k][0][1]});
+                    b_hi = __builtin_bit_cast(bf16x4, u32x2{runs.b[k][0][2], runs.b[k][0][3]});
+                    c_lo = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][0] & keep, runs.c[k][0][1] & keep});
+                    c_hi = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][2] & keep, runs.c[k][0][3] & keep});
+                } else {
+                    constexpr int WPR = RunsW16<KQ, IO>::WPR;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        b_lo[e] = to_bf16(run16_elem<IO, WPR>(runs.b[k], e));
+                        b_hi[e] = to_bf16(run16_elem<IO, WPR>(runs.b[k], 4 + e));
+                        c_lo[e] = to_bf16(as_f32(as_u32(run16_elem<IO, WPR>(runs.c[k], e)) & keep));
+                        c_hi[e] = to_bf16(as_f32(as_u32(run16_elem<IO, WPR>(runs.c[k], 4 + e)) & keep));
+                    }
+                }
+                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
+                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos + 8]) = b_hi;
+                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos]) = c_lo;
+                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos + 8]) = c_hi;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sBt[(8 * u + e) * RSJ + j] = b_lo[e];
+                    sBt[(8 * u + 4 + e) * RSJ + j] = b_hi[e];
+                }
+            }
+        }
+        load_runs_w16<KQ, QPI, IO>(runs, p, B_g, C_g, cn, N, jrow, qq);
+
+        // ---- decay preamble, dtX^T and dtXs^T ------------------------------
+        // The prefix is summed in fp64; the decays that only feed bf16
+        // operands are formed in fp32 from Lcum log2(e).
+        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+        const double lend = __shfl(lcum, 63, 64);
+        const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
+        {
+            // dt and the decay of this wave's 16 tokens, through the wave's own
+            // LDS row (one write, four broadcast reads each).
+            sDt[wave][0][lane] = dtv;
+            sDt[wave][1][lane] = sdec;
+            float vx[16], vs[16];
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sDt[wave][0][16 * w4 + 4 * i4]);
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sDt[wave][1][16 * w4 + 4 * i4]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float dx = d4[k] * io_widen<IO>(st.x[4 * i4 + k]);
+                    vx[4 * i4 + k] = dx;
+                    vs[4 * i4 + k] = s4[k] * dx;
+                }
+            }
+            store16_nat(&sXt[par][hw][lane * RSJ + 16 * w4], vx);
+            store16_nat(&sXst[hw][lane * RSJ + 16 * w4], vs);
+        }
+        if (w4 == 0) {
+            sL2[hw][lane] = (float)(lcum * 1.4426950408889634074);
+            sE[hw][lane] = expf((float)lcum);
+        }
+        load_stage_w16<IO>(st, p, dt_h, x_h, cn, lane, w4, pw);
+        __syncthreads();
+
+        // ---- G1: this wave's blocks of M^T = (B C^T) . decay, into M[t][j] --
+        // Block idx = w4 + 4 i: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
+        {
+            f32x4 d[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int idx = w4 + 4 * i;
+                if (idx >= 10) break;
+                const int tb = g1_tb(idx), jb = g1_jb(idx);
+                const __bf16* arow = &sB[(16 * jb + c16) * RS + 8 * q];
+                const __bf16* brow = &sC[(16 * tb + c16) * RS + 8 * q];
+                d[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+                    d[i] = mfma16(*reinterpret_cast<const bf16x8*>(arow + 32 * s),
+                                  *reinterpret_cast<const bf16x8*>(brow + 32 * s), d[i]);
+            }
+            if constexpr (M_IN_B) {
+                __syncthreads();   // every wave's B reads are done
+                *reinterpret_cast<unsigned*>(&sMh[zoff]) = 0u;
+            }
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int idx = w4 + 4 * i;
+                if (idx >= 10) break;
+                const int tb = g1_tb(idx), jb = g1_jb(idx);
+                const int t = 16 * tb + c16;
+                const int j0 = 16 * jb + 4 * q;
+                const float l_t = sL2[hw][t];
+                const f32x4 lj = *reinterpret_cast<const f32x4*>(&sL2[hw][j0]);
+                bf16x4 m;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    m[r] = to_bf16(keep_if_le(d[i][r] * __builtin_amdgcn_exp2f(l_t - lj[r]), j0 + r, t));
+                *reinterpret_cast<bf16x4*>(&sMh[t * RSJ + j0]) = m;
+            }
+        }
+
+        // ---- G3: y = exp(Lcum_t) . (C R), R the state before this chunk -----
+        f32x4 acc[4];
+        {
+            bf16x8 rb[KS];
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    rb[s][e] = to_bf16(R[2 * s][e]);
+                    rb[s][4 + e] = to_bf16(R[2 * s + 1][e]);
+                }
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                const __bf16* crow = &sC[(16 * tb + c16) * RS + 8 * q];
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+                    acc[tb] = mfma16(*reinterpret_cast<const bf16x8*>(crow + 32 * s), rb[s], acc[tb]);
+                const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sE[hw][16 * tb + 4 * q]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[tb][r] *= e4[r];
+            }
+        }
+        // ---- G4: R <- exp(L_end) R + B^T . dtXs (after G3 has used R) -------
+        {
+            const float a_c = expf((float)lend);
+            bf16x8 xs[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) xs[s] = *reinterpret_cast<const bf16x8*>(&sXst[hw][pp * RSJ + 32 * s + 8 * q]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                f32x4 rn = R[nb] * a_c;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    rn = mfma16(*reinterpret_cast<const bf16x8*>(&sBt[(16 * nb + c16) * RSJ + 32 * s + 8 * q]), xs[s], rn);
+                R[nb] = rn;
+            }
+        }
+        __syncthreads();   // M complete
+
+        // ---- G2: y += M . dtX (causal: t block tb needs j < 16 (tb + 1)) ----
+        {
+            bf16x8 xb[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) xb[s] = *reinterpret_cast<const bf16x8*>(&sXt[par][hw][pp * RSJ + 32 * s + 8 * q]);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    if (s == 1 && tb < 2) continue;
+                    const bf16x8 ma = *reinterpret_cast<const bf16x8*>(&sMh[(16 * tb + c16) * RSJ + 32 * s + 8 * q]);
+                    acc[tb] = mfma16(ma, xb[s], acc[tb]);
+                }
+        }
+        store_y16<IO>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+
+        if constexpr (M_IN_B) __syncthreads();
+    }
+}
+
+#define HELIX_PASS_C_WALK16(NP)                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP)>(p, b);                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP), __bf16>(p, b);                               \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_f16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP), _Float16>(p, b);                             \
+    }
+
+HELIX_PASS_C_WALK16(64)
+HELIX_PASS_C_WALK16(128)
+HELIX_PASS_C_WALK16(256)

@@ -351,7 +351,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 for (int r = 0; r < 4; ++r) {
                     const int t = 16 * tb + 4 * g4 + r;
                     const float v = ya[tb][r];
-                    io_store<IO>(ry, v, store_off_if_lt((t * sy0 + pc * sy2) * ES, t, tlen, pc, pw), 0);
+                    io_store<IO, HELIX_NT>(ry, v, store_off_if_lt((t * sy0 + pc * sy2) * ES, t, tlen, pc, pw), 0);
                 }
         }
         __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX

@@ -98,12 +98,15 @@ constexpr const char* kX6StateSbf[] = {"helix_chunk_state_x6sbf_n64", "helix_chu
                                        "helix_chunk_state_x6sbf_n256"};
 constexpr const char* kX6StateAgg[] = {"helix_chunk_state_x6agg_n64", "helix_chunk_state_x6agg_n128",
                                        "helix_chunk_state_x6agg_n256"};
+constexpr const char* kWalk16[] = {"helix_scan_walk16_bf16_n64", "helix_scan_walk16_bf16_n128",
+                                    "helix_scan_walk16_bf16_n256"};
 constexpr const char* kX6OutF32[] = {"helix_chunk_out_x6_n64", "helix_chunk_out_x6_n128", nullptr};
 
 // The selectable trait sets: [family: fp32, bf16, bf16 walk][np index], with
 // Pass A on fp32 MFMA or bf16x6. Built once; names live as long as the process.
 struct TraitSets {
     HelixMatmulTraits t[2][3][3];
+    HelixMatmulTraits w16[2][3];   // the walk family with the 16 x 16 tile Pass C
     std::string names[2][3][3];
     TraitSets() {
         const HelixMatmulTraits* base[3] = {kF32Traits, kBf16Traits, kBf16WalkTraits};
@@ -126,13 +129,28 @@ struct TraitSets {
                     v.mfma_c = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
                 }
             }
+        for (int x6 = 0; x6 < 2; ++x6)
+            for (int k = 0; k < 3; ++k) {
+                w16[x6][k] = t[x6][2][k];
+                w16[x6][k].k_chunk_out = kWalk16[k];
+                w16[x6][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
+                w16[x6][k].walk_hpw = HELIX_WALK16_HPW(64 << k);
+            }
     }
 };
+
+// The walking Pass C runs on 16 x 16 tiles (pass_c_walk16.hip) unless
+// HELIX_WALK=32 asks for the 32 x 32 tile kernel (pass_c_walk.hip).
+bool walk16_on() {
+    const char* v = std::getenv("HELIX_WALK");
+    return !(v && v[0] == '3' && v[1] == '2');
+}
 
 const HelixMatmulTraits& pick_traits(int fam, int k) {
     static const TraitSets sets;
     const char* v = std::getenv("HELIX_X6");
     const int x6 = (v && v[0] == '0') ? 0 : 1;
+    if (fam == 2 && walk16_on()) return sets.w16[x6][k];
     return sets.t[x6][fam][k];
 }
 
@@ -140,9 +158,11 @@ const HelixMatmulTraits& pick_traits(int fam, int k) {
 // stay fp32). A bf16 multipass request walks segments in Pass C with Pass A's
 // aggregate kernel reading the 16-bit operands; every other request runs the
 // single-pass kernel with fp32 compute. [io: 0 bf16, 1 f16][0 walk, 1 single][np]
+bool walk16_on();
+
 struct IoTraitSets {
-    HelixMatmulTraits t[2][2][3];
-    std::string names[2][2][3], ka[2][3], kc[2][3], k1[2][3];
+    HelixMatmulTraits t[2][2][3], w16[2][3];
+    std::string names[2][2][3], ka[2][3], kc[2][3], k1[2][3], kc16[2][3];
     IoTraitSets() {
         const char* io[2] = {"bf16", "f16"};
         const int nps[3] = {64, 128, 256};
@@ -161,12 +181,18 @@ struct IoTraitSets {
                 t[i][1][k] = {HELIX_BACKEND_SGMMA, names[i][1][k].c_str(), nullptr, nullptr, nullptr, false,
                               "v_mfma_f32_16x16x4_f32", "v_mfma_f32_16x16x4_f32", nps[k], false,
                               k1[i][k].c_str()};
+                kc16[i][k] = std::string("helix_scan_walk16_bf16_") + io[i] + "io_n" + np;
+                w16[i][k] = t[i][0][k];
+                w16[i][k].k_chunk_out = kc16[i][k].c_str();
+                w16[i][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
+                w16[i][k].walk_hpw = HELIX_WALK16_HPW(nps[k]);
             }
     }
 };
 
 const HelixMatmulTraits& io_traits(helix_dtype io, bool walk, int k) {
     static const IoTraitSets sets;
+    if (walk && walk16_on()) return sets.w16[io == HELIX_F16 ? 1 : 0][k];
     return sets.t[io == HELIX_F16 ? 1 : 0][walk ? 0 : 1][k];
 }
 
@@ -190,6 +216,9 @@ const char* const kKernelNames[] = {
     "helix_scan_walk_bf16_f16io_n64",     "helix_scan_walk_bf16_f16io_n128",     "helix_scan_walk_bf16_f16io_n256",
     "helix_scan_1pass_bf16io_n64",        "helix_scan_1pass_bf16io_n128",        "helix_scan_1pass_bf16io_n256",
     "helix_scan_1pass_f16io_n64",         "helix_scan_1pass_f16io_n128",         "helix_scan_1pass_f16io_n256",
+    "helix_scan_walk16_bf16_n64",         "helix_scan_walk16_bf16_n128",         "helix_scan_walk16_bf16_n256",
+    "helix_scan_walk16_bf16_bf16io_n64",  "helix_scan_walk16_bf16_bf16io_n128",  "helix_scan_walk16_bf16_bf16io_n256",
+    "helix_scan_walk16_bf16_f16io_n64",   "helix_scan_walk16_bf16_f16io_n128",   "helix_scan_walk16_bf16_f16io_n256",
 };
 
 int np_index(int d_state) {

@@ -221,7 +221,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c) {
             const unsigned hpg = (unsigned)(d->n_head / d->n_group);
-            const unsigned hpw = HELIX_WALK_HPW(tr.np);
+            const unsigned hpw = tr.walk_hpw > 0 ? (unsigned)tr.walk_hpw : HELIX_WALK_HPW(tr.np);
             const unsigned pairs = (hpg + hpw - 1) / hpw;
             const unsigned n_wg = tr.walk
                 ? (unsigned)params.n_seg * (unsigned)d->n_group * pairs * (unsigned)params.n_pslab *

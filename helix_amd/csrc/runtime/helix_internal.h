@@ -45,6 +45,8 @@ struct HelixMatmulTraits {
     // caps.mm:18-25). Set only in the single-pass trait set, where the three
     // pass names are null.
     const char*   k_single;
+    // Heads per workgroup of a walking Pass C; 0 means HELIX_WALK_HPW(np).
+    int           walk_hpw;
 };
 
 namespace helix::rt {

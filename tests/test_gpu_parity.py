@@ -70,6 +70,9 @@ MODES = [
     ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}, True),
+    # The walk on 32 x 32 tiles (the default walk runs 16 x 16 tiles).
+    ("bf16walk32", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk", "HELIX_WALK": "32"}, True),
+    ("bf16walk32/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk", "HELIX_WALK": "32"}, True),
     # fp32-MFMA kernels instead of bf16x6 split products.
     ("fp32/mma/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {"HELIX_X6": "0"}, True),
     ("fp32/mma", HELIX_BACKEND_SGMMA, None, "short", {"HELIX_X6": "0"}, True),
@@ -128,6 +131,7 @@ def _baseline(name, memory):
 
 CASES = [(n, path, mem) for n, c in CONFIGS.items() for path in c.paths for mem in ("dist", "long")]
 CASES += [(n, "bf16walk", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
+CASES += [(n, "bf16walk32", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
 CASES += [(n, path + "/mma", "long") for n, c in CONFIGS.items() for path in c.paths]
 CASES += [(n, "1pass", mem) for n in CONFIGS for mem in ("dist", "long")]
 
@@ -140,7 +144,8 @@ def test_baseline_config(gpu, name, path, memory):
     d.multipass = path != "1pass"
     d.backend = (HELIX_BACKEND_MPP if path.startswith("bf16")
                  else HELIX_BACKEND_AUTO if path == "1pass" else HELIX_BACKEND_SGMMA)
-    with env(HELIX_BF16_PASSC="walk" if path == "bf16walk" else None,
+    with env(HELIX_BF16_PASSC="walk" if path.startswith("bf16walk") else None,
+             HELIX_WALK="32" if path == "bf16walk32" else None,
              HELIX_X6="0" if path.endswith("/mma") else None):
         assert gpu.supported(d)
         assert (gpu.select_backend(d) == HELIX_BACKEND_MPP) == path.startswith("bf16")

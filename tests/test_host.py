@@ -194,9 +194,11 @@ def test_16bit_storage_selection(host, io, name):
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
         f"helix_chunk_state_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
-        f"helix_scan_walk_bf16_{name}io_n128".encode())
+        f"helix_scan_walk16_bf16_{name}io_n128".encode())
     assert k.total_bytes == host.scratch_size(d) > 0 and k.s_local_bytes == 0
     with env(HELIX_BF16_PASSC="tile"):     # only the walk reads 16-bit operands
+        assert host.plan_info(d).kernel_c == f"helix_scan_walk16_bf16_{name}io_n128".encode()
+    with env(HELIX_WALK="32"):             # the 32 x 32 tile walk
         assert host.plan_info(d).kernel_c == f"helix_scan_walk_bf16_{name}io_n128".encode()
     for backend, multipass in ((HELIX_BACKEND_SGMMA, True), (HELIX_BACKEND_AUTO, False),
                                (HELIX_BACKEND_SGMMA, False)):
@@ -252,7 +254,9 @@ def test_backend_selection(host):
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk_bf16_n128")
+        b"helix_chunk_state_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
+    with env(HELIX_WALK="32"):
+        assert host.plan_info(mp(shape)).kernel_c == b"helix_scan_walk_bf16_n128"
     with env(HELIX_BF16_PASSC="tile"):
         k = host.plan_info(mp(shape))
         assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
@@ -263,7 +267,7 @@ def test_backend_selection(host):
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
     with env(HELIX_BF16_PASSC="walk"):
         k = host.plan_info(mp(shape))
-        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk_bf16_n128")
+        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
     with env(HELIX_X6="0"):
         k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
         assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_f32_n128", b"helix_chunk_out_f32_n128")
