@@ -123,6 +123,27 @@ def time_variant(v: Variant, steps: int, stream, only: str | None = None):
         os.environ.pop("HELIX_ONLY_PASS", None)
 
 
+def time_passes(v: Variant, steps: int, stream):
+    """Per-pass event times (ms): each step encodes Pass A, B and C as three
+    single-pass encodes in a row (HELIX_ONLY_PASS), each between two events
+    on the launch stream, so every pass runs in the same order, and on the
+    same cache state, as inside a whole scan."""
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in "ABC"]
+           for _ in range(steps)]
+    try:
+        torch.cuda.synchronize()
+        for step in evs:
+            for k, (a, b) in zip("ABC", step):
+                os.environ["HELIX_ONLY_PASS"] = k
+                a.record(stream)
+                v.encode(stream)
+                b.record(stream)
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("HELIX_ONLY_PASS", None)
+    return {k: [step[i][0].elapsed_time(step[i][1]) for step in evs] for i, k in enumerate("ABC")}
+
+
 def pass_algorithmic_bytes(plan):
     """Bytes each pass must move once at config 2 on the bf16 path (the
     scratch it writes or reads included, since the pass cannot avoid it)."""
@@ -156,7 +177,8 @@ def profiled_traffic(kernel: str):
 
 def dist(ts):
     s = sorted(ts)
-    return {"min": s[0], "median": s[len(s) // 2], "max": s[-1], "spread": s[-1] / s[0]}
+    return {"min": s[0], "median": s[len(s) // 2], "mean": statistics.fmean(s), "max": s[-1],
+            "spread": s[-1] / s[0]}
 
 
 def cpu_baseline(budget_s: float = 20.0):
@@ -239,17 +261,18 @@ def main():
         variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
 
-    # Warm-up: W steps each, then alternate until the wall clock has run
-    # warmup_ms (the reference's protocol against clock ramps).
-    for v in variants:
+    def warm_up(v, ms):
+        """W steps, then more until the wall clock has run `ms` (the
+        reference's protocol against clock ramps). Each variant is warmed
+        right before it is timed, on its own: alternating variants would hand
+        each timed pass another variant's cache state."""
         for _ in range(args.warmup):
             v.encode(stream)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    while (time.perf_counter() - t0) * 1e3 < args.warmup_ms:
-        for v in variants:
-            v.encode(stream)
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < ms:
+            v.encode(stream)
+            torch.cuda.synchronize()
 
     L, S, H, P, N, G = (CFG[k] for k in "LSHPNG")
     F = algorithmic_flops(L, S, H, P, N)
@@ -258,7 +281,8 @@ def main():
     F_C = F - F_A
     bytes_alg = algorithmic_bytes(L, S, H, P, N, G)
     results = {}
-    for v in variants:
+    for i, v in enumerate(variants):
+        warm_up(v, args.warmup_ms if i == 0 else min(args.warmup_ms, 200.0))
         # Whole op: K steps bracketed by synchronize; per-step events too.
         torch.cuda.synchronize()
         w0 = time.perf_counter()
@@ -266,7 +290,7 @@ def main():
         torch.cuda.synchronize()
         wall = (time.perf_counter() - w0) / args.steps * 1e3
         # Per-pass split (HELIX_ONLY_PASS) exists only for the multipass path.
-        passes = ({k: dist(time_variant(v, args.steps, stream, only=k)) for k in "ABC"}
+        passes = ({k: dist(ts_k) for k, ts_k in time_passes(v, args.steps, stream).items()}
                   if v.multipass else None)
         d = dist(ts)
         ms = statistics.fmean(ts)
@@ -285,7 +309,7 @@ def main():
     pass_bytes = pass_algorithmic_bytes(plan)
     dom = max("ABC", key=lambda k: pa[k]["median"])
     kname = {"A": plan.kernel_a, "B": plan.kernel_b, "C": plan.kernel_c}[dom].decode()
-    t = pa[dom]["median"] * 1e-3
+    t = pa[dom]["mean"] * 1e-3     # average launch duration, as rocprofv3 --stats reports it
     roof = {"kernel": f"{kname} (Pass {dom})", "bound": "hbm",
             "achieved": pass_bytes[dom] / t / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "algorithmic_bytes": pass_bytes[dom]}
