@@ -152,10 +152,13 @@ def pass_algorithmic_bytes(plan):
     dt = S * L * H * 4
     bc = S * L * G * N * 4
     state = S * H * P * N * 4
+    # With bf16 copies of B and C, Pass A also reads C and writes both copies,
+    # and Pass C reads the copies instead.
+    cp = plan.bccopy_bytes
     return {
-        "A": x + dt + bc + plan.s_local_bytes + plan.s_seg_bytes,
+        "A": x + dt + bc + plan.s_local_bytes + plan.s_seg_bytes + ((bc + cp) if cp else 0),
         "B": 2 * plan.s_seg_bytes + 2 * state,
-        "C": x + dt + 2 * bc + plan.s_local_bytes + plan.s_seg_bytes + y,
+        "C": x + dt + (cp if cp else 2 * bc) + plan.s_local_bytes + plan.s_seg_bytes + y,
     }
 
 

@@ -48,6 +48,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("kernel_b", ctypes.c_char_p),
         ("kernel_c", ctypes.c_char_p),
         ("kernel_1pass", ctypes.c_char_p),
+        ("bccopy_bytes", c_uint64),
     ]
 
 

@@ -30,6 +30,10 @@
  *   ld      [seq][cg][head]                f32: sum of chunk log-decays before c
  *                                               within c's segment
  *   segld   [seq][seg][head]               f32: whole-segment log-decay
+ *   bcopy, ccopy [seq][t][group][n]        bf16: B and C of the group's cpg*64
+ *                                  tokens (t counted from the group's first
+ *                                  token), written by Pass A for the walking
+ *                                  Pass C (optional; rows past n_tok unwritten)
  * A TILE holds one 64-channel slab of one head's state, [64 p][np n] padded,
  * in the order Pass A's MFMA result registers hold it (v_mfma_f32_32x32x2_f32
  * computing R[n][p], M = n, N = p), grouped in units of four registers:
@@ -98,7 +102,7 @@ typedef struct HelixScanParams {
     int hblk;             /* heads per Pass C workgroup */
     int n_hblk;           /* head blocks per B/C group */
     int np;               /* d_state padded to the kernels' tile width (64/128/256) */
-    int pad0;
+    int cpg;              /* chunks per group of the plan (scratch strides) */
 
     /* Scratch strides in elements (see the layout comment above). */
     long long sl_cg, sl_seq;     /* s_local: chunk stride (H*n_pslab*64*np), seq stride */
@@ -123,6 +127,8 @@ typedef struct HelixScanBuffers {
     float*       s_seg;
     float*       ld;
     float*       segld;
+    void*        bcopy;   /* bf16 copies of B and C (see the layout above), or null */
+    void*        ccopy;
 } HelixScanBuffers;
 
 #endif /* HELIX_PARAMS_H */

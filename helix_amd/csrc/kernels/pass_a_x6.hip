@@ -99,6 +99,72 @@ __device__ __forceinline__ void load_stage_x6(StageX6<NP, IO>& st, const HelixSc
     }
 }
 
+// bf16 copies of B and C for the walking Pass C (bcopy/ccopy, helix_params.h).
+// The K = heads_per_group * n_pslab workgroups of a chunk share its 64 rows:
+// workgroup `id` takes rows j = id + K k. Thread tid handles the quads
+// (four state indices) q = tid + 256 i, i < 2, of those rows: row slot
+// k = q / (N/4), quad u = q % (N/4) (the host selects this only when the
+// rows fit: ceil(64 / K) * N/4 <= 512). The fp32 quads travel with the
+// chunk's register stage; rows past tlen are neither read nor written.
+struct CopyBC {
+    u32x4 b[2], c[2];
+};
+struct CopyMap {
+    int j[2], u[2];     // row and quad of slot i; j >= 64 means none
+};
+
+__device__ __forceinline__ CopyMap copy_map(int tid, int id, int K, int N) {
+    CopyMap m;
+    const int nq = N >> 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = tid + 256 * i;
+        const int k = q / nq;
+        m.u[i] = q - k * nq;
+        m.j[i] = min(id + K * k, 64);
+    }
+    return m;
+}
+
+__device__ __forceinline__ void load_copy_bc(CopyBC& cp, const CopyMap& m, const HelixScanParams& p,
+                                             const float* __restrict__ B_g, const float* __restrict__ C_g,
+                                             int c, int N) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
+    const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+    const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * 4u);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        cp.b[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            rb, store_off_if_lt((m.j[i] * sb0 + 4 * m.u[i]) * 4, m.j[i], tlen, 0, 1), 0, 0);
+        cp.c[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            rc, store_off_if_lt((m.j[i] * sc0 + 4 * m.u[i]) * 4, m.j[i], tlen, 0, 1), 0, 0);
+    }
+}
+
+// Store the staged quads as bf16 (round to nearest even, as Pass C rounds
+// its operands) at rows j of chunk c of the group's copy.
+__device__ __forceinline__ void store_copy_bc(const CopyBC& cp, const CopyMap& m, const HelixScanParams& p,
+                                              const HelixScanBuffers& b, int seq, int g, int c, int N) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const long long gn = (long long)p.n_group * N;
+    const long long base = ((long long)seq * p.cpg * HELIX_CS + (long long)c * HELIX_CS) * gn + (long long)g * N;
+    const unsigned bytes = (unsigned)((HELIX_CS - 1) * gn + N) * 2u;
+    const helix_rsrc rb = make_rsrc(static_cast<__bf16*>(b.bcopy) + base, bytes);
+    const helix_rsrc rc = make_rsrc(static_cast<__bf16*>(b.ccopy) + base, bytes);
+    const int gni = (int)gn;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int off = store_off_if_lt((m.j[i] * gni + 4 * m.u[i]) * 2, m.j[i], tlen, 0, 1);
+        const u32x2 wb = {pk_bf16(as_f32(cp.b[i][0]), as_f32(cp.b[i][1])), pk_bf16(as_f32(cp.b[i][2]), as_f32(cp.b[i][3]))};
+        const u32x2 wc = {pk_bf16(as_f32(cp.c[i][0]), as_f32(cp.c[i][1])), pk_bf16(as_f32(cp.c[i][2]), as_f32(cp.c[i][3]))};
+        __builtin_amdgcn_raw_buffer_store_b64(wb, rb, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(wc, rc, off, 0, 0);
+    }
+}
+
 // Stage 16 consecutive tokens (chunks c0, c0 + 1) of row r of a three-plane
 // operand from fp32 values v[0..15].
 template <int ROWS>
@@ -121,8 +187,9 @@ HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[1
 }
 
 // MODE as in pass_a.hip: 0 store R_c fp32, 1 store R_c bf16, 2 aggregates only.
-// IO: the caller's storage type of x and B.
-template <int NP, int MODE, typename IO = float>
+// IO: the caller's storage type of x and B. BCC: also write the bf16 copies
+// of B and C (fp32 storage only).
+template <int NP, int MODE, typename IO = float, bool BCC = false>
 __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr bool SBF = MODE == 1;
     constexpr int NTW = NP / 64;      // N tiles per wave
@@ -149,6 +216,10 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
     const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
     const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
+    const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
+    const CopyMap cmap = BCC ? copy_map(tid, (h % p.heads_per_group) * p.n_pslab + slab,
+                                        p.heads_per_group * p.n_pslab, N)
+                             : CopyMap{};
 
     const long long tile_off = state_tile_off(p, h, slab);
     const unsigned tile_elems = 64u * NP;
@@ -163,7 +234,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 
     // Two register stages in turn: the loads of chunk c+2 are issued while
     // chunks c and c+1 are processed (a copy between stages would wait on them).
-    auto step = [&](StageX6<NP, IO>& st, int c) {
+    auto step = [&](StageX6<NP, IO>& st, CopyBC& cp, int c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
 
@@ -202,6 +273,8 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
             *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(2, rn, 2 * wave + hi)]) = q2;
         }
 
+        if constexpr (BCC) store_copy_bc(cp, cmap, p, b, seq, g, c, N);
+
         if (MODE != 2 && c > c_begin) {
             const long long off = seq * p.sl_seq + (long long)c * p.sl_cg + tile_off;
             const void* dst = SBF ? (const void*)(static_cast<const __bf16*>(b.s_local) + off)
@@ -227,7 +300,10 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 
         // This register stage is free again: chunk c+2's inputs travel while
         // this chunk's and the next one's GEMMs run.
-        if (c + 2 < c_end) load_stage_x6<NP, IO>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
+        if (c + 2 < c_end) {
+            load_stage_x6<NP, IO>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
+            if constexpr (BCC) load_copy_bc(cp, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c + 2, N);
+        }
 
         const float a_c = expf((float)lend);
 #pragma unroll
@@ -258,11 +334,16 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         __syncthreads();
     };
     StageX6<NP, IO> sa, sb;
+    CopyBC ca, cb;
     load_stage_x6<NP, IO>(sa, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
-    if (c_begin + 1 < c_end) load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
+    if constexpr (BCC) load_copy_bc(ca, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c_begin, N);
+    if (c_begin + 1 < c_end) {
+        load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
+        if constexpr (BCC) load_copy_bc(cb, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c_begin + 1, N);
+    }
     for (int c = c_begin; c < c_end; c += 2) {
-        step(sa, c);
-        if (c + 1 < c_end) step(sb, c + 1);
+        step(sa, ca, c);
+        if (c + 1 < c_end) step(sb, cb, c + 1);
     }
 
     const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
@@ -291,6 +372,10 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_n##NP(        \
         HelixScanParams p, HelixScanBuffers b) {                                                \
         chunk_state_x6_impl<NP, 2>(p, b);                                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_bc_n##NP(     \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, float, true>(p, b);                                          \
     }
 
 // Aggregates from 16-bit storage of x and B (io_dtype BF16 / F16), for the

@@ -153,8 +153,10 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
         }
 }
 
-// IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
-template <int NP, int HPW, typename IO = float>
+// IO: the caller's storage type of x, B, C and y (dt, A and the states are
+// fp32). BIO: the type B and C are read in; __bf16 with fp32 storage when
+// they come from Pass A's bf16 copies (the host points B and C there).
+template <int NP, int HPW, typename IO = float, typename BIO = IO>
 __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int NW  = 4 * HPW;              // HPW heads per workgroup, four waves each
     constexpr int NB  = NP / 16;              // 16-row state tiles of R
@@ -212,8 +214,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     const float A_h = b.A[(long long)h * p.s_a];
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
     const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
-    const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
-    const IO* __restrict__ C_g = reinterpret_cast<const IO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
+    const BIO* __restrict__ B_g = reinterpret_cast<const BIO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
+    const BIO* __restrict__ C_g = reinterpret_cast<const BIO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
 
     const int pp = 16 * w4 + c16;                 // this lane's P column in the slab
 
@@ -256,8 +258,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     // Issued in the loop's order (runs, then x and dt): the counter state at
     // the loop head is then the same on entry as around the loop, and the
     // wait for the runs never covers the previous chunk's y stores.
-    RunsW16<KQ, IO> runs;
-    load_runs_w16<KQ, QPI, IO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
+    RunsW16<KQ, BIO> runs;
+    load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
     StageW16<IO> st;
     load_stage_w16<IO>(st, p, dt_h, x_h, c_begin, lane, w4, pw);
 
@@ -280,7 +282,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             // C is zeroed past tlen and d_state; that is all G1 and G3 need
             // (B rows past tlen only meet zero dtXs columns in G4). With bf16
             // storage a run's elements are already MFMA operands.
-            constexpr bool RAW = __is_same(IO, __bf16);
+            constexpr bool RAW = __is_same(BIO, __bf16);
 #pragma unroll
             for (int k = 0; k < KQ; ++k) {
                 const int u = qq + QPI * k;
@@ -294,13 +296,13 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                     c_lo = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][0] & keep, runs.c[k][0][1] & keep});
                     c_hi = __builtin_bit_cast(bf16x4, u32x2{runs.c[k][0][2] & keep, runs.c[k][0][3] & keep});
                 } else {
-                    constexpr int WPR = RunsW16<KQ, IO>::WPR;
+                    constexpr int WPR = RunsW16<KQ, BIO>::WPR;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        b_lo[e] = to_bf16(run16_elem<IO, WPR>(runs.b[k], e));
-                        b_hi[e] = to_bf16(run16_elem<IO, WPR>(runs.b[k], 4 + e));
-                        c_lo[e] = to_bf16(as_f32(as_u32(run16_elem<IO, WPR>(runs.c[k], e)) & keep));
-                        c_hi[e] = to_bf16(as_f32(as_u32(run16_elem<IO, WPR>(runs.c[k], 4 + e)) & keep));
+                        b_lo[e] = to_bf16(run16_elem<BIO, WPR>(runs.b[k], e));
+                        b_hi[e] = to_bf16(run16_elem<BIO, WPR>(runs.b[k], 4 + e));
+                        c_lo[e] = to_bf16(as_f32(as_u32(run16_elem<BIO, WPR>(runs.c[k], e)) & keep));
+                        c_hi[e] = to_bf16(as_f32(as_u32(run16_elem<BIO, WPR>(runs.c[k], 4 + e)) & keep));
                     }
                 }
                 *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
@@ -314,7 +316,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 }
             }
         }
-        load_runs_w16<KQ, QPI, IO>(runs, p, B_g, C_g, cn, N, jrow, qq);
+        load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, cn, N, jrow, qq);
 
         // ---- decay preamble, dtX^T and dtXs^T ------------------------------
         // The prefix is summed in fp64; the decays that only feed bf16
@@ -452,6 +454,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \
         scan_walk16_impl<NP, HELIX_WALK16_HPW(NP)>(p, b);                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_bc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP), float, __bf16>(p, b);                        \
     }                                                                                           \
     extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_bf16io_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \

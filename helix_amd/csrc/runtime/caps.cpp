@@ -100,6 +100,10 @@ constexpr const char* kX6StateAgg[] = {"helix_chunk_state_x6agg_n64", "helix_chu
                                        "helix_chunk_state_x6agg_n256"};
 constexpr const char* kWalk16[] = {"helix_scan_walk16_bf16_n64", "helix_scan_walk16_bf16_n128",
                                     "helix_scan_walk16_bf16_n256"};
+constexpr const char* kWalk16Bc[] = {"helix_scan_walk16_bf16_bc_n64", "helix_scan_walk16_bf16_bc_n128",
+                                      "helix_scan_walk16_bf16_bc_n256"};
+constexpr const char* kX6StateAggBc[] = {"helix_chunk_state_x6agg_bc_n64", "helix_chunk_state_x6agg_bc_n128",
+                                         "helix_chunk_state_x6agg_bc_n256"};
 constexpr const char* kX6OutF32[] = {"helix_chunk_out_x6_n64", "helix_chunk_out_x6_n128", nullptr};
 
 // The selectable trait sets: [family: fp32, bf16, bf16 walk][np index], with
@@ -107,6 +111,7 @@ constexpr const char* kX6OutF32[] = {"helix_chunk_out_x6_n64", "helix_chunk_out_
 struct TraitSets {
     HelixMatmulTraits t[2][3][3];
     HelixMatmulTraits w16[2][3];   // the walk family with the 16 x 16 tile Pass C
+    HelixMatmulTraits w16bc[3];    // ... reading bf16 B and C copies from Pass A (bf16x6)
     std::string names[2][3][3];
     TraitSets() {
         const HelixMatmulTraits* base[3] = {kF32Traits, kBf16Traits, kBf16WalkTraits};
@@ -136,8 +141,25 @@ struct TraitSets {
                 w16[x6][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[x6][k].walk_hpw = HELIX_WALK16_HPW(64 << k);
             }
+        for (int k = 0; k < 3; ++k) {
+            w16bc[k] = w16[1][k];
+            w16bc[k].k_chunk_state = kX6StateAggBc[k];
+            w16bc[k].k_chunk_out = kWalk16Bc[k];
+            w16bc[k].bccopy = true;
+        }
     }
 };
+
+// Pass A writes bf16 copies of B and C for the walking Pass C (fp32
+// storage, bf16x6 Pass A) unless HELIX_WALK_BCCOPY=0, when the K =
+// heads_per_group * n_pslab workgroups of a chunk cover its 64 rows with two
+// quads of four state indices per thread (pass_a_x6.hip, copy_map).
+bool bccopy_on(const helix_scan_desc& d) {
+    const char* v = std::getenv("HELIX_WALK_BCCOPY");
+    if (v && v[0] == '0') return false;
+    const long K = (long)(d.n_head / d.n_group) * ((d.head_dim + HELIX_HD - 1) / HELIX_HD);
+    return (64 + K - 1) / K * (d.d_state / 4) <= 2 * 256;
+}
 
 // The walking Pass C runs on 16 x 16 tiles (pass_c_walk16.hip) unless
 // HELIX_WALK=32 asks for the 32 x 32 tile kernel (pass_c_walk.hip).
@@ -146,11 +168,11 @@ bool walk16_on() {
     return !(v && v[0] == '3' && v[1] == '2');
 }
 
-const HelixMatmulTraits& pick_traits(int fam, int k) {
+const HelixMatmulTraits& pick_traits(int fam, int k, const helix_scan_desc& d) {
     static const TraitSets sets;
     const char* v = std::getenv("HELIX_X6");
     const int x6 = (v && v[0] == '0') ? 0 : 1;
-    if (fam == 2 && walk16_on()) return sets.w16[x6][k];
+    if (fam == 2 && walk16_on()) return (x6 && bccopy_on(d)) ? sets.w16bc[k] : sets.w16[x6][k];
     return sets.t[x6][fam][k];
 }
 
@@ -219,6 +241,8 @@ const char* const kKernelNames[] = {
     "helix_scan_walk16_bf16_n64",         "helix_scan_walk16_bf16_n128",         "helix_scan_walk16_bf16_n256",
     "helix_scan_walk16_bf16_bf16io_n64",  "helix_scan_walk16_bf16_bf16io_n128",  "helix_scan_walk16_bf16_bf16io_n256",
     "helix_scan_walk16_bf16_f16io_n64",   "helix_scan_walk16_bf16_f16io_n128",   "helix_scan_walk16_bf16_f16io_n256",
+    "helix_scan_walk16_bf16_bc_n64",      "helix_scan_walk16_bf16_bc_n128",      "helix_scan_walk16_bf16_bc_n256",
+    "helix_chunk_state_x6agg_bc_n64",     "helix_chunk_state_x6agg_bc_n128",     "helix_chunk_state_x6agg_bc_n256",
 };
 
 int np_index(int d_state) {
@@ -277,19 +301,19 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
     if (!d.multipass) return kSingleTraits[k];
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND"))
-        if (f[0] == 's') return pick_traits(0, k);
+        if (f[0] == 's') return pick_traits(0, k, d);
     const bool want_bf16 = d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP;
     if (want_bf16 && d.multipass) {
         // HELIX_BF16_PASSC=walk|tile overrides the choice between the
         // chunk-walking Pass C (state in registers, no per-chunk scratch) and
         // the chunk-parallel one.
         if (const char* v = std::getenv("HELIX_BF16_PASSC")) {
-            if (v[0] == 'w') return pick_traits(2, k);
-            if (v[0] == 't') return pick_traits(1, k);
+            if (v[0] == 'w') return pick_traits(2, k, d);
+            if (v[0] == 't') return pick_traits(1, k, d);
         }
-        return pick_traits(prefer_walk(d) ? 2 : 1, k);
+        return pick_traits(prefer_walk(d) ? 2 : 1, k, d);
     }
-    return pick_traits(0, k);
+    return pick_traits(0, k, d);
 }
 
 size_t scratch_budget_bytes() {
@@ -332,7 +356,8 @@ bool prefer_walk(const helix_scan_desc& d) {
     return choose_seg_len(d, (int)std::min<long>(n_chunks, 1 << 30)) >= kMaxSegLen;
 }
 
-void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int np, int cpg, MultipassPlan* pl) {
+void layout(const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, int np, int cpg,
+            MultipassPlan* pl) {
     // State scratch is stored as padded slab tiles of 64 x np (helix_params.h).
     const size_t n_pslab = (size_t)(d.head_dim + HELIX_HD - 1) / HELIX_HD;
     const size_t state = (size_t)d.n_seq * d.n_head * n_pslab * 64 * (size_t)np;
@@ -344,11 +369,14 @@ void layout(const helix_scan_desc& d, bool bf16_state, bool walk, int np, int cp
     pl->sg_elems = state * (size_t)pl->segs_per_group;
     pl->ld_elems = (size_t)d.n_seq * cpg * d.n_head;
     pl->sd_elems = (size_t)d.n_seq * pl->segs_per_group * d.n_head;
+    pl->bc_elems = bccopy ? (size_t)d.n_seq * (size_t)cpg * HELIX_CS * d.n_group * d.d_state : 0;
     size_t off = 0;
     pl->off_sl = off; off += align256(pl->sl_elems * pl->sl_elem_bytes);
     pl->off_sg = off; off += align256(pl->sg_elems * sizeof(float));
     pl->off_ld = off; off += align256(pl->ld_elems * sizeof(float));
     pl->off_sd = off; off += align256(pl->sd_elems * sizeof(float));
+    pl->off_bc = off; off += align256(pl->bc_elems * 2);
+    pl->off_cc = off; off += align256(pl->bc_elems * 2);
     pl->total_bytes = off;
 }
 
@@ -367,11 +395,12 @@ MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& 
                          (size_t)tr.np;
     // A walking Pass C keeps no per-chunk state; only segment aggregates
     // (about one state per seg_len chunks) count against the budget.
-    const size_t per_chunk = tr.walk ? state : state * (bf16_state ? 2 : 4);
+    const size_t bc_chunk = tr.bccopy ? (size_t)d.n_seq * HELIX_CS * d.n_group * d.d_state * 2 * 2 : 0;
+    const size_t per_chunk = (tr.walk ? state : state * (bf16_state ? 2 : 4)) + bc_chunk;
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(d, bf16_state, tr.walk, tr.np, (int)cpg, &pl);
+        layout(d, bf16_state, tr.walk, tr.bccopy, tr.np, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }

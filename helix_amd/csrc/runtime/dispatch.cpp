@@ -167,6 +167,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     params.sg_seq  = (long long)plan.segs_per_group * HT;
     params.ld_seq  = (long long)plan.chunks_per_group * d->n_head;
     params.sd_seq  = (long long)plan.segs_per_group * d->n_head;
+    params.cpg     = plan.chunks_per_group;
 
     HelixScanBuffers bufs;
     std::memset(&bufs, 0, sizeof(bufs));
@@ -184,6 +185,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     bufs.s_seg   = reinterpret_cast<float*>(sc + plan.off_sg);
     bufs.ld      = reinterpret_cast<float*>(sc + plan.off_ld);
     bufs.segld   = reinterpret_cast<float*>(sc + plan.off_sd);
+    bufs.bcopy   = plan.bc_elems ? sc + plan.off_bc : nullptr;
+    bufs.ccopy   = plan.bc_elems ? sc + plan.off_cc : nullptr;
 
     // Debug-only per-pass timing split (reference dispatch.mm:207-216):
     // HELIX_ONLY_PASS=A|B|C enqueues just that pass; the output is then
@@ -228,7 +231,26 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
                       (unsigned)d->n_seq
                 : (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) * (unsigned)d->n_seq;
             const unsigned threads = tr.walk ? HELIX_WG * hpw : HELIX_WG;
-            e = hipModuleLaunchKernel(fC, n_wg, 1, 1, threads, 1, 1, 0, stream, args, nullptr);
+            // With bf16 copies, Pass C reads B and C from them: dense
+            // [seq][t][group][n] rows counted from the group's first token.
+            // The base is moved back by that token so that the kernel's
+            // absolute row t0 lands on the group's row t0 - 64 base.
+            HelixScanParams pc = params;
+            HelixScanBuffers bc = bufs;
+            if (tr.bccopy) {
+                const long long gn = (long long)d->n_group * d->d_state;
+                for (long long* s3 : {pc.s_b, pc.s_c}) {
+                    s3[0] = gn;
+                    s3[1] = d->d_state;
+                    s3[2] = 1;
+                }
+                pc.seq_b = pc.seq_c = (long long)plan.chunks_per_group * HELIX_CS * gn;
+                const uintptr_t back = (uintptr_t)((long long)base * HELIX_CS * gn * 2);
+                bc.B = reinterpret_cast<const float*>(reinterpret_cast<uintptr_t>(bufs.bcopy) - back);
+                bc.C = reinterpret_cast<const float*>(reinterpret_cast<uintptr_t>(bufs.ccopy) - back);
+            }
+            void* args_c[] = {&pc, &bc};
+            e = hipModuleLaunchKernel(fC, n_wg, 1, 1, threads, 1, 1, 0, stream, args_c, nullptr);
         }
         if (e != hipSuccess) {
             (void)hipGetLastError();
@@ -293,6 +315,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->total_bytes = pl.total_bytes;
     out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
     out->s_seg_bytes = pl.sg_elems * sizeof(float);
+    out->bccopy_bytes = pl.bc_elems * 2 * 2;
     out->launches = 3 * pl.n_groups;
     out->np = tr.np;
     out->kernel_a = tr.k_chunk_state;

@@ -47,6 +47,8 @@ struct HelixMatmulTraits {
     const char*   k_single;
     // Heads per workgroup of a walking Pass C; 0 means HELIX_WALK_HPW(np).
     int           walk_hpw;
+    // Pass A writes bf16 copies of B and C that the walking Pass C reads.
+    bool          bccopy;
 };
 
 namespace helix::rt {
@@ -77,7 +79,8 @@ struct MultipassPlan {
     size_t sg_elems         = 0;   // s_seg elements (fp32)
     size_t ld_elems         = 0;
     size_t sd_elems         = 0;
-    size_t off_sl = 0, off_sg = 0, off_ld = 0, off_sd = 0;
+    size_t bc_elems         = 0;   // elements of each bf16 copy of B and C (0: none)
+    size_t off_sl = 0, off_sg = 0, off_ld = 0, off_sd = 0, off_bc = 0, off_cc = 0;
     size_t total_bytes      = 0;
 };
 

@@ -70,6 +70,10 @@ MODES = [
     ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}, True),
+    # The 16 x 16 walk on the caller's fp32 B and C instead of Pass A's bf16
+    # copies.
+    ("bf16walk/nocopy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk", "HELIX_WALK_BCCOPY": "0"},
+     True),
     # The walk on 32 x 32 tiles (the default walk runs 16 x 16 tiles).
     ("bf16walk32", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk", "HELIX_WALK": "32"}, True),
     ("bf16walk32/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk", "HELIX_WALK": "32"}, True),

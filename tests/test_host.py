@@ -253,10 +253,19 @@ def test_backend_selection(host):
             == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
+    # Pass A writes bf16 copies of B and C that the walking Pass C reads.
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
+        b"helix_chunk_state_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+    L, S, H, P, N, G = shape
+    assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
+    assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
+    with env(HELIX_WALK_BCCOPY="0"):
+        k0 = host.plan_info(mp(shape))
+        assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
+        assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
     with env(HELIX_WALK="32"):
-        assert host.plan_info(mp(shape)).kernel_c == b"helix_scan_walk_bf16_n128"
+        k32 = host.plan_info(mp(shape))
+        assert (k32.kernel_a, k32.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk_bf16_n128")
     with env(HELIX_BF16_PASSC="tile"):
         k = host.plan_info(mp(shape))
         assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
@@ -267,7 +276,7 @@ def test_backend_selection(host):
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
     with env(HELIX_BF16_PASSC="walk"):
         k = host.plan_info(mp(shape))
-        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
+        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
     with env(HELIX_X6="0"):
         k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
         assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_f32_n128", b"helix_chunk_out_f32_n128")
@@ -303,6 +312,28 @@ def test_backend_selection(host):
 # ---------------------------------------------------------------------------
 # Scratch planning (reference caps.mm:153-241)
 # ---------------------------------------------------------------------------
+
+def test_bc_copy_condition(host):
+    # The copies need the K = heads_per_group * n_pslab workgroups of a chunk
+    # to cover its 64 rows with two quads of four state indices per thread:
+    # ceil(64 / K) * d_state / 4 <= 512.
+    with env(HELIX_BF16_PASSC="walk"):
+        for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), False),
+                                   ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((1, 192, 128, 1), False),
+                                   ((2, 192, 128, 1), True), ((2, 64, 64, 1), True), ((1, 64, 64, 1), False)]:
+            d = mp((4096, 1, H, P, N, G))
+            k = host.plan_info(d)
+            assert (k.bccopy_bytes > 0) == copy, (H, P, N, G)
+            assert k.kernel_c.endswith(b"_n%d" % k.np)
+            assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
+    # Not with 16-bit storage (Pass C reads the caller's 16-bit B and C), nor
+    # with the fp32-MFMA Pass A.
+    d = mp((4096, 1, 64, 64, 128, 8))
+    d.io_dtype = HELIX_BF16
+    assert host.plan_info(d).bccopy_bytes == 0
+    with env(HELIX_X6="0"):
+        assert host.plan_info(mp((4096, 1, 64, 64, 128, 8))).bccopy_bytes == 0
+
 
 @pytest.mark.parametrize("passc", [None, "walk"])
 @pytest.mark.parametrize("name", list(CONFIG_SHAPES))
