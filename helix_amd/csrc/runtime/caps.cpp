@@ -343,17 +343,16 @@ int choose_seg_len(const helix_scan_desc& d, int cpg) {
     return (int)std::max<long>(1, std::min<long>(len, cpg));
 }
 
-// The bf16 path walks segments in Pass C (no per-chunk state in scratch)
-// when the plan gives full-length segments, where its lower traffic pays
-// for the longer per-workgroup chains; with short segments the
-// chunk-parallel Pass C is faster. Measured at config 2: 0.205 vs 0.209 ms;
-// config 4a: 0.936 vs 0.949 ms; config 3 (8-chunk segments): 0.111 vs
-// 0.102 ms. d_state 256 keeps the chunk-parallel kernel (one head per
-// walking workgroup there).
+// The bf16 path walks segments in Pass C (no per-chunk state in scratch):
+// with the 16 x 16 walk and Pass A's bf16 copies of B and C it is faster
+// than the chunk-parallel Pass C at every shape measured, short segments
+// included (one MI355X, total scan: config 1 66 vs 72 us, config 2 161 vs
+// 211, config 3 89 vs 100, config 4a 786 vs 952, config 4b 859 vs 937; L=512
+// 42 vs 48; d_state 256 at L=4096 H=32 G=1 128 vs 146; d_state 64 127 vs
+// 135). At d_state 256 it needs the copies: the walk on the caller's B and C
+// measured slower there (460 vs 427 us at L=8192 H=64 G=8).
 bool prefer_walk(const helix_scan_desc& d) {
-    if (d.d_state > 128) return false;
-    const long n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
-    return choose_seg_len(d, (int)std::min<long>(n_chunks, 1 << 30)) >= kMaxSegLen;
+    return d.d_state <= 128 || (walk16_on() && bccopy_on(d));
 }
 
 void layout(const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, int np, int cpg,

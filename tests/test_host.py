@@ -237,11 +237,14 @@ def test_backend_selection(host):
     # path's Pass C up to d_state 128.
     assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
-    # The bf16 path walks segments in Pass C when the plan gives full-length
-    # segments (d_state <= 128), and runs chunk-parallel otherwise.
+    # The bf16 path walks segments in Pass C up to d_state 128, and at d_state
+    # 256 when Pass A can write bf16 copies of B and C; chunk-parallel
+    # otherwise.
     assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
-            == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)")
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+    assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
     with env(HELIX_BF16_PASSC="tile"):
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C, pass A bf16x6 (d_state<=256)"
