@@ -41,19 +41,34 @@ REF_TOKS = 1315051.0
 
 CFG = dict(L=8192, S=1, H=64, P=64, N=128, G=8)
 
+# BASELINE.json's configurations (config 4 in its two head-dim variants): shape,
+# the paths each is quoted on, and the distributions that differ from the common
+# ones (h0 standard deviation, dt_raw mean and standard deviation).
+CONFIGS = [
+    dict(name="0", L=256, S=1, H=8, P=64, N=64, G=1, paths=("fp32",)),
+    dict(name="1", L=2048, S=1, H=64, P=64, N=128, G=8, paths=("fp32",)),
+    dict(name="2", L=8192, S=1, H=64, P=64, N=128, G=8, paths=("bf16", "fp32")),
+    dict(name="3", L=1000, S=4, H=32, P=128, N=128, G=1, paths=("fp32",), s0_sigma=0.1,
+         dt_mu=-2.0, dt_sigma=1.0),
+    dict(name="4a", L=4096, S=8, H=80, P=64, N=128, G=1, paths=("bf16",), s0_sigma=0.1),
+    dict(name="4b", L=4096, S=8, H=27, P=192, N=128, G=1, paths=("bf16",), s0_sigma=0.1),
+]
 
-def make_inputs(seed: int, dev):
-    """BASELINE.json config-2 distributions, generated on the device."""
-    L, S, H, P, N, G = (CFG[k] for k in "LSHPNG")
+
+def make_inputs(seed: int, dev, cfg=None):
+    """BASELINE.json distributions at a config's shape (config 2 by default),
+    generated on the device."""
+    cfg = cfg or dict(CFG)
+    L, S, H, P, N, G = (cfg[k] for k in "LSHPNG")
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     x = torch.randn((S, L, H, P), generator=g, device=dev)
-    dt = -1.0 + 0.5 * torch.randn((S, L, H), generator=g, device=dev)
+    dt = cfg.get("dt_mu", -1.0) + cfg.get("dt_sigma", 0.5) * torch.randn((S, L, H), generator=g, device=dev)
     A = -torch.exp(math.log(1.0) + (math.log(16.0) - math.log(1.0))
                    * torch.rand((H,), generator=g, device=dev))
     B = torch.randn((S, L, G, N), generator=g, device=dev) / math.sqrt(N)
     C = torch.randn((S, L, G, N), generator=g, device=dev) / math.sqrt(N)
-    s0 = torch.zeros((S, H, P, N), device=dev)
+    s0 = cfg.get("s0_sigma", 0.0) * torch.randn((S, H, P, N), generator=g, device=dev)
     return x, dt, A, B, C, s0
 
 
@@ -230,6 +245,45 @@ def cpu_baseline(budget_s: float = 20.0):
     return out
 
 
+def config_report(ctx, stream, dev, steps: int, warm_ms: float):
+    """Every BASELINE config on each path it is quoted on: tokens/s, GFLOP/s,
+    fraction of the op roofline and the per-pass split (medians of `steps`
+    event-timed encodes after `warm_ms` of warm-up). The roofline rule is the
+    headline's: max(F_A/fp32_peak + F_C/P_C, alg_bytes/8 TB/s), P_C the bf16
+    peak on the bf16 path and the fp32 peak on the fp32 path."""
+    out = {}
+    for i, cfg in enumerate(CONFIGS):
+        L, S, H, P, N, G = (cfg[k] for k in "LSHPNG")
+        tensors = make_inputs(1000 + i, dev, cfg)
+        F = algorithmic_flops(L, S, H, P, N)
+        F_A = 2.0 * S * H * ((L + 63) // 64) * 64 * N * P
+        nbytes = algorithmic_bytes(L, S, H, P, N, G)
+        for path in cfg["paths"]:
+            v = Variant(path, ctx, HELIX_BACKEND_MPP if path == "bf16" else HELIX_BACKEND_SGMMA, tensors)
+            for _ in range(3):
+                v.encode(stream)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            while (time.perf_counter() - t0) * 1e3 < warm_ms:
+                v.encode(stream)
+                torch.cuda.synchronize()
+            ms = dist(time_variant(v, steps, stream))["median"]
+            passes = time_passes(v, steps, stream)
+            peak_c = PEAK_BF16_MFMA if path == "bf16" else PEAK_FP32_MFMA
+            t_roof = max(F_A / PEAK_FP32_MFMA + (F - F_A) / peak_c, nbytes / PEAK_HBM)
+            out[f"{cfg['name']}/{path}"] = {
+                "shape": f"S={S} L={L} H={H} P={P} N={N} G={G}",
+                "tok_s": S * L / (ms * 1e-3), "gflops": F / (ms * 1e-3) / 1e9, "ms": ms,
+                "roofline_frac": t_roof / (ms * 1e-3), "t_roof_us": t_roof * 1e6,
+                "passes_us": {k: dist(ts)["median"] * 1e3 for k, ts in passes.items()},
+                "plan": {"groups": v.plan.n_groups, "seg_len": v.plan.seg_len},
+            }
+            del v
+        del tensors
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +294,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--variants", action="store_true",
                     help="also time alternative kernel choices (reported under 'variants')")
+    ap.add_argument("--config-steps", type=int, default=20,
+                    help="event-timed encodes per config and path in the per-config report "
+                         "(0 skips the report)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
                     help="also run a plain device copy of this size (a known-traffic kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -263,6 +320,8 @@ def main():
                                 env={"HELIX_BF16_PASSC": "tile"}))
         variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
+        variants.append(Variant("bf16-passA-x6", ctx, HELIX_BACKEND_MPP, tensors,
+                                env={"HELIX_PASSA_SPLIT": "6"}))
 
     def warm_up(v, ms):
         """W steps, then more until the wall clock has run `ms` (the
@@ -336,11 +395,11 @@ def main():
         "scaling": "weak",
         "vs_baseline": value / REF_TOKS,
         "dtype": "bf16",
-        "data": "synthetic (BASELINE.json config 2 distributions, torch RNG seed 1002)",
+        "data": "synthetic (BASELINE.json distributions; config 2 on torch RNG seed 1002, config i of the per-config report on seed 1000+i)",
         "config": {
             "workload": "config 2: SSD prefill scan S=1 L=8192 H=64 P=64 N=128 G=8 chunk=64, "
-                        "bf16 Pass C operands, Pass A on bf16x6 split products (fp32-accurate "
-                        "state), fp32 Pass B, inputs resident in HBM",
+                        "bf16 Pass C operands, Pass A on bf16x3 split products (state to about "
+                        "2^-16 relative), fp32 Pass B, inputs resident in HBM",
             "kernel": r["kernel"],
             "plan": {"groups": plan.n_groups, "seg_len": plan.seg_len, "hblk": plan.hblk,
                      "scratch_MiB": plan.total_bytes / 2**20},
@@ -372,6 +431,9 @@ def main():
             if rv["passes"]:
                 e["passes_ms_median"] = {k: rv["passes"][k]["median"] for k in "ABC"}
             out["variants"][v.name] = e
+    if args.config_steps > 0:
+        out["configs"] = config_report(ctx, stream, dev, args.config_steps,
+                                       min(args.warmup_ms, 100.0))
     if args.calib_copy:
         n = args.calib_copy * (1 << 20) // 4
         src = torch.randn(n, device=dev)

@@ -290,6 +290,14 @@ HELIX_DEV void split3_pair(float a, float b, unsigned& w0, unsigned& w1, unsigne
     w2 = pk_bf16(ra - pk_lo(w1), rb - pk_hi(w1));
 }
 
+// Two-way bf16 split of the pair (a, b): v = v0 + v1 + e with |e| <= 2^-18 |v|,
+// 6 VALU operations for two values. Three products a0b0 + a0b1 + a1b0 leave
+// out terms of at most 3 * 2^-18 of |ab| (about 1.1e-5).
+HELIX_DEV void split2_pair(float a, float b, unsigned& w0, unsigned& w1) {
+    w0 = pk_bf16(a, b);
+    w1 = pk_bf16(a - pk_lo(w0), b - pk_hi(w0));
+}
+
 // Six-product MFMA of split operands a[3] x b[3], smallest terms first.
 HELIX_DEV f32x16 mfma_x6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 acc) {
     acc = mfma_bf16(a[2], b[0], acc);

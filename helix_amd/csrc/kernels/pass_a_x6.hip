@@ -165,36 +165,46 @@ __device__ __forceinline__ void store_copy_bc(const CopyBC& cp, const CopyMap& m
     }
 }
 
-// Stage 16 consecutive tokens (chunks c0, c0 + 1) of row r of a three-plane
-// operand from fp32 values v[0..15].
-template <int ROWS>
-HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[16]) {
+// Split eight fp32 values v[0..7] into NS bf16 planes (NS = 3: split3_pair,
+// NS = 2: split2_pair) and store them as chunk c of row r.
+template <int ROWS, int NS>
+HELIX_DEV void stage_split8(__bf16* planes, int r, int c, const float* v) {
+    u32x4 q[NS];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        u32x4 q0, q1, q2;
+    for (int e = 0; e < 4; ++e) {
+        unsigned w[3];
+        if constexpr (NS == 3)
+            split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
+        else
+            split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            unsigned w0, w1, w2;
-            split3_pair(v[8 * half + 2 * e], v[8 * half + 2 * e + 1], w0, w1, w2);
-            q0[e] = w0;
-            q1[e] = w1;
-            q2[e] = w2;
-        }
-        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(0, r, c0 + half)]) = q0;
-        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(1, r, c0 + half)]) = q1;
-        *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(2, r, c0 + half)]) = q2;
+        for (int k = 0; k < NS; ++k) q[k][e] = w[k];
     }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(k, r, c)]) = q[k];
+}
+
+// Stage 16 consecutive tokens (chunks c0, c0 + 1) of row r of an NS-plane
+// operand from fp32 values v[0..15].
+template <int ROWS, int NS>
+HELIX_DEV void stage_split_row(__bf16* planes, int r, int c0, const float (&v)[16]) {
+    stage_split8<ROWS, NS>(planes, r, c0, v);
+    stage_split8<ROWS, NS>(planes, r, c0 + 1, v + 8);
 }
 
 // MODE as in pass_a.hip: 0 store R_c fp32, 1 store R_c bf16, 2 aggregates only.
 // IO: the caller's storage type of x and B. BCC: also write the bf16 copies
-// of B and C (fp32 storage only).
-template <int NP, int MODE, typename IO = float, bool BCC = false>
+// of B and C (fp32 storage only). NS: bf16 planes per operand, 3 (six
+// products, fp32 accuracy) or 2 (three products, about 2^-16 relative; the
+// segment aggregates that only the bf16 path's walking Pass C and Pass B
+// consume).
+template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3>
 __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(NS == 2 || NS == 3, "two or three split planes");
     constexpr bool SBF = MODE == 1;
     constexpr int NTW = NP / 64;      // N tiles per wave
-    __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];
-    __shared__ __attribute__((aligned(16))) __bf16 sXt[3 * HELIX_HD * HELIX_CS];
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[NS * NP * HELIX_CS];
+    __shared__ __attribute__((aligned(16))) __bf16 sXt[NS * HELIX_HD * HELIX_CS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
@@ -253,24 +263,15 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = bcast(cf, 16 * wave + i) * io_widen<IO>(st.x[i]);
-            stage_split_row<HELIX_HD>(sXt, lane, 2 * wave, v);
+            stage_split_row<HELIX_HD, NS>(sXt, lane, 2 * wave, v);
         }
         // B^T rows NB lo + k, chunk 2 wave + hi (tokens 16 wave + 8 hi + e).
 #pragma unroll
         for (int k = 0; k < NP / 32; ++k) {
-            u32x4 q0, q1, q2;
+            float v[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                unsigned w0, w1, w2;
-                split3_pair(x6_b(st, 2 * e, k), x6_b(st, 2 * e + 1, k), w0, w1, w2);
-                q0[e] = w0;
-                q1[e] = w1;
-                q2[e] = w2;
-            }
-            const int rn = (NP / 32) * lo + k;
-            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(0, rn, 2 * wave + hi)]) = q0;
-            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(1, rn, 2 * wave + hi)]) = q1;
-            *reinterpret_cast<u32x4*>(&sBt[x6_off<NP, 8>(2, rn, 2 * wave + hi)]) = q2;
+            for (int e = 0; e < 8; ++e) v[e] = x6_b(st, e, k);
+            stage_split8<NP, NS>(sBt, (NP / 32) * lo + k, 2 * wave + hi, v);
         }
 
         if constexpr (BCC) store_copy_bc(cp, cmap, p, b, seq, g, c, N);
@@ -313,21 +314,26 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
 #pragma unroll
         for (int s = 0; s < HELIX_CS / 16; ++s) {
             const int cx = 2 * s + hi;
-            const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(0, pt * 32 + lo, cx)]);
-            const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(1, pt * 32 + lo, cx)]);
-            const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(2, pt * 32 + lo, cx)]);
+            bf16x8 xs[NS];
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+                xs[k] = *reinterpret_cast<const bf16x8*>(&sXt[x6_off<HELIX_HD, 8>(k, pt * 32 + lo, cx)]);
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
                 const int rn = (nt0 + 2 * i) * 32 + lo;
-                const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(0, rn, cx)]);
-                const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(1, rn, cx)]);
-                const bf16x8 b2 = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(2, rn, cx)]);
-                acc[i] = mfma_bf16(b2, x0, acc[i]);
-                acc[i] = mfma_bf16(b1, x1, acc[i]);
-                acc[i] = mfma_bf16(b0, x2, acc[i]);
-                acc[i] = mfma_bf16(b1, x0, acc[i]);
-                acc[i] = mfma_bf16(b0, x1, acc[i]);
-                acc[i] = mfma_bf16(b0, x0, acc[i]);
+                bf16x8 bs[NS];
+#pragma unroll
+                for (int k = 0; k < NS; ++k)
+                    bs[k] = *reinterpret_cast<const bf16x8*>(&sBt[x6_off<NP, 8>(k, rn, cx)]);
+                // Smallest terms first.
+                if constexpr (NS == 3) {
+                    acc[i] = mfma_bf16(bs[2], xs[0], acc[i]);
+                    acc[i] = mfma_bf16(bs[1], xs[1], acc[i]);
+                    acc[i] = mfma_bf16(bs[0], xs[2], acc[i]);
+                }
+                acc[i] = mfma_bf16(bs[1], xs[0], acc[i]);
+                acc[i] = mfma_bf16(bs[0], xs[1], acc[i]);
+                acc[i] = mfma_bf16(bs[0], xs[0], acc[i]);
             }
         }
         lam += (float)lend;
@@ -378,6 +384,27 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         chunk_state_x6_impl<NP, 2, float, true>(p, b);                                          \
     }
 
+// Segment aggregates on two split planes (three products) for the bf16 path's
+// walking Pass C: fp32 storage, with and without the bf16 copies of B and C,
+// and 16-bit storage of x and B.
+#define HELIX_PASS_A_X3(NP)                                                                     \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x3agg_n##NP(        \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, float, false, 2>(p, b);                                      \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x3agg_bc_n##NP(     \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, float, true, 2>(p, b);                                       \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x3agg_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, __bf16, false, 2>(p, b);                                     \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x3agg_f16io_n##NP(  \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        chunk_state_x6_impl<NP, 2, _Float16, false, 2>(p, b);                                   \
+    }
+
 // Aggregates from 16-bit storage of x and B (io_dtype BF16 / F16), for the
 // chunk-walking Pass C.
 #define HELIX_PASS_A_X6_IO(NP)                                                                  \
@@ -396,3 +423,6 @@ HELIX_PASS_A_X6(256)
 HELIX_PASS_A_X6_IO(64)
 HELIX_PASS_A_X6_IO(128)
 HELIX_PASS_A_X6_IO(256)
+HELIX_PASS_A_X3(64)
+HELIX_PASS_A_X3(128)
+HELIX_PASS_A_X3(256)

@@ -105,6 +105,15 @@ constexpr const char* kWalk16Bc[] = {"helix_scan_walk16_bf16_bc_n64", "helix_sca
 constexpr const char* kX6StateAggBc[] = {"helix_chunk_state_x6agg_bc_n64", "helix_chunk_state_x6agg_bc_n128",
                                          "helix_chunk_state_x6agg_bc_n256"};
 constexpr const char* kX6OutF32[] = {"helix_chunk_out_x6_n64", "helix_chunk_out_x6_n128", nullptr};
+// Pass A on two split planes (three bf16 products, about 2^-16 relative per
+// product) for the walking bf16 Pass C, whose own operands are bf16: the
+// segment aggregates it and Pass B consume stay 500x more accurate than
+// Pass C's output. HELIX_PASSA_SPLIT=6 keeps the six-product kernels.
+constexpr const char* kX3StateAgg[] = {"helix_chunk_state_x3agg_n64", "helix_chunk_state_x3agg_n128",
+                                       "helix_chunk_state_x3agg_n256"};
+constexpr const char* kX3StateAggBc[] = {"helix_chunk_state_x3agg_bc_n64", "helix_chunk_state_x3agg_bc_n128",
+                                         "helix_chunk_state_x3agg_bc_n256"};
+constexpr const char* kMfmaX3 = "v_mfma_f32_32x32x16_bf16 (bf16x3 split operands)";
 
 // The selectable trait sets: [family: fp32, bf16, bf16 walk][np index], with
 // Pass A on fp32 MFMA or bf16x6. Built once; names live as long as the process.
@@ -112,7 +121,8 @@ struct TraitSets {
     HelixMatmulTraits t[2][3][3];
     HelixMatmulTraits w16[2][3];   // the walk family with the 16 x 16 tile Pass C
     HelixMatmulTraits w16bc[3];    // ... reading bf16 B and C copies from Pass A (bf16x6)
-    std::string names[2][3][3];
+    HelixMatmulTraits w16x3[3], w16x3bc[3];   // the same two with Pass A on bf16x3
+    std::string names[2][3][3], x3names[2][3];
     TraitSets() {
         const HelixMatmulTraits* base[3] = {kF32Traits, kBf16Traits, kBf16WalkTraits};
         const char* const* x6[3] = {kX6StateF32, kX6StateSbf, kX6StateAgg};
@@ -147,8 +157,30 @@ struct TraitSets {
             w16bc[k].k_chunk_out = kWalk16Bc[k];
             w16bc[k].bccopy = true;
         }
+        for (int k = 0; k < 3; ++k) {
+            HelixMatmulTraits* dst[2] = {&w16x3[k], &w16x3bc[k]};
+            const HelixMatmulTraits* src[2] = {&w16[1][k], &w16bc[k]};
+            const char* ka[2] = {kX3StateAgg[k], kX3StateAggBc[k]};
+            for (int i = 0; i < 2; ++i) {
+                *dst[i] = *src[i];
+                std::string nm = src[i]->name;
+                const size_t at = nm.find("bf16x6");
+                if (at != std::string::npos) nm.replace(at, 6, "bf16x3");
+                x3names[i][k] = nm;
+                dst[i]->name = x3names[i][k].c_str();
+                dst[i]->k_chunk_state = ka[i];
+                dst[i]->mfma_a = kMfmaX3;
+            }
+        }
     }
 };
+
+// Pass A of the walking bf16 path on two split planes unless
+// HELIX_PASSA_SPLIT=6.
+bool passa_x3_on() {
+    const char* v = std::getenv("HELIX_PASSA_SPLIT");
+    return !(v && v[0] == '6');
+}
 
 // Pass A writes bf16 copies of B and C for the walking Pass C (fp32
 // storage, bf16x6 Pass A) unless HELIX_WALK_BCCOPY=0, when the K =
@@ -172,7 +204,10 @@ const HelixMatmulTraits& pick_traits(int fam, int k, const helix_scan_desc& d) {
     static const TraitSets sets;
     const char* v = std::getenv("HELIX_X6");
     const int x6 = (v && v[0] == '0') ? 0 : 1;
-    if (fam == 2 && walk16_on()) return (x6 && bccopy_on(d)) ? sets.w16bc[k] : sets.w16[x6][k];
+    if (fam == 2 && walk16_on()) {
+        if (x6 && passa_x3_on()) return bccopy_on(d) ? sets.w16x3bc[k] : sets.w16x3[k];
+        return (x6 && bccopy_on(d)) ? sets.w16bc[k] : sets.w16[x6][k];
+    }
     return sets.t[x6][fam][k];
 }
 
@@ -183,8 +218,8 @@ const HelixMatmulTraits& pick_traits(int fam, int k, const helix_scan_desc& d) {
 bool walk16_on();
 
 struct IoTraitSets {
-    HelixMatmulTraits t[2][2][3], w16[2][3];
-    std::string names[2][2][3], ka[2][3], kc[2][3], k1[2][3], kc16[2][3];
+    HelixMatmulTraits t[2][2][3], w16[2][3], w16x3[2][3];
+    std::string names[2][2][3], ka[2][3], kc[2][3], k1[2][3], kc16[2][3], ka3[2][3], names3[2][3];
     IoTraitSets() {
         const char* io[2] = {"bf16", "f16"};
         const int nps[3] = {64, 128, 256};
@@ -208,13 +243,20 @@ struct IoTraitSets {
                 w16[i][k].k_chunk_out = kc16[i][k].c_str();
                 w16[i][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[i][k].walk_hpw = HELIX_WALK16_HPW(nps[k]);
+                ka3[i][k] = std::string("helix_chunk_state_x3agg_") + io[i] + "io_n" + np;
+                names3[i][k] = std::string("mfma bf16 pass C, chunk walk, pass A bf16x3, ") + io[i] +
+                               " storage (d_state<=" + np + ")";
+                w16x3[i][k] = w16[i][k];
+                w16x3[i][k].name = names3[i][k].c_str();
+                w16x3[i][k].k_chunk_state = ka3[i][k].c_str();
+                w16x3[i][k].mfma_a = kMfmaX3;
             }
     }
 };
 
 const HelixMatmulTraits& io_traits(helix_dtype io, bool walk, int k) {
     static const IoTraitSets sets;
-    if (walk && walk16_on()) return sets.w16[io == HELIX_F16 ? 1 : 0][k];
+    if (walk && walk16_on()) return (passa_x3_on() ? sets.w16x3 : sets.w16)[io == HELIX_F16 ? 1 : 0][k];
     return sets.t[io == HELIX_F16 ? 1 : 0][walk ? 0 : 1][k];
 }
 
@@ -243,6 +285,10 @@ const char* const kKernelNames[] = {
     "helix_scan_walk16_bf16_f16io_n64",   "helix_scan_walk16_bf16_f16io_n128",   "helix_scan_walk16_bf16_f16io_n256",
     "helix_scan_walk16_bf16_bc_n64",      "helix_scan_walk16_bf16_bc_n128",      "helix_scan_walk16_bf16_bc_n256",
     "helix_chunk_state_x6agg_bc_n64",     "helix_chunk_state_x6agg_bc_n128",     "helix_chunk_state_x6agg_bc_n256",
+    "helix_chunk_state_x3agg_n64",        "helix_chunk_state_x3agg_n128",        "helix_chunk_state_x3agg_n256",
+    "helix_chunk_state_x3agg_bc_n64",     "helix_chunk_state_x3agg_bc_n128",     "helix_chunk_state_x3agg_bc_n256",
+    "helix_chunk_state_x3agg_bf16io_n64", "helix_chunk_state_x3agg_bf16io_n128", "helix_chunk_state_x3agg_bf16io_n256",
+    "helix_chunk_state_x3agg_f16io_n64",  "helix_chunk_state_x3agg_f16io_n128",  "helix_chunk_state_x3agg_f16io_n256",
 };
 
 int np_index(int d_state) {

@@ -30,7 +30,7 @@ from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND
                             HELIX_ERR_INVALID_ARG, HELIX_ERR_SCRATCH_TOO_SMALL,
                             HELIX_ERR_UNSUPPORTED_SHAPE, HELIX_OK, HELIX_TENSOR_NULL, HelixTensor,
                             desc_init)
-from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, T, env, run, upload
+from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, T, env, run, s1_tolerance, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -91,6 +91,7 @@ def test_state_splitting(gpu, split_problem, path, split):
     p, y_ref, s_ref = split_problem
     first, second = _sub(p, 0, split), _sub(p, split, p.d.n_tok)
     with env(**extra):
+        s_rel, s_abs = s1_tolerance(gpu, _desc(p, backend, multipass))
         s_mid = torch.full(first.s_shape(), float("nan"), device="cuda")
         _, y1, _ = run(gpu, first, desc=_desc(first, backend, multipass), s1_gpu=s_mid)
         _, y2, s1 = run(gpu, second, desc=_desc(second, backend, multipass), s0_gpu=s_mid)
@@ -103,9 +104,10 @@ def test_state_splitting(gpu, split_problem, path, split):
           flush=True)
     assert np.all(np.isfinite(y_split)) and np.all(np.isfinite(s1))
     assert e_ref <= gate and e_self <= gate
-    # The carried state never passes through bf16 on any path.
+    # The carried state never passes through bf16 on any path (fp32 bound, or
+    # the bf16x3 bound of the walking bf16 path's default Pass A).
     assert es_ref <= F32_GATE and _rel(s1, s1_full) <= F32_GATE
-    assert po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0
+    assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
 
 
 # ---------------------------------------------------------------------------

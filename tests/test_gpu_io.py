@@ -22,7 +22,7 @@ from oracle import pyoracle as po
 from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_F16,
                             HELIX_OK, HELIX_TENSOR_NULL)
 from baseline_configs import CONFIGS
-from gpu_harness import BF16_ABS, BF16_GATE, BF16_REL, F32_ABS, F32_GATE, F32_REL, T
+from gpu_harness import BF16_ABS, BF16_GATE, BF16_REL, F32_ABS, F32_GATE, F32_REL, X3_ABS, X3_REL, T
 
 pytestmark = pytest.mark.gpu
 
@@ -79,7 +79,9 @@ def check(io, desc, y, s1, y_ref, s_ref):
     else:
         assert ey <= F32_GATE + U[io], ey
         assert po.allclose_ratio(y, y_ref, F32_REL + U[io], F32_ABS) <= 1.0
-    assert es <= F32_GATE and po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0, es
+    # s1 at the fp32 bound, or the bf16x3 bound when Pass A runs three products.
+    s_rel, s_abs = (X3_REL, X3_ABS) if "pass A bf16x3" in desc else (F32_REL, F32_ABS)
+    assert es <= F32_GATE and po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0, es
     return ey, es
 
 

@@ -190,11 +190,15 @@ def test_16bit_storage_selection(host, io, name):
     d = mp(shape)
     d.io_dtype = io
     assert host.supported(d)
-    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
+    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x3, {name} storage (d_state<=128)"
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_chunk_state_x3agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
+    with env(HELIX_PASSA_SPLIT="6"):       # Pass A on six split products
+        assert host.plan_info(d).kernel_a == f"helix_chunk_state_x6agg_{name}io_n128".encode()
+        assert host.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage "
+                                        "(d_state<=128)")
     assert k.total_bytes == host.scratch_size(d) > 0 and k.s_local_bytes == 0
     with env(HELIX_BF16_PASSC="tile"):     # only the walk reads 16-bit operands
         assert host.plan_info(d).kernel_c == f"helix_scan_walk16_bf16_{name}io_n128".encode()
@@ -240,31 +244,35 @@ def test_backend_selection(host):
     # The bf16 path walks segments in Pass C up to d_state 128, and at d_state
     # 256 when Pass A can write bf16 copies of B and C; chunk-parallel
     # otherwise.
-    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
+    # Its Pass A runs three split products (bf16x3); HELIX_PASSA_SPLIT=6 six.
+    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+            == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)")
     assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
+            == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=256)")
+    with env(HELIX_PASSA_SPLIT="6"):
+        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
+        assert host.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_x6agg_bc_n128"
     with env(HELIX_BF16_PASSC="tile"):
         assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
     assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C, pass A bf16x6 (d_state<=256)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
     with env(HELIX_BF16_PASSC="walk"):
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
+        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     # Pass A writes bf16 copies of B and C that the walking Pass C reads.
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+        b"helix_chunk_state_x3agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
     L, S, H, P, N, G = shape
     assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
     assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
     with env(HELIX_WALK_BCCOPY="0"):
         k0 = host.plan_info(mp(shape))
-        assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
+        assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x3agg_n128", b"helix_scan_walk16_bf16_n128")
         assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
     with env(HELIX_WALK="32"):
         k32 = host.plan_info(mp(shape))
@@ -279,7 +287,7 @@ def test_backend_selection(host):
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
     with env(HELIX_BF16_PASSC="walk"):
         k = host.plan_info(mp(shape))
-        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
+        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x3agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
     with env(HELIX_X6="0"):
         k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
         assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_f32_n128", b"helix_chunk_out_f32_n128")
