@@ -103,6 +103,9 @@ typedef struct HelixScanParams {
     int n_hblk;           /* head blocks per B/C group */
     int np;               /* d_state padded to the kernels' tile width (64/128/256) */
     int cpg;              /* chunks per group of the plan (scratch strides) */
+    int fuse_b;           /* 1 => no Pass B launch: the walking Pass C forms S_seg
+                             from s0 and the aggregates D_s, and its last segment
+                             writes s1 (single-group plans only) */
 
     /* Scratch strides in elements (see the layout comment above). */
     long long sl_cg, sl_seq;     /* s_local: chunk stride (H*n_pslab*64*np), seq stride */

@@ -150,6 +150,7 @@ struct TraitSets {
                 w16[x6][k].k_chunk_out = kWalk16[k];
                 w16[x6][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[x6][k].walk_hpw = HELIX_WALK16_HPW(64 << k);
+                w16[x6][k].walk_fuse_b = true;
             }
         for (int k = 0; k < 3; ++k) {
             w16bc[k] = w16[1][k];
@@ -243,6 +244,7 @@ struct IoTraitSets {
                 w16[i][k].k_chunk_out = kc16[i][k].c_str();
                 w16[i][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[i][k].walk_hpw = HELIX_WALK16_HPW(nps[k]);
+                w16[i][k].walk_fuse_b = true;
                 ka3[i][k] = std::string("helix_chunk_state_x3agg_") + io[i] + "io_n" + np;
                 names3[i][k] = std::string("mfma bf16 pass C, chunk walk, pass A bf16x3, ") + io[i] +
                                " storage (d_state<=" + np + ")";
@@ -360,6 +362,12 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
         return pick_traits(prefer_walk(d) ? 2 : 1, k, d);
     }
     return pick_traits(0, k, d);
+}
+
+bool fuse_b_on(const HelixMatmulTraits& tr, const MultipassPlan& plan) {
+    const char* v = std::getenv("HELIX_FUSE_B");
+    if (v && v[0] == '0') return false;
+    return tr.walk_fuse_b && plan.n_groups == 1;
 }
 
 size_t scratch_budget_bytes() {

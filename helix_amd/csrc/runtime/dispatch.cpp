@@ -168,6 +168,10 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     params.ld_seq  = (long long)plan.chunks_per_group * d->n_head;
     params.sd_seq  = (long long)plan.segs_per_group * d->n_head;
     params.cpg     = plan.chunks_per_group;
+    // A single-group plan on a walking Pass C that runs Pass B's segment scan
+    // itself: no Pass B launch.
+    const bool fuse_b = helix::rt::fuse_b_on(tr, plan);
+    params.fuse_b  = fuse_b ? 1 : 0;
 
     HelixScanBuffers bufs;
     std::memset(&bufs, 0, sizeof(bufs));
@@ -219,7 +223,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fA, (unsigned)params.n_seg, (unsigned)d->n_head,
                                       (unsigned)(d->n_seq * params.n_pslab), HELIX_WG, 1, 1, 0,
                                       stream, args, nullptr);
-        if (e == hipSuccess && do_b)
+        if (e == hipSuccess && do_b && !fuse_b)
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c) {
@@ -316,10 +320,11 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
     out->s_seg_bytes = pl.sg_elems * sizeof(float);
     out->bccopy_bytes = pl.bc_elems * 2 * 2;
-    out->launches = 3 * pl.n_groups;
+    const bool fuse_b = helix::rt::fuse_b_on(tr, pl);   // as helix_scan_encode decides
+    out->launches = fuse_b ? 2 : 3 * pl.n_groups;
     out->np = tr.np;
     out->kernel_a = tr.k_chunk_state;
-    out->kernel_b = tr.k_state_scan;
+    out->kernel_b = fuse_b ? nullptr : tr.k_state_scan;
     out->kernel_c = tr.k_chunk_out;
     return HELIX_OK;
 }

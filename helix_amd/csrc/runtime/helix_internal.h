@@ -49,6 +49,10 @@ struct HelixMatmulTraits {
     int           walk_hpw;
     // Pass A writes bf16 copies of B and C that the walking Pass C reads.
     bool          bccopy;
+    // The walking Pass C can run Pass B's segment scan in its prologue
+    // (HelixScanParams::fuse_b); the encoder then skips Pass B's launch
+    // whenever the plan has a single group.
+    bool          walk_fuse_b;
 };
 
 namespace helix::rt {
@@ -85,6 +89,10 @@ struct MultipassPlan {
 };
 
 MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& tr);
+
+// Whether the walking Pass C runs Pass B's segment scan itself (no Pass B
+// launch): a single-group plan on a kernel that can, unless HELIX_FUSE_B=0.
+bool fuse_b_on(const HelixMatmulTraits& tr, const MultipassPlan& plan);
 
 // Scratch budget in bytes: $HELIX_SCRATCH_MB or the default.
 size_t scratch_budget_bytes();

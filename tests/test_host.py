@@ -193,7 +193,7 @@ def test_16bit_storage_selection(host, io, name):
     assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x3, {name} storage (d_state<=128)"
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_x3agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_chunk_state_x3agg_{name}io_n128".encode(), None,
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
     with env(HELIX_PASSA_SPLIT="6"):       # Pass A on six split products
         assert host.plan_info(d).kernel_a == f"helix_chunk_state_x6agg_{name}io_n128".encode()
@@ -265,8 +265,14 @@ def test_backend_selection(host):
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     # Pass A writes bf16 copies of B and C that the walking Pass C reads.
+    # Pass B runs in the walk's prologue (single group): no kernel of its own.
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x3agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+        b"helix_chunk_state_x3agg_bc_n128", None, b"helix_scan_walk16_bf16_bc_n128")
+    assert k.launches == 2
+    with env(HELIX_SCRATCH_MB="1"):        # many groups: Pass B carries them through s1
+        km = host.plan_info(mp(shape))
+        assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
+        assert km.launches == 3 * km.n_groups
     L, S, H, P, N, G = shape
     assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
     assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
@@ -387,7 +393,11 @@ def _plan_invariants(host, name, backend):
     # every region 256-byte aligned and the total covers them all
     assert info.total_bytes % 256 == 0
     assert info.total_bytes >= want_sl + info.s_seg_bytes
-    assert info.launches == 3 * info.n_groups
+    # The 16 x 16 walk runs Pass B's segment scan in its prologue when the plan
+    # has one group: no Pass B launch.
+    fused = b"walk16" in info.kernel_c and info.n_groups == 1
+    assert info.launches == (2 if fused else 3 * info.n_groups)
+    assert (info.kernel_b is None) == fused
 
 
 def test_plan_single_group_for_baseline_configs(host):
