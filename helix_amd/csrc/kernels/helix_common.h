@@ -500,8 +500,39 @@ HELIX_DEV int sgpr_fresh(int v) {
     return v;
 }
 
+// Load of a wave-uniform element through the scalar unit (s_load, counted by
+// lgkmcnt): reading through the constant address space tells the compiler the
+// data does not change during the kernel (an input, or what an earlier launch
+// wrote). A vector load would join the in-order vmcnt queue, so waiting for
+// it would also wait for every load issued before it.
+HELIX_DEV float sload_f32(const float* p, long long i) {
+    return ((const __attribute__((address_space(4))) float*)p)[i];
+}
+HELIX_DEV int sload_i32(const int* p, long long i) {
+    return ((const __attribute__((address_space(4))) int*)p)[i];
+}
+
 // This thread's wave index, as a wave-uniform (SGPR) value: everything derived
 // from it (row offsets, branch conditions) then stays scalar.
 HELIX_DEV int wave_uniform() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// The decay record of token t = lane of chunk c (group-local) of head h, as
+// the walking Pass C uses it: {dt_t, exp(L_end - Lcum_t), Lcum_t log2(e),
+// exp(Lcum_t)}, with dt and the decay zero past tlen. Pass A forms dt_t,
+// Lcum_t and L_end for its own GEMM; storing these four values once per
+// (seq, chunk, head) spares the walk's four waves per head recomputing the
+// softplus and the fp64 scan every chunk. exp(L_end) is the record of token
+// 63 (Lcum_63 = L_end).
+HELIX_DEV void store_decay_record(const HelixScanParams& p, const HelixScanBuffers& b, int seq, int c, int h,
+                                  int lane, int tlen, float dtv, double lcum, double lend) {
+    const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
+    const float l2 = (float)(lcum * 1.4426950408889634074);
+    const float e = expf((float)lcum);
+    const float* rec = b.pre + (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 4);
+    const helix_rsrc r = make_rsrc(rec, HELIX_CS * 16u);
+    const u32x4 w = {__builtin_bit_cast(unsigned, dtv), __builtin_bit_cast(unsigned, sdec),
+                     __builtin_bit_cast(unsigned, l2), __builtin_bit_cast(unsigned, e)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, lane * 16, 0, 0);
+}
 
 #endif  // HELIX_COMMON_H

@@ -132,6 +132,9 @@ typedef struct HelixScanBuffers {
     float*       segld;
     void*        bcopy;   /* bf16 copies of B and C (see the layout above), or null */
     void*        ccopy;
+    float*       pre;     /* per-token decay records [seq][chunk][head][64][4] that
+                             Pass A writes for the 16 x 16 walk, or null:
+                             {dt, exp(L_end - Lcum), Lcum log2(e), exp(Lcum)} */
 } HelixScanBuffers;
 
 #endif /* HELIX_PARAMS_H */

@@ -139,6 +139,8 @@ __device__ __forceinline__ void chunk_state_impl(const HelixScanParams& p, const
         const double lcum = wave_incl_sum((double)A_h * (double)dtv);
         const double lend = __shfl(lcum, 63, 64);
         const float cf = (lane < tlen) ? exp_diff(lend, lcum) * dtv : 0.0f;
+        if (MODE == 2 && b.pre && wave == 0 && slab == 0)
+            store_decay_record(p, b, seq, c, h, lane, tlen, dtv, lcum, lend);
 
         // dtXs[j][p] = exp(L_end - Lcum_j) dt_j x[j][p] (cf_j = 0 past tlen);
         // B[j][n] zero past tlen and d_state.

@@ -52,26 +52,26 @@ HELIX_DEV int g1_jb(int idx) {
     return idx - tb * (tb + 1) / 2;
 }
 
-// x of tokens 16 wave + i at channel p = lane and dt of token lane, prefetched
-// a chunk ahead in storage form.
+// x of tokens 16 wave + i at channel p = lane and the decay record of token
+// lane (Pass A's store_decay_record), prefetched a chunk ahead in storage form.
 template <typename IO>
 struct StageW16 {
-    float dtraw;
+    u32x4 rec;
     typename IoWord<IO>::type x[16];
 };
 
 template <typename IO>
 __device__ __forceinline__ void load_stage_w16(StageW16<IO>& st, const HelixScanParams& p,
-                                               const float* __restrict__ dt_h,
+                                               const float* __restrict__ rec_h,
                                                const IO* __restrict__ x_h, int c, int lane,
                                                int wave, int pw) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
-    const int sdt = (int)p.s_dt[0], sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
-    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    const int sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
     const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0],
                                      ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
-    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
@@ -166,6 +166,12 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     constexpr int RS  = NP + 8;               // bf16 row stride of C[t][n], B[j][n]
     constexpr int RSJ = HELIX_CS + 8;         // bf16 row stride of B^T, dtX^T, dtXs^T, M
     constexpr int NCH = NP / 8;               // 8-element runs per C / B row
+    // B^T[n][j] sits at row n, 16-byte chunk (j / 8) ^ ((n / 16) % 8). The
+    // staging writes are a transpose: one instruction writes column j of rows
+    // 8 u + e for eight u, which without the swizzle share one bank row
+    // (8-way conflicts); G4's 16-byte reads take 16 consecutive rows of one
+    // chunk, which the swizzle leaves in distinct banks.
+    auto bt_off = [](int n, int j) { return n * RSJ + (((j >> 3) ^ ((n >> 4) & 7)) << 3) + (j & 7); };
 
     // M takes the place of B's rows when they fit (B is dead once G1 has read
     // it): G1 then keeps its blocks in registers until every wave is past
@@ -212,8 +218,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     const int c_end   = min(c_begin + p.seg_len, p.n_cg);
     if (c_begin >= c_end) return;
 
-    const float A_h = b.A[(long long)h * p.s_a];
-    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    // Decay records of this head, chunk stride n_head * 64 records.
+    const float* __restrict__ rec_h = b.pre + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * 4);
     const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
     const BIO* __restrict__ B_g = reinterpret_cast<const BIO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
     const BIO* __restrict__ C_g = reinterpret_cast<const BIO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
@@ -248,7 +254,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     RunsW16<KQ, BIO> runs;
     load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
     StageW16<IO> st;
-    load_stage_w16<IO>(st, p, dt_h, x_h, c_begin, lane, w4, pw);
+    load_stage_w16<IO>(st, p, rec_h, x_h, c_begin, lane, w4, pw);
 
     // The segment's start state, after the first chunk's loads are issued so
     // that their latency overlaps the prologue's tile loads.
@@ -277,7 +283,9 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             // The last segment's workgroup takes one more step and stores s1.
             // State index n = 16 nb + 4 q + r of channel p0 + pp; tile
             // padding (pp >= pw, n >= d_state) starts from zero, as in Pass B.
-            const int src = p.has_ids ? b.ids[seq] : seq;
+            // ids and the segment log-decays come through the scalar unit, so
+            // using them does not wait for the first chunk's vector loads.
+            const int src = p.has_ids ? sload_i32(b.ids, seq) : seq;
             const long long hs = (long long)h * p.s_s[0];
             const unsigned sbytes = (unsigned)(((long long)(P - 1) * p.s_s[1] + N) * 4);
             const int soff = (int)((p0 + pp) * p.s_s[1]) * 4;
@@ -301,7 +309,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 for (int k = 0; k < BLK; ++k) {
                     const int s = min(sb + k, nd - 1);
                     load_tile(s, T[k]);
-                    a[k] = expf(sd[(long long)s * p.n_head]);
+                    a[k] = expf(sload_f32(sd, (long long)s * p.n_head));
                 }
 #pragma unroll
                 for (int k = 0; k < BLK; ++k) {
@@ -381,20 +389,19 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos + 8]) = c_hi;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    sBt[(8 * u + e) * RSJ + j] = b_lo[e];
-                    sBt[(8 * u + 4 + e) * RSJ + j] = b_hi[e];
+                    sBt[bt_off(8 * u + e, j)] = b_lo[e];
+                    sBt[bt_off(8 * u + 4 + e, j)] = b_hi[e];
                 }
             }
         }
         load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, cn, N, jrow, qq);
 
-        // ---- decay preamble, dtX^T and dtXs^T ------------------------------
-        // The prefix is summed in fp64; the decays that only feed bf16
-        // operands are formed in fp32 from Lcum log2(e).
-        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
-        const double lcum = wave_incl_sum((double)A_h * (double)dtv);
-        const double lend = __shfl(lcum, 63, 64);
-        const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
+        // ---- decay record, dtX^T and dtXs^T --------------------------------
+        // Pass A's record of token lane: dt (0 past tlen), exp(L_end - Lcum)
+        // (0 past tlen), Lcum log2(e), exp(Lcum); exp(L_end) is token 63's.
+        const float dtv = as_f32(st.rec[0]);
+        const float sdec = as_f32(st.rec[1]);
+        const float a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[3], 63));
         {
             // dt and the decay of this wave's 16 tokens, through the wave's own
             // LDS row (one write, four broadcast reads each).
@@ -416,10 +423,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             store16_nat(&sXst[hw][lane * RSJ + 16 * w4], vs);
         }
         if (w4 == 0) {
-            sL2[hw][lane] = (float)(lcum * 1.4426950408889634074);
-            sE[hw][lane] = expf((float)lcum);
+            sL2[hw][lane] = as_f32(st.rec[2]);
+            sE[hw][lane] = as_f32(st.rec[3]);
         }
-        load_stage_w16<IO>(st, p, dt_h, x_h, cn, lane, w4, pw);
+        load_stage_w16<IO>(st, p, rec_h, x_h, cn, lane, w4, pw);
         __syncthreads();
 
         // ---- G1: this wave's blocks of M^T = (B C^T) . decay, into M[t][j] --
@@ -485,7 +492,6 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         }
         // ---- G4: R <- exp(L_end) R + B^T . dtXs (after G3 has used R) -------
         {
-            const float a_c = expf((float)lend);
             bf16x8 xs[2];
 #pragma unroll
             for (int s = 0; s < 2; ++s) xs[s] = *reinterpret_cast<const bf16x8*>(&sXst[hw][pp * RSJ + 32 * s + 8 * q]);
@@ -494,7 +500,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 f32x4 rn = R[nb] * a_c;
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
-                    rn = mfma16(*reinterpret_cast<const bf16x8*>(&sBt[(16 * nb + c16) * RSJ + 32 * s + 8 * q]), xs[s], rn);
+                    rn = mfma16(*reinterpret_cast<const bf16x8*>(&sBt[bt_off(16 * nb + c16, 32 * s + 8 * q)]), xs[s], rn);
                 R[nb] = rn;
             }
         }

@@ -151,6 +151,7 @@ struct TraitSets {
                 w16[x6][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[x6][k].walk_hpw = HELIX_WALK16_HPW(64 << k);
                 w16[x6][k].walk_fuse_b = true;
+                w16[x6][k].walk_rec = true;
             }
         for (int k = 0; k < 3; ++k) {
             w16bc[k] = w16[1][k];
@@ -245,6 +246,7 @@ struct IoTraitSets {
                 w16[i][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[i][k].walk_hpw = HELIX_WALK16_HPW(nps[k]);
                 w16[i][k].walk_fuse_b = true;
+                w16[i][k].walk_rec = true;
                 ka3[i][k] = std::string("helix_chunk_state_x3agg_") + io[i] + "io_n" + np;
                 names3[i][k] = std::string("mfma bf16 pass C, chunk walk, pass A bf16x3, ") + io[i] +
                                " storage (d_state<=" + np + ")";
@@ -364,10 +366,19 @@ const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d)
     return pick_traits(0, k, d);
 }
 
+// The walk's prologue loads up to segs_per_group segment aggregates per
+// workgroup, four at a time; past four segments the second round of loads
+// costs more than Pass B's own launch (config 2, 8 segments: 149 vs 142 us;
+// configs 4a/4b, 4 segments: 701 vs 712 and 767 vs 782 us).
+constexpr int kFuseBMaxSegs = 4;
+
 bool fuse_b_on(const HelixMatmulTraits& tr, const MultipassPlan& plan) {
-    const char* v = std::getenv("HELIX_FUSE_B");
-    if (v && v[0] == '0') return false;
-    return tr.walk_fuse_b && plan.n_groups == 1;
+    if (!tr.walk_fuse_b || plan.n_groups != 1) return false;
+    if (const char* v = std::getenv("HELIX_FUSE_B")) {
+        if (v[0] == '0') return false;
+        if (v[0] == '1') return true;
+    }
+    return plan.segs_per_group <= kFuseBMaxSegs;
 }
 
 size_t scratch_budget_bytes() {
@@ -409,7 +420,7 @@ bool prefer_walk(const helix_scan_desc& d) {
     return d.d_state <= 128 || (walk16_on() && bccopy_on(d));
 }
 
-void layout(const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, int np, int cpg,
+void layout(const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, bool rec, int np, int cpg,
             MultipassPlan* pl) {
     // State scratch is stored as padded slab tiles of 64 x np (helix_params.h).
     const size_t n_pslab = (size_t)(d.head_dim + HELIX_HD - 1) / HELIX_HD;
@@ -430,6 +441,8 @@ void layout(const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, i
     pl->off_sd = off; off += align256(pl->sd_elems * sizeof(float));
     pl->off_bc = off; off += align256(pl->bc_elems * 2);
     pl->off_cc = off; off += align256(pl->bc_elems * 2);
+    pl->rec_elems = rec ? (size_t)d.n_seq * (size_t)cpg * d.n_head * HELIX_CS * 4 : 0;
+    pl->off_rec = off; off += align256(pl->rec_elems * sizeof(float));
     pl->total_bytes = off;
 }
 
@@ -449,11 +462,12 @@ MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& 
     // A walking Pass C keeps no per-chunk state; only segment aggregates
     // (about one state per seg_len chunks) count against the budget.
     const size_t bc_chunk = tr.bccopy ? (size_t)d.n_seq * HELIX_CS * d.n_group * d.d_state * 2 * 2 : 0;
-    const size_t per_chunk = (tr.walk ? state : state * (bf16_state ? 2 : 4)) + bc_chunk;
+    const size_t rec_chunk = tr.walk_rec ? (size_t)d.n_seq * d.n_head * HELIX_CS * 16 : 0;
+    const size_t per_chunk = (tr.walk ? state : state * (bf16_state ? 2 : 4)) + bc_chunk + rec_chunk;
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(d, bf16_state, tr.walk, tr.bccopy, tr.np, (int)cpg, &pl);
+        layout(d, bf16_state, tr.walk, tr.bccopy, tr.walk_rec, tr.np, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }

@@ -191,6 +191,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     bufs.segld   = reinterpret_cast<float*>(sc + plan.off_sd);
     bufs.bcopy   = plan.bc_elems ? sc + plan.off_bc : nullptr;
     bufs.ccopy   = plan.bc_elems ? sc + plan.off_cc : nullptr;
+    bufs.pre     = plan.rec_elems ? reinterpret_cast<float*>(sc + plan.off_rec) : nullptr;
 
     // Debug-only per-pass timing split (reference dispatch.mm:207-216):
     // HELIX_ONLY_PASS=A|B|C enqueues just that pass; the output is then

@@ -53,6 +53,9 @@ struct HelixMatmulTraits {
     // (HelixScanParams::fuse_b); the encoder then skips Pass B's launch
     // whenever the plan has a single group.
     bool          walk_fuse_b;
+    // Pass A stores per-token decay records (HelixScanBuffers::pre) that the
+    // walking Pass C reads instead of recomputing its decay preamble.
+    bool          walk_rec;
 };
 
 namespace helix::rt {
@@ -84,14 +87,16 @@ struct MultipassPlan {
     size_t ld_elems         = 0;
     size_t sd_elems         = 0;
     size_t bc_elems         = 0;   // elements of each bf16 copy of B and C (0: none)
-    size_t off_sl = 0, off_sg = 0, off_ld = 0, off_sd = 0, off_bc = 0, off_cc = 0;
+    size_t rec_elems        = 0;   // fp32 elements of the decay records (0: none)
+    size_t off_sl = 0, off_sg = 0, off_ld = 0, off_sd = 0, off_bc = 0, off_cc = 0, off_rec = 0;
     size_t total_bytes      = 0;
 };
 
 MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& tr);
 
 // Whether the walking Pass C runs Pass B's segment scan itself (no Pass B
-// launch): a single-group plan on a kernel that can, unless HELIX_FUSE_B=0.
+// launch): a single-group plan of at most four segments on a kernel that can;
+// HELIX_FUSE_B=0 / 1 turns it off / on for any single-group plan.
 bool fuse_b_on(const HelixMatmulTraits& tr, const MultipassPlan& plan);
 
 // Scratch budget in bytes: $HELIX_SCRATCH_MB or the default.

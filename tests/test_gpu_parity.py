@@ -73,9 +73,12 @@ MODES = [
     ("bf16walk", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk"}, True),
     ("bf16walk/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_BF16_PASSC": "walk"}, True),
-    # The walk with Pass B launched on its own (by default the walk runs Pass
-    # B's segment scan in its prologue when the plan has one group).
+    # The walk with Pass B launched on its own, and with Pass B's segment scan
+    # run in the walk's prologue (by default: single-group plans of at most
+    # four segments).
     ("bf16walk/passB/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "0"},
+     True),
+    ("bf16walk/fuseB/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "1"},
      True),
     # The walk with Pass A on six split products: s1 at the fp32 bound.
     ("bf16walk/x6", HELIX_BACKEND_MPP, None, "short", {"HELIX_BF16_PASSC": "walk", "HELIX_PASSA_SPLIT": "6"},

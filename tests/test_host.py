@@ -193,7 +193,7 @@ def test_16bit_storage_selection(host, io, name):
     assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x3, {name} storage (d_state<=128)"
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_x3agg_{name}io_n128".encode(), None,
+        f"helix_chunk_state_x3agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
     with env(HELIX_PASSA_SPLIT="6"):       # Pass A on six split products
         assert host.plan_info(d).kernel_a == f"helix_chunk_state_x6agg_{name}io_n128".encode()
@@ -265,10 +265,17 @@ def test_backend_selection(host):
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     # Pass A writes bf16 copies of B and C that the walking Pass C reads.
-    # Pass B runs in the walk's prologue (single group): no kernel of its own.
+    # Config 2 plans eight segments: Pass B keeps its own launch; HELIX_FUSE_B=1
+    # runs it in the walk's prologue instead.
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x3agg_bc_n128", None, b"helix_scan_walk16_bf16_bc_n128")
-    assert k.launches == 2
+        b"helix_chunk_state_x3agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+    assert k.segs_per_group == 8 and k.launches == 3
+    with env(HELIX_FUSE_B="1"):
+        kf = host.plan_info(mp(shape))
+        assert kf.kernel_b is None and kf.launches == 2
+    # Config 4a: one group of four segments per sequence, fused by default.
+    k4 = host.plan_info(mp(CONFIG_SHAPES["cfg4a"]))
+    assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2
     with env(HELIX_SCRATCH_MB="1"):        # many groups: Pass B carries them through s1
         km = host.plan_info(mp(shape))
         assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
@@ -394,8 +401,8 @@ def _plan_invariants(host, name, backend):
     assert info.total_bytes % 256 == 0
     assert info.total_bytes >= want_sl + info.s_seg_bytes
     # The 16 x 16 walk runs Pass B's segment scan in its prologue when the plan
-    # has one group: no Pass B launch.
-    fused = b"walk16" in info.kernel_c and info.n_groups == 1
+    # has one group of at most four segments: no Pass B launch.
+    fused = b"walk16" in info.kernel_c and info.n_groups == 1 and info.segs_per_group <= 4
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
 
