@@ -535,4 +535,17 @@ HELIX_DEV void store_decay_record(const HelixScanParams& p, const HelixScanBuffe
     __builtin_amdgcn_raw_buffer_store_b128(w, r, lane * 16, 0, 0);
 }
 
+// The fp32 path's form of the record (its Pass C forms the intra-chunk decays
+// from fp64 differences of Lcum): {dt_t, exp(Lcum_t), Lcum_t as fp64}.
+HELIX_DEV void store_decay_record64(const HelixScanParams& p, const HelixScanBuffers& b, int seq, int c, int h,
+                                    int lane, float dtv, double lcum) {
+    const float e = expf((float)lcum);
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, lcum);
+    const float* rec = b.pre + (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 4);
+    const helix_rsrc r = make_rsrc(rec, HELIX_CS * 16u);
+    const u32x4 w = {__builtin_bit_cast(unsigned, dtv), __builtin_bit_cast(unsigned, e), (unsigned)u,
+                     (unsigned)(u >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, lane * 16, 0, 0);
+}
+
 #endif  // HELIX_COMMON_H

@@ -133,8 +133,10 @@ typedef struct HelixScanBuffers {
     void*        bcopy;   /* bf16 copies of B and C (see the layout above), or null */
     void*        ccopy;
     float*       pre;     /* per-token decay records [seq][chunk][head][64][4] that
-                             Pass A writes for the 16 x 16 walk, or null:
-                             {dt, exp(L_end - Lcum), Lcum log2(e), exp(Lcum)} */
+                             Pass A writes for the Pass C that reads them, or
+                             null: {dt, exp(L_end - Lcum), Lcum log2(e), exp(Lcum)}
+                             for the 16 x 16 walk, {dt, exp(Lcum), Lcum (fp64)}
+                             for the fp32 path's bf16x6 Pass C */
 } HelixScanBuffers;
 
 #endif /* HELIX_PARAMS_H */

@@ -255,6 +255,8 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         const float cf = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
         if (MODE == 2 && b.pre && wave == 0 && slab == 0)
             store_decay_record(p, b, seq, c, h, lane, tlen, dtv, lcum, lend);
+        if (MODE == 0 && b.pre && wave == 0 && slab == 0)
+            store_decay_record64(p, b, seq, c, h, lane, dtv, lcum);
 
         // dtXs^T[p][j] = exp(L_end - Lcum_j) dt_j x[j][p], row p = lane, and
         // B^T[n][j] (rows below). No masks: tokens past tlen have

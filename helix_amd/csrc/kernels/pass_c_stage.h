@@ -12,18 +12,20 @@
 // tile (pt, nt) = (m / NT, m % NT), i.e. rows p = pt*32 + lo and state
 // indices n = nt*32 + 8w + 4hi + 0..3. The units stay in their loaded form
 // until staged, so none of these loads has a consumer before then.
-template <int NP, typename SL>
+// REC: the item's decay record (store_decay_record64) replaces dt and A.
+template <int NP, typename SL, bool REC = false>
 struct StageC {
     float A;
     float dtraw;
+    u32x4 rec;
     float ld;
     float x[16];
     u32x4 sg[NP / 16];
     typename RawUnit<SL>::type sl[NP / 16];   // R_c; 0 for a segment's first chunk
 };
 
-template <int NP, typename SL>
-__device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScanParams& p,
+template <int NP, typename SL, bool REC = false>
+__device__ __forceinline__ void load_stage_c(StageC<NP, SL, REC>& st, const HelixScanParams& p,
                                              const HelixScanBuffers& b, const float* __restrict__ x_s,
                                              const float* __restrict__ dt_s, const SL* __restrict__ sl_s,
                                              const float* __restrict__ sg_s, int seq, int cg, int t0,
@@ -31,7 +33,7 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
     const int P = p.head_dim;
     const int p0 = slab * HELIX_HD;
     const int pw = min(HELIX_HD, P - p0);
-    st.A = b.A[(long long)h * p.s_a];
+    if constexpr (!REC) st.A = b.A[(long long)h * p.s_a];
     st.ld = b.ld[seq * p.ld_seq + (long long)cg * p.n_head + h];
     // dt and x of this head and chunk through buffer resources based at the
     // chunk's first token (the host keeps a chunk's extent below 2 GiB).
@@ -40,7 +42,13 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL>& st, const HelixScan
                                      ((tlen - 1) * sdt + 1) * 4u);
     const helix_rsrc rx = make_rsrc(x_s + h * p.s_x[1] + (long long)t0 * p.s_x[0] + (long long)p0 * p.s_x[2],
                                     ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
-    st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    if constexpr (REC) {
+        const helix_rsrc rr = make_rsrc(b.pre + (((long long)seq * p.cpg + cg) * p.n_head + h) * (HELIX_CS * 4),
+                                        HELIX_CS * 16u);
+        st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    } else {
+        st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
+    }
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {

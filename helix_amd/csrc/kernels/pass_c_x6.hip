@@ -139,8 +139,9 @@ __device__ __forceinline__ void chunk_out_x6_impl(const HelixScanParams& p, cons
     const float* __restrict__ sg_s = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg;
 
     const int n_items = (h_end - h_begin) * p.n_pslab;
-    StageC<NP, float> st;
-    load_stage_c<NP, float>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, h_begin, 0, lane, wave);
+    // Pass A's decay records replace the per-item softplus and fp64 scan.
+    StageC<NP, float, true> st;
+    load_stage_c<NP, float, true>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, h_begin, 0, lane, wave);
 
     for (int item = 0; item < n_items; ++item) {
         const int h    = h_begin + item / p.n_pslab;
@@ -148,11 +149,13 @@ __device__ __forceinline__ void chunk_out_x6_impl(const HelixScanParams& p, cons
         const int p0 = slab * HELIX_HD;
         const int pw = min(HELIX_HD, P - p0);
 
-        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
-        const double lcum = wave_incl_sum((double)st.A * (double)dtv);
+        // Record of token lane: dt (0 past tlen), exp(Lcum), Lcum (fp64).
+        const float dtv = as_f32(st.rec[0]);
+        const double lcum = __builtin_bit_cast(double, (unsigned long long)st.rec[2] |
+                                                           ((unsigned long long)st.rec[3] << 32));
         const float es = expf(st.ld);
         sL[wave][lane] = lcum;                       // this wave's own copy
-        if (wave == 0) sE[lane] = expf((float)lcum);
+        if (wave == 0) sE[lane] = as_f32(st.rec[1]);
 
         // dtX^T[p][j], row p = lane, tokens 16 wave .. 16 wave + 15.
         {
@@ -213,7 +216,7 @@ __device__ __forceinline__ void chunk_out_x6_impl(const HelixScanParams& p, cons
         // The register stage is free: the next item's inputs travel during the GEMMs.
         if (item + 1 < n_items) {
             const int hn = h_begin + (item + 1) / p.n_pslab;
-            load_stage_c<NP, float>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, hn,
+            load_stage_c<NP, float, true>(st, p, b, x_s, dt_s, sl_s, sg_s, seq, cg, t0, tlen, cis, hn,
                                     (item + 1) % p.n_pslab, lane, wave);
         }
 

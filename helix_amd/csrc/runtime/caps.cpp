@@ -142,6 +142,7 @@ struct TraitSets {
                 if (x6c) {
                     v.k_chunk_out = kX6OutF32[k];
                     v.mfma_c = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
+                    v.rec_kind = 2;
                 }
             }
         for (int x6 = 0; x6 < 2; ++x6)
@@ -151,7 +152,7 @@ struct TraitSets {
                 w16[x6][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[x6][k].walk_hpw = HELIX_WALK16_HPW(64 << k);
                 w16[x6][k].walk_fuse_b = true;
-                w16[x6][k].walk_rec = true;
+                w16[x6][k].rec_kind = 1;
             }
         for (int k = 0; k < 3; ++k) {
             w16bc[k] = w16[1][k];
@@ -246,7 +247,7 @@ struct IoTraitSets {
                 w16[i][k].mfma_c = "v_mfma_f32_16x16x32_bf16";
                 w16[i][k].walk_hpw = HELIX_WALK16_HPW(nps[k]);
                 w16[i][k].walk_fuse_b = true;
-                w16[i][k].walk_rec = true;
+                w16[i][k].rec_kind = 1;
                 ka3[i][k] = std::string("helix_chunk_state_x3agg_") + io[i] + "io_n" + np;
                 names3[i][k] = std::string("mfma bf16 pass C, chunk walk, pass A bf16x3, ") + io[i] +
                                " storage (d_state<=" + np + ")";
@@ -462,12 +463,12 @@ MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& 
     // A walking Pass C keeps no per-chunk state; only segment aggregates
     // (about one state per seg_len chunks) count against the budget.
     const size_t bc_chunk = tr.bccopy ? (size_t)d.n_seq * HELIX_CS * d.n_group * d.d_state * 2 * 2 : 0;
-    const size_t rec_chunk = tr.walk_rec ? (size_t)d.n_seq * d.n_head * HELIX_CS * 16 : 0;
+    const size_t rec_chunk = tr.rec_kind ? (size_t)d.n_seq * d.n_head * HELIX_CS * 16 : 0;
     const size_t per_chunk = (tr.walk ? state : state * (bf16_state ? 2 : 4)) + bc_chunk + rec_chunk;
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(d, bf16_state, tr.walk, tr.bccopy, tr.walk_rec, tr.np, (int)cpg, &pl);
+        layout(d, bf16_state, tr.walk, tr.bccopy, tr.rec_kind != 0, tr.np, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }

@@ -53,9 +53,11 @@ struct HelixMatmulTraits {
     // (HelixScanParams::fuse_b); the encoder then skips Pass B's launch
     // whenever the plan has a single group.
     bool          walk_fuse_b;
-    // Pass A stores per-token decay records (HelixScanBuffers::pre) that the
-    // walking Pass C reads instead of recomputing its decay preamble.
-    bool          walk_rec;
+    // Pass A stores per-token decay records (HelixScanBuffers::pre) that Pass
+    // C reads instead of recomputing its decay preamble: 0 none, 1 the
+    // walk's form (store_decay_record), 2 the fp64 form of the fp32 path's
+    // bf16x6 Pass C (store_decay_record64).
+    int           rec_kind;
 };
 
 namespace helix::rt {
