@@ -142,13 +142,15 @@ def time_passes(v: Variant, steps: int, stream):
     """Per-pass event times (ms): each step encodes Pass A, B and C as three
     single-pass encodes in a row (HELIX_ONLY_PASS), each between two events
     on the launch stream, so every pass runs in the same order, and on the
-    same cache state, as inside a whole scan."""
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in "ABC"]
+    same cache state, as inside a whole scan. A fourth, empty encode
+    (HELIX_ONLY_PASS=X launches nothing) between two events measures what
+    the event pair itself adds ('X'); pass_us() subtracts it."""
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in "ABCX"]
            for _ in range(steps)]
     try:
         torch.cuda.synchronize()
         for step in evs:
-            for k, (a, b) in zip("ABC", step):
+            for k, (a, b) in zip("ABCX", step):
                 os.environ["HELIX_ONLY_PASS"] = k
                 a.record(stream)
                 v.encode(stream)
@@ -156,7 +158,14 @@ def time_passes(v: Variant, steps: int, stream):
         torch.cuda.synchronize()
     finally:
         os.environ.pop("HELIX_ONLY_PASS", None)
-    return {k: [step[i][0].elapsed_time(step[i][1]) for step in evs] for i, k in enumerate("ABC")}
+    return {k: [step[i][0].elapsed_time(step[i][1]) for step in evs] for i, k in enumerate("ABCX")}
+
+
+def pass_us(passes, stat="median"):
+    """Per-pass kernel time (us): the pass's event-bracketed time less that
+    of an empty encode between the same two events."""
+    x = dist(passes["X"])[stat]
+    return {k: max(0.0, dist(ts)[stat] - x) * 1e3 for k, ts in passes.items() if k != "X"}
 
 
 def pass_algorithmic_bytes(plan):
@@ -171,12 +180,14 @@ def pass_algorithmic_bytes(plan):
     # and Pass C reads the copies instead.
     cp = plan.bccopy_bytes
     # With Pass B run by the walking Pass C (no kernel_b), Pass C also reads s0
-    # and writes s1; the segment aggregates are read once either way.
+    # and writes s1; the segment aggregates are read once either way. Pass A
+    # writes the per-token decay records, which Pass C reads instead of dt.
     fused = not plan.kernel_b
+    rec = plan.rec_bytes
     return {
-        "A": x + dt + bc + plan.s_local_bytes + plan.s_seg_bytes + ((bc + cp) if cp else 0),
+        "A": x + dt + bc + plan.s_local_bytes + plan.s_seg_bytes + ((bc + cp) if cp else 0) + rec,
         "B": 0 if fused else 2 * plan.s_seg_bytes + 2 * state,
-        "C": x + dt + (cp if cp else 2 * bc) + plan.s_local_bytes + plan.s_seg_bytes + y
+        "C": x + (rec if rec else dt) + (cp if cp else 2 * bc) + plan.s_local_bytes + plan.s_seg_bytes + y
              + (2 * state if fused else 0),
     }
 
@@ -279,8 +290,7 @@ def config_report(ctx, stream, dev, steps: int, warm_ms: float):
                 "shape": f"S={S} L={L} H={H} P={P} N={N} G={G}",
                 "tok_s": S * L / (ms * 1e-3), "gflops": F / (ms * 1e-3) / 1e9, "ms": ms,
                 "roofline_frac": t_roof / (ms * 1e-3), "t_roof_us": t_roof * 1e6,
-                "passes_us": {k: dist(ts)["median"] * 1e3 for k, ts in passes.items()
-                              if k != "B" or v.plan.kernel_b},
+                "passes_us": {k: us for k, us in pass_us(passes).items() if k != "B" or v.plan.kernel_b},
                 "plan": {"groups": v.plan.n_groups, "seg_len": v.plan.seg_len},
             }
             del v
@@ -359,8 +369,7 @@ def main():
         torch.cuda.synchronize()
         wall = (time.perf_counter() - w0) / args.steps * 1e3
         # Per-pass split (HELIX_ONLY_PASS) exists only for the multipass path.
-        passes = ({k: dist(ts_k) for k, ts_k in time_passes(v, args.steps, stream).items()}
-                  if v.multipass else None)
+        passes = time_passes(v, args.steps, stream) if v.multipass else None
         d = dist(ts)
         ms = statistics.fmean(ts)
         peak_c = PEAK_BF16_MFMA if v.name == "bf16" else PEAK_FP32_MFMA
@@ -373,24 +382,25 @@ def main():
     # work; Pass A: ~0.32 GB against ~20 us of bf16x6 MFMA work), so each is
     # priced on its algorithmic bytes: what it must read and write once.
     r = results["bf16"]
-    pa = r["passes"]
+    pa = pass_us(r["passes"])                   # median kernel time per pass, us
+    pmean = pass_us(r["passes"], "mean")        # mean, as rocprofv3 --stats averages
     plan = r["plan"]
     pass_bytes = pass_algorithmic_bytes(plan)
     # Pass B has no kernel of its own when the walking Pass C runs its scan
     # (plan.kernel_b is null): its bytes and time are then Pass C's.
     kernels = {"A": plan.kernel_a, "B": plan.kernel_b, "C": plan.kernel_c}
     live = [k for k in "ABC" if kernels[k]]
-    dom = max(live, key=lambda k: pa[k]["median"])
+    dom = max(live, key=lambda k: pa[k])
     kname = kernels[dom].decode()
-    t = pa[dom]["mean"] * 1e-3     # average launch duration, as rocprofv3 --stats reports it
+    t = pmean[dom] * 1e-6          # average launch duration, as rocprofv3 --stats reports it
     roof = {"kernel": f"{kname} (Pass {dom})", "bound": "hbm",
             "achieved": pass_bytes[dom] / t / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
             "algorithmic_bytes": pass_bytes[dom]}
     roof["frac"] = roof["achieved"] / roof["peak"]
     roof["traffic"] = profiled_traffic(kname)
     passes_roof = {k: {"kernel": kernels[k].decode(),
-                       "us": pa[k]["median"] * 1e3, "algorithmic_bytes": pass_bytes[k],
-                       "hbm_frac": pass_bytes[k] / (pa[k]["median"] * 1e-3) / PEAK_HBM} for k in live}
+                       "us": pa[k], "algorithmic_bytes": pass_bytes[k],
+                       "hbm_frac": pass_bytes[k] / (pa[k] * 1e-6) / PEAK_HBM} for k in live}
 
     ms = r["ms"]
     value = S * L / (ms * 1e-3)
@@ -423,13 +433,16 @@ def main():
         "roofline": roof,
         "passes_roofline": passes_roof,
         "timing_ms": {k: round(vv, 5) for k, vv in r["d"].items()},
-        "passes_ms_median": {k: pa[k]["median"] for k in live},
+        # Per-pass kernel times: event-bracketed single-pass encodes less an
+        # empty encode between the same events (event_pair_us).
+        "passes_us": {k: pa[k] for k in live},
+        "event_pair_us": dist(r["passes"]["X"])["median"] * 1e3,
         "fp32_path": {
             "tok_s": S * L / (results["fp32"]["ms"] * 1e-3),
             "gflops": F / (results["fp32"]["ms"] * 1e-3) / 1e9,
             "ms_per_step": results["fp32"]["ms"],
             "roofline_frac": results["fp32"]["t_roof"] / (results["fp32"]["ms"] * 1e-3),
-            "passes_ms_median": {k: results["fp32"]["passes"][k]["median"] for k in "ABC"},
+            "passes_us": pass_us(results["fp32"]["passes"]),
             "kernel": results["fp32"]["kernel"],
         },
     }
@@ -440,7 +453,7 @@ def main():
             rv = results[v.name]
             e = {"ms_per_step": rv["ms"], "kernel": rv["kernel"]}
             if rv["passes"]:
-                e["passes_ms_median"] = {k: rv["passes"][k]["median"] for k in "ABC"}
+                e["passes_us"] = pass_us(rv["passes"])
             out["variants"][v.name] = e
     if args.config_steps > 0:
         out["configs"] = config_report(ctx, stream, dev, args.config_steps,

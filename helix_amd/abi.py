@@ -49,6 +49,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("kernel_c", ctypes.c_char_p),
         ("kernel_1pass", ctypes.c_char_p),
         ("bccopy_bytes", c_uint64),
+        ("rec_bytes", c_uint64),
     ]
 
 

@@ -321,6 +321,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
     out->s_seg_bytes = pl.sg_elems * sizeof(float);
     out->bccopy_bytes = pl.bc_elems * 2 * 2;
+    out->rec_bytes = pl.rec_elems * sizeof(float);
     const bool fuse_b = helix::rt::fuse_b_on(tr, pl);   // as helix_scan_encode decides
     out->launches = fuse_b ? 2 : 3 * pl.n_groups;
     out->np = tr.np;

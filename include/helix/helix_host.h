@@ -41,6 +41,7 @@ typedef struct {
     const char* kernel_c;
     const char* kernel_1pass;   /* the single-pass kernel, else NULL             */
     uint64_t bccopy_bytes;      /* bf16 copies of B and C Pass A writes for C    */
+    uint64_t rec_bytes;         /* per-token decay records Pass A writes for C   */
 } helix_plan_info;
 
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */

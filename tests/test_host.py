@@ -282,6 +282,15 @@ def test_backend_selection(host):
         assert km.launches == 3 * km.n_groups
     L, S, H, P, N, G = shape
     assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
+    # Pass A writes one 16-byte decay record per (seq, chunk, head, token) for
+    # the walk and for the fp32 path's bf16x6 Pass C; no other Pass C reads one.
+    recs = S * (-(-L // 64)) * H * 64 * 16
+    assert k.rec_bytes == recs
+    assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == recs
+    with env(HELIX_X6="0"):
+        assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == 0
+    with env(HELIX_BF16_PASSC="tile"):
+        assert host.plan_info(mp(shape)).rec_bytes == 0
     assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
     with env(HELIX_WALK_BCCOPY="0"):
         k0 = host.plan_info(mp(shape))
