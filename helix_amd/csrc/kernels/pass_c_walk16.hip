@@ -301,7 +301,9 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
             const bool last = seg == p.n_seg - 1;
             const int nd = seg + (last ? 1 : 0);
-            constexpr int BLK = 4;          // tiles in flight
+            // Tiles in flight: four up to d_state 128, two at 256 (32 f32x4
+            // registers either way; four tiles of 16 spill at d_state 256).
+            constexpr int BLK = NB <= 8 ? 4 : 2;
             for (int sb = 0; sb < nd; sb += BLK) {
                 f32x4 T[BLK][NB];
                 float a[BLK];
@@ -429,13 +431,16 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         load_stage_w16<IO>(st, p, rec_h, x_h, cn, lane, w4, pw);
         __syncthreads();
 
-        // ---- G1: this wave's blocks of M^T = (B C^T) . decay, into M[t][j] --
-        // Block idx = w4 + 4 i: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
+        // ---- G1: C B^T once for the workgroup's heads (they share B and C);
+        // wave w takes blocks idx = w + NW i and writes every head's M^T =
+        // (B C^T) . decay block from its registers into that head's M[t][j].
+        // Block idx: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
         {
-            f32x4 d[3];
+            constexpr int NBLK = (10 + NW - 1) / NW;
+            f32x4 d[NBLK];
 #pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int idx = w4 + 4 * i;
+            for (int i = 0; i < NBLK; ++i) {
+                const int idx = wave + NW * i;
                 if (idx >= 10) break;
                 const int tb = g1_tb(idx), jb = g1_jb(idx);
                 const __bf16* arow = &sB[(16 * jb + c16) * RS + 8 * q];
@@ -451,19 +456,22 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 *reinterpret_cast<unsigned*>(&sMh[zoff]) = 0u;
             }
 #pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int idx = w4 + 4 * i;
+            for (int i = 0; i < NBLK; ++i) {
+                const int idx = wave + NW * i;
                 if (idx >= 10) break;
                 const int tb = g1_tb(idx), jb = g1_jb(idx);
                 const int t = 16 * tb + c16;
                 const int j0 = 16 * jb + 4 * q;
-                const float l_t = sL2[hw][t];
-                const f32x4 lj = *reinterpret_cast<const f32x4*>(&sL2[hw][j0]);
-                bf16x4 m;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    m[r] = to_bf16(keep_if_le(d[i][r] * __builtin_amdgcn_exp2f(l_t - lj[r]), j0 + r, t));
-                *reinterpret_cast<bf16x4*>(&sMh[t * RSJ + j0]) = m;
+                for (int hh = 0; hh < HPW; ++hh) {
+                    const float l_t = sL2[hh][t];
+                    const f32x4 lj = *reinterpret_cast<const f32x4*>(&sL2[hh][j0]);
+                    bf16x4 m;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        m[r] = to_bf16(keep_if_le(d[i][r] * __builtin_amdgcn_exp2f(l_t - lj[r]), j0 + r, t));
+                    *reinterpret_cast<bf16x4*>(&sM[hh * (HELIX_CS * RSJ) + t * RSJ + j0]) = m;
+                }
             }
         }
 
