@@ -40,6 +40,7 @@ PEAK_BF16_MFMA = 2516.6e12  # FLOP/s (dense)
 REF_TOKS = 1315051.0
 
 CFG = dict(L=8192, S=1, H=64, P=64, N=128, G=8)
+ARENA_BYTES = 4 << 30   # the headline workload's inputs, outputs and scratch fit
 
 # BASELINE.json's configurations (config 4 in its two head-dim variants): shape,
 # the paths each is quoted on, and the distributions that differ from the common
@@ -325,6 +326,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     ctx = Context(0)
+    # One device allocation for the whole workload, as a serving runtime's
+    # arena: torch's caching allocator keeps this block and carves the
+    # inputs, outputs and scratch out of it. Separate allocations made the
+    # first variant's scan up to 7 us slower than an identical later one
+    # (where x and the scratch land decides what stays in the Infinity Cache
+    # between Pass A and Pass C); inside one block the two agree to ~1.5 us.
+    _arena = torch.empty(ARENA_BYTES, dtype=torch.uint8, device=dev)
+    del _arena
     tensors = make_inputs(1002, dev)
     stream = torch.cuda.current_stream(dev)
     variants = [Variant("bf16", ctx, HELIX_BACKEND_MPP, tensors),
