@@ -242,21 +242,31 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
     for (int i = 0; i < NTW; ++i) acc[i] = zero16();
     float lam = 0.0f;  // log-decay accumulated over this segment before chunk c
 
-    // Two register stages in turn: the loads of chunk c+2 are issued while
-    // chunks c and c+1 are processed (a copy between stages would wait on them).
-    auto step = [&](StageX6<NP, IO>& st, CopyBC& cp, int c) {
+    // Decay preamble of chunk c (lane = token; dtv = 0 past tlen), formed by
+    // one wave per chunk: wave (c - c_begin) % 4, one chunk ahead, while its
+    // MFMAs for the previous chunk run. It leaves cf_j = exp(L_end - Lcum_j)
+    // dt_j for the 64 tokens and (float)L_end in sPre[(c - c_begin) % 2],
+    // and stores the chunk's decay record for Pass C.
+    __shared__ __attribute__((aligned(16))) float sPre[2][HELIX_CS + 4];
+    auto preamble = [&](float dtraw, int c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
-
-        // Decay preamble (lane = token; dtv = 0 past tlen).
-        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+        const float dtv = keep_if_lt(helix_dt(p, dtraw), lane, tlen);
         const double lcum = wave_incl_sum((double)A_h * (double)dtv);
         const double lend = __shfl(lcum, 63, 64);
-        const float cf = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
-        if (MODE == 2 && b.pre && wave == 0 && slab == 0)
-            store_decay_record(p, b, seq, c, h, lane, tlen, dtv, lcum, lend);
-        if (MODE == 0 && b.pre && wave == 0 && slab == 0)
-            store_decay_record64(p, b, seq, c, h, lane, dtv, lcum);
+        float* dst = sPre[(c - c_begin) & 1];
+        dst[lane] = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
+        if (lane == 0) dst[HELIX_CS] = (float)lend;
+        if (MODE == 2 && b.pre && slab == 0) store_decay_record(p, b, seq, c, h, lane, tlen, dtv, lcum, lend);
+        if (MODE == 0 && b.pre && slab == 0) store_decay_record64(p, b, seq, c, h, lane, dtv, lcum);
+    };
+
+    // Two register stages in turn: the loads of chunk c+2 are issued while
+    // chunks c and c+1 are processed (a copy between stages would wait on them).
+    // next_dtraw is chunk c+1's dt, from the other stage.
+    auto step = [&](StageX6<NP, IO>& st, CopyBC& cp, int c, float next_dtraw) {
+        const int buf  = (c - c_begin) & 1;
+        const float lendf = sPre[buf][HELIX_CS];
 
         // dtXs^T[p][j] = exp(L_end - Lcum_j) dt_j x[j][p], row p = lane, and
         // B^T[n][j] (rows below). No masks: tokens past tlen have
@@ -266,7 +276,11 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         {
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = bcast(cf, 16 * wave + i) * io_widen<IO>(st.x[i]);
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4 cf4 = *reinterpret_cast<const f32x4*>(&sPre[buf][16 * wave + 4 * i4]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[4 * i4 + k] = cf4[k] * io_widen<IO>(st.x[4 * i4 + k]);
+            }
             stage_split_row<HELIX_HD, NS>(sXt, lane, 2 * wave, v);
         }
         // B^T rows NB lo + k, chunk 2 wave + hi (tokens 16 wave + 8 hi + e).
@@ -310,7 +324,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
             if constexpr (BCC) load_copy_bc(cp, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c + 2, N);
         }
 
-        const float a_c = expf((float)lend);
+        const float a_c = expf(lendf);
 #pragma unroll
         for (int i = 0; i < NTW; ++i) acc[i] *= a_c;
 
@@ -340,7 +354,10 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
                 acc[i] = mfma_bf16(bs[0], xs[0], acc[i]);
             }
         }
-        lam += (float)lend;
+        // The next chunk's preamble, by one wave, while this chunk's MFMAs run;
+        // the barrier below publishes it.
+        if (c + 1 < c_end && wave == ((c + 1 - c_begin) & 3)) preamble(next_dtraw, c + 1);
+        lam += lendf;
         __syncthreads();
     };
     StageX6<NP, IO> sa, sb;
@@ -351,9 +368,11 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
         if constexpr (BCC) load_copy_bc(cb, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c_begin + 1, N);
     }
+    if (wave == 0) preamble(sa.dtraw, c_begin);
+    __syncthreads();
     for (int c = c_begin; c < c_end; c += 2) {
-        step(sa, ca, c);
-        if (c + 1 < c_end) step(sb, cb, c + 1);
+        step(sa, ca, c, sb.dtraw);
+        if (c + 1 < c_end) step(sb, cb, c + 1, sa.dtraw);
     }
 
     const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
