@@ -40,6 +40,10 @@ PATHS = [
     ("bf16", HELIX_BACKEND_MPP, True, {}),
     ("bf16tile", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "tile"}),
     ("bf16walk", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk"}),
+    # Pass B's segment scan in the walk's prologue (ids and s0/s1 strides go
+    # through it), and in its own launch.
+    ("bf16walk/fuseB", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "1"}),
+    ("bf16walk/passB", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "0"}),
     ("1pass", HELIX_BACKEND_AUTO, False, {}),
 ]
 PATH_IDS = [p[0] for p in PATHS]
