@@ -28,7 +28,7 @@
 // n-contiguous operand (C and B rows in LDS), and R feeds G3 straight from
 // its registers.
 //
-// LDS (bf16, rows padded by 8): C[t][n], B[j][n] (perm32 order), B^T[n][j],
+// LDS (bf16, rows padded by 16): C[t][n], B[j][n] (perm32 order), B^T[n][j],
 // and per head dtX^T[p][j] (two buffers, by chunk parity), dtXs^T[p][j] and
 // M[t][j] (natural j order).
 #include "helix_common.h"
@@ -163,8 +163,13 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     constexpr int NB  = NP / 16;              // 16-row state tiles of R
     constexpr int KS  = NP / 32;              // K steps over the state
     constexpr int NT32 = NP / 32;             // 32 x 32 tiles of the slab tile layout
-    constexpr int RS  = NP + 8;               // bf16 row stride of C[t][n], B[j][n]
-    constexpr int RSJ = HELIX_CS + 8;         // bf16 row stride of B^T, dtX^T, dtXs^T, M
+    // Row strides (bf16) of C[t][n], B[j][n] and of B^T, dtX^T, dtXs^T, M. Every
+    // operand read takes 16 rows (lane % 16) x four 16-byte chunks (lane / 16);
+    // measured on gfx950 (SQ_LDS_BANK_CONFLICT), that is conflict-free when
+    // the row stride in dwords is 8 mod 16 and about 17% conflicted at the
+    // 4 mod 16 of an 8-element pad. Padding 16 elements gives NP/2 + 8 and 40.
+    constexpr int RS  = NP + 16;
+    constexpr int RSJ = HELIX_CS + 16;
     constexpr int NCH = NP / 8;               // 8-element runs per C / B row
     // B^T[n][j] sits at row n, 16-byte chunk (j / 8) ^ ((n / 16) % 8). The
     // staging writes are a transpose: one instruction writes column j of rows
