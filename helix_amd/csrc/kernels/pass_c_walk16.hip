@@ -77,28 +77,29 @@ __device__ __forceinline__ void load_stage_w16(StageW16<IO>& st, const HelixScan
     for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
 }
 
-// This lane's B and C runs of one chunk, as loaded: KQ runs of eight state
-// indices of row jrow, two 16-byte words each in fp32 storage, one in 16-bit.
+// This lane's B and C runs of one chunk, as loaded: the run of eight state
+// indices 8u .. 8u+7 of KQ rows jrow + RPI k, two 16-byte words each in fp32
+// storage, one in 16-bit.
 template <int KQ, typename IO>
 struct RunsW16 {
     static constexpr int WPR = sizeof(IO) == 4 ? 2 : 1;
     u32x4 b[KQ][WPR], c[KQ][WPR];
 };
 
-template <int KQ, int QPI, typename IO>
+template <int KQ, int RPI, typename IO>
 __device__ __forceinline__ void load_runs_w16(RunsW16<KQ, IO>& r, const HelixScanParams& p,
                                               const IO* __restrict__ B_g, const IO* __restrict__ C_g,
-                                              int c, int N, int jrow, int qq) {
+                                              int c, int N, int jrow, int u) {
     constexpr int ES = (int)sizeof(IO);
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
     const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
     const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * (unsigned)ES);
-    const int jr = min(jrow, tlen - 1);
+    const int n0 = min(8 * u, N - 8);   // d_state % 8 == 0: a run is all in or out
 #pragma unroll
     for (int k = 0; k < KQ; ++k) {
-        const int n0 = min(8 * (qq + QPI * k), N - 8);   // d_state % 8 == 0: a run is all in or out
+        const int jr = min(jrow + RPI * k, tlen - 1);
 #pragma unroll
         for (int w = 0; w < RunsW16<KQ, IO>::WPR; ++w) {
             r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * ES + 16 * w, 0, 0);
@@ -245,19 +246,23 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     if constexpr (!M_IN_B) *reinterpret_cast<unsigned*>(&sMh[zoff]) = 0u;
 
     // B and C are staged once for the workgroup's heads. All NW waves share
-    // the 64 rows, RPW each: lane (jj = lane % RPW, qq = lane / RPW) holds
-    // state indices 8u .. 8u+7, u = qq + (64/RPW) k, of row RPW wave + jj.
+    // the 64 rows, RPW each. An instruction covers RPI whole rows, NCH lanes
+    // per row: lane holds state indices 8u .. 8u+7, u = lane % NCH, of rows
+    // RPW wave + lane / NCH + RPI k. (With lanes spread over eight rows and
+    // eight runs instead, the 8-byte LDS writes measured 19 cycles each
+    // against 8; the global loads are whole rows too.)
     constexpr int RPW = HELIX_CS / NW;
-    constexpr int QPI = 64 / RPW;                 // runs per wave instruction
-    constexpr int KQ  = NCH / QPI;
-    const int jj = lane % RPW, qq = lane / RPW;
-    const int jrow = RPW * wave + jj;
+    constexpr int RPI = 64 / NCH;                 // rows per wave instruction
+    constexpr int KQ  = RPW / RPI;
+    static_assert(RPI * NCH == 64 && KQ * RPI == RPW, "whole rows per instruction");
+    const int ur = lane % NCH;
+    const int jrow = RPW * wave + lane / NCH;
 
     // Issued in the loop's order (runs, then x and dt): the counter state at
     // the loop head is then the same on entry as around the loop, and the
     // wait for the runs never covers the previous chunk's y stores.
     RunsW16<KQ, BIO> runs;
-    load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, c_begin, N, jrow, qq);
+    load_runs_w16<KQ, RPI, BIO>(runs, p, B_g, C_g, c_begin, N, jrow, ur);
     StageW16<IO> st;
     load_stage_w16<IO>(st, p, rec_h, x_h, c_begin, lane, w4, pw);
 
@@ -370,9 +375,9 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             constexpr bool RAW = __is_same(BIO, __bf16);
 #pragma unroll
             for (int k = 0; k < KQ; ++k) {
-                const int u = qq + QPI * k;
+                const int u = ur;
                 const int cpos = perm32(8 * u);           // elements 8u+4 .. 8u+7 sit 8 further
-                const int j = jrow;
+                const int j = jrow + RPI * k;
                 const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * u)) >> 31);
                 bf16x4 b_lo, b_hi, c_lo, c_hi;
                 if constexpr (RAW) {
@@ -401,7 +406,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 }
             }
         }
-        load_runs_w16<KQ, QPI, BIO>(runs, p, B_g, C_g, cn, N, jrow, qq);
+        load_runs_w16<KQ, RPI, BIO>(runs, p, B_g, C_g, cn, N, jrow, ur);
 
         // ---- decay record, dtX^T and dtXs^T --------------------------------
         // Pass A's record of token lane: dt (0 past tlen), exp(L_end - Lcum)
