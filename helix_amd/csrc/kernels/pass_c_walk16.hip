@@ -119,16 +119,29 @@ HELIX_DEV float run16_elem(const u32x4 (&w)[WPR], int e) {
     }
 }
 
-// Sixteen consecutive tokens' values of one row, in natural order.
-HELIX_DEV void store16_nat(__bf16* row, const float (&v)[16]) {
+// Element offset of column col of row `row` in a bf16 LDS buffer of row
+// stride RSX: the 16-byte chunk index is XOR-ed with (row / 4) % 8. Every
+// operand read takes 16 consecutive rows of one chunk per 16 lanes; with the
+// swizzle those take 4 cycles per 16-byte read instruction instead of 5.8 on
+// gfx950 (measured), and the 8- and 16-byte staging writes of M and dtX^T
+// 8 and 7.5 instead of 16 and 10. The chunk index stays in its group of 8.
+template <int RSX>
+HELIX_DEV int swz_off(int row, int col) {
+    return row * RSX + ((((col >> 3) ^ ((row >> 2) & 7))) << 3) + (col & 7);
+}
+
+// Sixteen consecutive tokens' values of one row, in natural order: columns
+// col0 .. col0 + 15 of row `row` (col0 a multiple of 8).
+template <int RSX>
+HELIX_DEV void store16_nat(__bf16* buf, int row, int col0, const float (&v)[16]) {
     bf16x8 a, b;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         a[e] = to_bf16(v[e]);
         b[e] = to_bf16(v[8 + e]);
     }
-    *reinterpret_cast<bf16x8*>(row) = a;
-    *reinterpret_cast<bf16x8*>(row + 8) = b;
+    *reinterpret_cast<bf16x8*>(&buf[swz_off<RSX>(row, col0)]) = a;
+    *reinterpret_cast<bf16x8*>(&buf[swz_off<RSX>(row, col0 + 8)]) = b;
 }
 
 // Store the wave's y tile of one chunk: acc[tb] register r holds
@@ -241,7 +254,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         const int row = e2 >> 4, col = e2 & 15;
         const int t = row < 16 ? row : row + 16;
         const int j = row < 16 ? 16 + col : 48 + col;
-        return t * RSJ + j;
+        return swz_off<RSJ>(t, j);
     }();
     if constexpr (!M_IN_B) *reinterpret_cast<unsigned*>(&sMh[zoff]) = 0u;
 
@@ -395,10 +408,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                         c_hi[e] = to_bf16(as_f32(as_u32(run16_elem<BIO, WPR>(runs.c[k], 4 + e)) & keep));
                     }
                 }
-                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos]) = b_lo;
-                *reinterpret_cast<bf16x4*>(&sB[j * RS + cpos + 8]) = b_hi;
-                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos]) = c_lo;
-                *reinterpret_cast<bf16x4*>(&sC[j * RS + cpos + 8]) = c_hi;
+                *reinterpret_cast<bf16x4*>(&sB[swz_off<RS>(j, cpos)]) = b_lo;
+                *reinterpret_cast<bf16x4*>(&sB[swz_off<RS>(j, cpos + 8)]) = b_hi;
+                *reinterpret_cast<bf16x4*>(&sC[swz_off<RS>(j, cpos)]) = c_lo;
+                *reinterpret_cast<bf16x4*>(&sC[swz_off<RS>(j, cpos + 8)]) = c_hi;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     sBt[bt_off(8 * u + e, j)] = b_lo[e];
@@ -431,8 +444,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                     vs[4 * i4 + k] = s4[k] * dx;
                 }
             }
-            store16_nat(&sXt[par][hw][lane * RSJ + 16 * w4], vx);
-            store16_nat(&sXst[hw][lane * RSJ + 16 * w4], vs);
+            store16_nat<RSJ>(sXt[par][hw], lane, 16 * w4, vx);
+            store16_nat<RSJ>(sXst[hw], lane, 16 * w4, vs);
         }
         if (w4 == 0) {
             sL2[hw][lane] = as_f32(st.rec[2]);
@@ -453,13 +466,12 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 const int idx = wave + NW * i;
                 if (idx >= 10) break;
                 const int tb = g1_tb(idx), jb = g1_jb(idx);
-                const __bf16* arow = &sB[(16 * jb + c16) * RS + 8 * q];
-                const __bf16* brow = &sC[(16 * tb + c16) * RS + 8 * q];
+                const int ar = 16 * jb + c16, br = 16 * tb + c16;
                 d[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int s = 0; s < KS; ++s)
-                    d[i] = mfma16(*reinterpret_cast<const bf16x8*>(arow + 32 * s),
-                                  *reinterpret_cast<const bf16x8*>(brow + 32 * s), d[i]);
+                    d[i] = mfma16(*reinterpret_cast<const bf16x8*>(&sB[swz_off<RS>(ar, 32 * s + 8 * q)]),
+                                  *reinterpret_cast<const bf16x8*>(&sC[swz_off<RS>(br, 32 * s + 8 * q)]), d[i]);
             }
             if constexpr (M_IN_B) {
                 __syncthreads();   // every wave's B reads are done
@@ -480,7 +492,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         m[r] = to_bf16(keep_if_le(d[i][r] * __builtin_amdgcn_exp2f(l_t - lj[r]), j0 + r, t));
-                    *reinterpret_cast<bf16x4*>(&sM[hh * (HELIX_CS * RSJ) + t * RSJ + j0]) = m;
+                    *reinterpret_cast<bf16x4*>(&sM[hh * (HELIX_CS * RSJ) + swz_off<RSJ>(t, j0)]) = m;
                 }
             }
         }
@@ -499,10 +511,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
                 acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                const __bf16* crow = &sC[(16 * tb + c16) * RS + 8 * q];
+                const int cr = 16 * tb + c16;
 #pragma unroll
                 for (int s = 0; s < KS; ++s)
-                    acc[tb] = mfma16(*reinterpret_cast<const bf16x8*>(crow + 32 * s), rb[s], acc[tb]);
+                    acc[tb] = mfma16(*reinterpret_cast<const bf16x8*>(&sC[swz_off<RS>(cr, 32 * s + 8 * q)]), rb[s], acc[tb]);
                 const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sE[hw][16 * tb + 4 * q]);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[tb][r] *= e4[r];
@@ -512,7 +524,7 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         {
             bf16x8 xs[2];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) xs[s] = *reinterpret_cast<const bf16x8*>(&sXst[hw][pp * RSJ + 32 * s + 8 * q]);
+            for (int s = 0; s < 2; ++s) xs[s] = *reinterpret_cast<const bf16x8*>(&sXst[hw][swz_off<RSJ>(pp, 32 * s + 8 * q)]);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 f32x4 rn = R[nb] * a_c;
@@ -528,13 +540,13 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         {
             bf16x8 xb[2];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) xb[s] = *reinterpret_cast<const bf16x8*>(&sXt[par][hw][pp * RSJ + 32 * s + 8 * q]);
+            for (int s = 0; s < 2; ++s) xb[s] = *reinterpret_cast<const bf16x8*>(&sXt[par][hw][swz_off<RSJ>(pp, 32 * s + 8 * q)]);
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
                     if (s == 1 && tb < 2) continue;
-                    const bf16x8 ma = *reinterpret_cast<const bf16x8*>(&sMh[(16 * tb + c16) * RSJ + 32 * s + 8 * q]);
+                    const bf16x8 ma = *reinterpret_cast<const bf16x8*>(&sMh[swz_off<RSJ>(16 * tb + c16, 32 * s + 8 * q)]);
                     acc[tb] = mfma16(ma, xb[s], acc[tb]);
                 }
         }
