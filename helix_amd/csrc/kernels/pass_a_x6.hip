@@ -318,10 +318,15 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         __syncthreads();
 
         // This register stage is free again: chunk c+2's inputs travel while
-        // this chunk's and the next one's GEMMs run.
-        if (c + 2 < c_end) {
-            load_stage_x6<NP, IO>(st, p, dt_h, x_h, B_g, c + 2, lane, wave, pw, N);
-            if constexpr (BCC) load_copy_bc(cp, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c + 2, N);
+        // this chunk's and the next one's GEMMs run. The loads are issued on
+        // every path (past the segment they re-read its last chunk, unused):
+        // the compiler's vmcnt waits hold for every path through the loop, and
+        // a skipped group would make the other stage's group the most recent
+        // one, so each step would also wait for the loads just issued.
+        {
+            const int cn = min(c + 2, c_end - 1);
+            load_stage_x6<NP, IO>(st, p, dt_h, x_h, B_g, cn, lane, wave, pw, N);
+            if constexpr (BCC) load_copy_bc(cp, cmap, p, reinterpret_cast<const float*>(B_g), C_g, cn, N);
         }
 
         const float a_c = expf(lendf);
@@ -364,9 +369,10 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
     CopyBC ca, cb;
     load_stage_x6<NP, IO>(sa, p, dt_h, x_h, B_g, c_begin, lane, wave, pw, N);
     if constexpr (BCC) load_copy_bc(ca, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c_begin, N);
-    if (c_begin + 1 < c_end) {
-        load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, c_begin + 1, lane, wave, pw, N);
-        if constexpr (BCC) load_copy_bc(cb, cmap, p, reinterpret_cast<const float*>(B_g), C_g, c_begin + 1, N);
+    {
+        const int cn = min(c_begin + 1, c_end - 1);
+        load_stage_x6<NP, IO>(sb, p, dt_h, x_h, B_g, cn, lane, wave, pw, N);
+        if constexpr (BCC) load_copy_bc(cb, cmap, p, reinterpret_cast<const float*>(B_g), C_g, cn, N);
     }
     if (wave == 0) preamble(sa.dtraw, c_begin);
     __syncthreads();
