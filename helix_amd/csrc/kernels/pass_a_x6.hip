@@ -400,10 +400,6 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         HelixScanParams p, HelixScanBuffers b) {                                                \
         chunk_state_x6_impl<NP, 0>(p, b);                                                       \
     }                                                                                           \
-    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6sbf_n##NP(        \
-        HelixScanParams p, HelixScanBuffers b) {                                                \
-        chunk_state_x6_impl<NP, 1>(p, b);                                                       \
-    }                                                                                           \
     extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_chunk_state_x6agg_n##NP(        \
         HelixScanParams p, HelixScanBuffers b) {                                                \
         chunk_state_x6_impl<NP, 2>(p, b);                                                       \

@@ -209,6 +209,5 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
         chunk_out_f32_impl<NP>(p, b);                                                           \
     }
 
-HELIX_PASS_C_F32(64)
-HELIX_PASS_C_F32(128)
+// The fp32 path at d_state 256, where the bf16x6 Pass C does not fit its LDS.
 HELIX_PASS_C_F32(256)

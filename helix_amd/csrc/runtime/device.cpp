@@ -69,6 +69,7 @@ extern "C" helix_status helix_ctx_create(helix_ctx** out, void* device, const ch
     }
 
     auto* ctx = new helix_ctx();
+    ctx->tuning = helix::rt::tuning_from_env();
     ctx->device = dev;
     ctx->arch = prop.gcnArchName;
     ctx->n_cu = prop.multiProcessorCount;
@@ -119,6 +120,7 @@ extern "C" helix_status helix_ctx_create(helix_ctx** out, void* device, const ch
 extern "C" helix_status helix_ctx_create_host(helix_ctx** out) {
     if (!out) return HELIX_ERR_INVALID_ARG;
     auto* ctx = new helix_ctx();
+    ctx->tuning = helix::rt::tuning_from_env();
     ctx->device = -1;
     ctx->code_object = "<none: host-only context>";
     *out = ctx;

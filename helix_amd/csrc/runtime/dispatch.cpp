@@ -3,8 +3,9 @@
 // Counterpart of the reference's src/runtime/dispatch.mm:55-287. HELIX
 // enqueues onto the caller's HIP stream and never allocates, synchronizes or
 // waits. Every check (arguments, shape gate, scratch size, kernel handles,
-// launch limits) happens before the first launch, so an error leaves nothing
-// enqueued. Stream order sequences the passes; there are no barriers to
+// launch limits) happens before the first launch, so an error it reports
+// leaves nothing enqueued. (A failure of the HIP launch call itself after the
+// first group of a multi-group plan leaves the earlier groups enqueued.) Stream order sequences the passes; there are no barriers to
 // insert.
 //
 // multipass = false, or a diagonal A: one launch of the single-pass kernel, grid
@@ -123,7 +124,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_OK;
     }
 
-    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(*d, tr);
+    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(ctx, *d, tr);
     if (plan.n_chunks <= 0) {
         set_error(ctx, "empty problem");
         return HELIX_ERR_INVALID_ARG;
@@ -170,7 +171,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     params.cpg     = plan.chunks_per_group;
     // A single-group plan on a walking Pass C that runs Pass B's segment scan
     // itself: no Pass B launch.
-    const bool fuse_b = helix::rt::fuse_b_on(tr, plan);
+    const bool fuse_b = helix::rt::fuse_b_on(ctx, tr, plan);
     params.fuse_b  = fuse_b ? 1 : 0;
 
     HelixScanBuffers bufs;
@@ -192,6 +193,24 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     bufs.bcopy   = plan.bc_elems ? sc + plan.off_bc : nullptr;
     bufs.ccopy   = plan.bc_elems ? sc + plan.off_cc : nullptr;
     bufs.pre     = plan.rec_elems ? reinterpret_cast<float*>(sc + plan.off_rec) : nullptr;
+
+    // Launch sizes of the largest group, checked in 64 bits before anything is
+    // enqueued: the kernels decode their 1-D Pass C grid as a 32-bit count.
+    const unsigned hpg = (unsigned)(d->n_head / d->n_group);
+    const unsigned hpw = tr.walk_hpw > 0 ? (unsigned)tr.walk_hpw : HELIX_WALK_HPW(tr.np);
+    const unsigned pairs = (hpg + hpw - 1) / hpw;
+    auto pass_c_groups = [&](int n_cg, int n_seg) -> long long {
+        return tr.walk ? (long long)n_seg * d->n_group * pairs * params.n_pslab * d->n_seq
+                       : (long long)n_cg * d->n_group * plan.n_hblk * d->n_seq;
+    };
+    {
+        const int n_cg = std::min(plan.chunks_per_group, plan.n_chunks);
+        const long long wg_c = pass_c_groups(n_cg, (n_cg + plan.seg_len - 1) / plan.seg_len);
+        if (wg_c > 0xffffffffLL) {
+            set_error(ctx, "Pass C launch grid exceeds 2^32 workgroups");
+            return HELIX_ERR_INVALID_ARG;
+        }
+    }
 
     // Debug-only per-pass timing split (reference dispatch.mm:207-216):
     // HELIX_ONLY_PASS=A|B|C enqueues just that pass; the output is then
@@ -228,13 +247,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c) {
-            const unsigned hpg = (unsigned)(d->n_head / d->n_group);
-            const unsigned hpw = tr.walk_hpw > 0 ? (unsigned)tr.walk_hpw : HELIX_WALK_HPW(tr.np);
-            const unsigned pairs = (hpg + hpw - 1) / hpw;
-            const unsigned n_wg = tr.walk
-                ? (unsigned)params.n_seg * (unsigned)d->n_group * pairs * (unsigned)params.n_pslab *
-                      (unsigned)d->n_seq
-                : (unsigned)params.n_cg * (unsigned)(d->n_group * plan.n_hblk) * (unsigned)d->n_seq;
+            const unsigned n_wg = (unsigned)pass_c_groups(params.n_cg, params.n_seg);
             const unsigned threads = tr.walk ? HELIX_WG * hpw : HELIX_WG;
             // With bf16 copies, Pass C reads B and C from them: dense
             // [seq][t][group][n] rows counted from the group's first token.
@@ -258,6 +271,9 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fC, n_wg, 1, 1, threads, 1, 1, 0, stream, args_c, nullptr);
         }
         if (e != hipSuccess) {
+            // Every argument and limit was checked above, so a launch failure
+            // here comes from the runtime itself. Groups launched before the
+            // failing one stay enqueued: a multi-group encode is not atomic.
             (void)hipGetLastError();
             set_error(ctx, std::string("kernel launch failed: ") + hipGetErrorString(e));
             st = HELIX_ERR_PIPELINE;
@@ -308,7 +324,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->kernel_1pass = tr.k_single;
         return HELIX_OK;
     }
-    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(*d, tr);
+    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(ctx, *d, tr);
     out->n_chunks = pl.n_chunks;
     out->chunks_per_group = pl.chunks_per_group;
     out->n_groups = pl.n_groups;
@@ -322,7 +338,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->s_seg_bytes = pl.sg_elems * sizeof(float);
     out->bccopy_bytes = pl.bc_elems * 2 * 2;
     out->rec_bytes = pl.rec_elems * sizeof(float);
-    const bool fuse_b = helix::rt::fuse_b_on(tr, pl);   // as helix_scan_encode decides
+    const bool fuse_b = helix::rt::fuse_b_on(ctx, tr, pl);   // as helix_scan_encode decides
     out->launches = fuse_b ? 2 : 3 * pl.n_groups;
     out->np = tr.np;
     out->kernel_a = tr.k_chunk_state;

@@ -13,7 +13,25 @@
 #include "helix/helix.h"
 #include "../kernels/helix_params.h"
 
+// Tuning read from the environment once, when the context is created, so that
+// every plan a context makes (helix_scan_scratch_size, helix_scan_encode,
+// helix_scan_plan_info) is a pure function of the context and the descriptor.
+// Two knobs carry the reference's meaning (caps.mm:82-86,170-176); the rest
+// override planner choices for measurement and tests.
+struct helix_tuning {
+    long scratch_mb  = 2048;   // HELIX_SCRATCH_MB: scratch budget per encode
+    bool force_fp32  = false;  // HELIX_FORCE_BACKEND=s...: pin the fp32 path
+    int  passa_split = 6;      // HELIX_PASSA_SPLIT=3: bf16 path Pass A on two split
+                               // planes (three products, state to about 2^-16;
+                               // opt-in, narrower than the reference's fp32 Pass A)
+    int  fuse_b      = -1;     // HELIX_FUSE_B=0|1: Pass B in the walk's prologue
+    int  bccopy      = -1;     // HELIX_WALK_BCCOPY=0: no bf16 copies of B and C
+    int  seg_len     = 0;      // HELIX_SEG_LEN: chunks per Pass A segment
+    int  hblk        = 0;      // HELIX_HBLK: heads per chunk-parallel Pass C workgroup
+};
+
 struct helix_ctx {
+    helix_tuning tuning;
     int         device = -1;
     hipModule_t module = nullptr;
     std::string arch;          // gcnArchName, e.g. "gfx950:sramecc+:xnack-"
@@ -62,19 +80,23 @@ struct HelixMatmulTraits {
 
 namespace helix::rt {
 
+// The environment's tuning (see helix_tuning), read by helix_ctx_create*.
+helix_tuning tuning_from_env();
+
 // Every kernel name in the traits tables; all are resolved at context creation.
 const char* const* all_kernel_names(size_t* count);
 
 // Never fails: falls back to the fp32 path whenever bf16 is not requested or
-// not serviceable. Valid with ctx == nullptr (host-only planning).
-const HelixMatmulTraits& select_traits(helix_ctx* ctx, const helix_scan_desc& d);
+// not serviceable. A pure function of the context's tuning and the
+// descriptor; ctx == nullptr plans with the default tuning.
+const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d);
 
 // How the multipass scan is tiled over the sequence (see helix_params.h):
 // super-chunk groups bound live scratch; segments of seg_len chunks are the
 // unit of Pass A's in-register walk and of Pass B's scan; head blocks are the
 // unit of Pass C's reuse of C.B^T. A pure function of the descriptor, the
-// state precision and the environment, so helix_scan_scratch_size() and the
-// encoder agree exactly.
+// selected kernels and the context's tuning, so helix_scan_scratch_size() and
+// the encoder agree exactly.
 struct MultipassPlan {
     int    n_chunks         = 0;
     int    chunks_per_group = 0;
@@ -94,15 +116,13 @@ struct MultipassPlan {
     size_t total_bytes      = 0;
 };
 
-MultipassPlan plan_multipass(const helix_scan_desc& d, const HelixMatmulTraits& tr);
+MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr);
 
 // Whether the walking Pass C runs Pass B's segment scan itself (no Pass B
 // launch): a single-group plan of at most four segments on a kernel that can;
-// HELIX_FUSE_B=0 / 1 turns it off / on for any single-group plan.
-bool fuse_b_on(const HelixMatmulTraits& tr, const MultipassPlan& plan);
-
-// Scratch budget in bytes: $HELIX_SCRATCH_MB or the default.
-size_t scratch_budget_bytes();
+// the tuning's fuse_b (HELIX_FUSE_B=0 / 1) turns it off / on for any
+// single-group plan.
+bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const MultipassPlan& plan);
 
 // Fills the kernel-side params from the public descriptor. Returns false and
 // sets *why when a launch dimension would exceed the hardware grid limits.

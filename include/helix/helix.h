@@ -75,15 +75,23 @@ typedef enum {
 typedef enum {
     /* One scalar A per head: Mamba-2 / SSD. The form this build accelerates. */
     HELIX_A_SCALAR_PER_HEAD = 0,
-    /* One A per (head, state): Mamba-1 selective scan. Declined. */
+    /* One A per (head, state): Mamba-1 selective scan. Served by the fp32
+     * single-pass kernel up to d_state 128 (the reference declines it). */
     HELIX_A_DIAG_PER_CHANNEL = 1,
 } helix_a_form;
 
 /* Backend names are kept for ABI compatibility. On MI355X:
- *   SGMMA -> every pass on fp32 MFMA (v_mfma_f32_32x32x2_f32)
- *   MPP   -> Pass C on bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 elsewhere
+ *   SGMMA -> the fp32 path: every result fp32-accurate. Passes A and C run
+ *            fp32-accurate GEMMs on bf16 MFMA over operands split into three
+ *            bf16 parts (six products); at d_state 256 Pass C runs on fp32
+ *            MFMA (v_mfma_f32_32x32x2_f32)
+ *   MPP   -> the bf16 path: Pass C's GEMM operands are bf16
+ *            (v_mfma_f32_16x16x32_bf16, fp32 accumulation); Pass A keeps the
+ *            fp32-accurate six-product GEMM and Pass B is fp32, so the carried
+ *            state and s1 stay fp32-accurate
  *   AUTO  -> MPP whenever the shape is served by it, else SGMMA
- *   REF   -> reported when no usable context exists; never launched */
+ *   REF   -> reported when no usable context exists; never launched
+ * multipass = false runs the fp32 single-pass kernel under AUTO and SGMMA. */
 typedef enum {
     HELIX_BACKEND_AUTO  = 0,
     HELIX_BACKEND_SGMMA = 1,

@@ -162,8 +162,17 @@ def _outs(p: Problem):
     return np.zeros(p.y_shape(), np.float32), np.zeros(p.s_shape(), np.float32)
 
 
+def host_threads() -> int:
+    """Threads for the parallel oracle: the cores this process may run on, at
+    most 16 (the host-CPU share of one GPU on the GPU boxes)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, n))
+
+
 def scan(p: Problem, head_mask=None, threads=1, use_ids=True):
-    """fp64 sequential oracle; threads > 1 (or 0 = all cores) uses oracle_scan_mt."""
+    """fp64 sequential oracle; threads > 1 (or 0 = host_threads()) uses oracle_scan_mt."""
+    if threads == 0:
+        threads = host_threads()
     y, s1 = _outs(p)
     ids = p.ids if use_ids else None
     mask = None

@@ -16,7 +16,7 @@ import torch
 
 from oracle import pyoracle as po
 from ggml_fake import SsmScanOp, bridge
-from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, X3_ABS, X3_REL, env, upload
+from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, env, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -86,9 +86,8 @@ def test_bridge_parity(gpu, case):
         # The default path meets the fp32 per-element bound (ggml's op test is
         # an fp32 bar; reference integration/ggml/README.md:43-55).
         assert po.allclose_ratio(y, y_ref, F32_REL, F32_ABS) <= 1.0
-    # The bf16 request may run the walking path's three-product Pass A.
-    s_rel, s_abs = (X3_REL, X3_ABS) if mpp else (F32_REL, F32_ABS)
-    assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
+    # The carried state stays at the fp32 per-element bound on both paths.
+    assert po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0
 
 
 def test_declined_op_writes_nothing(gpu):

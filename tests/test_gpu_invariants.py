@@ -1,7 +1,7 @@
 """GPU tests beyond the shape matrix: invariants at realistic sizes and the
-boundary cases a real caller produces, on every path (multipass fp32,
-multipass bf16 with the chunk-walking and the chunk-parallel Pass C, single
-pass).
+boundary cases a real caller produces, on every path (multipass fp32;
+multipass bf16 with Pass B in its own launch and in the walk's prologue, and
+on the caller's B and C instead of Pass A's bf16 copies; single pass).
 
 * State splitting, the property that pins the carried state (Pass B, the
   cross-group carry, the single-pass register state):
@@ -30,7 +30,7 @@ from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND
                             HELIX_ERR_INVALID_ARG, HELIX_ERR_SCRATCH_TOO_SMALL,
                             HELIX_ERR_UNSUPPORTED_SHAPE, HELIX_OK, HELIX_TENSOR_NULL, HelixTensor,
                             desc_init)
-from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, T, env, run, s1_tolerance, upload
+from gpu_harness import BF16_GATE, F32_ABS, F32_GATE, F32_REL, T, ctx_for, run, s1_tolerance, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -38,12 +38,12 @@ pytestmark = pytest.mark.gpu
 PATHS = [
     ("fp32", HELIX_BACKEND_SGMMA, True, {}),
     ("bf16", HELIX_BACKEND_MPP, True, {}),
-    ("bf16tile", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "tile"}),
-    ("bf16walk", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk"}),
     # Pass B's segment scan in the walk's prologue (ids and s0/s1 strides go
     # through it), and in its own launch.
-    ("bf16walk/fuseB", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "1"}),
-    ("bf16walk/passB", HELIX_BACKEND_MPP, True, {"HELIX_BF16_PASSC": "walk", "HELIX_FUSE_B": "0"}),
+    ("bf16/fuseB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "1"}),
+    ("bf16/passB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "0"}),
+    # The walk on the caller's fp32 B and C instead of Pass A's bf16 copies.
+    ("bf16/nocopy", HELIX_BACKEND_MPP, True, {"HELIX_WALK_BCCOPY": "0"}),
     ("1pass", HELIX_BACKEND_AUTO, False, {}),
 ]
 PATH_IDS = [p[0] for p in PATHS]
@@ -94,12 +94,12 @@ def test_state_splitting(gpu, split_problem, path, split):
     label, backend, multipass, extra = path
     p, y_ref, s_ref = split_problem
     first, second = _sub(p, 0, split), _sub(p, split, p.d.n_tok)
-    with env(**extra):
-        s_rel, s_abs = s1_tolerance(gpu, _desc(p, backend, multipass))
-        s_mid = torch.full(first.s_shape(), float("nan"), device="cuda")
-        _, y1, _ = run(gpu, first, desc=_desc(first, backend, multipass), s1_gpu=s_mid)
-        _, y2, s1 = run(gpu, second, desc=_desc(second, backend, multipass), s0_gpu=s_mid)
-        _, y_full, s1_full = run(gpu, p, desc=_desc(p, backend, multipass))
+    ctx = ctx_for(gpu, **extra)
+    s_rel, s_abs = s1_tolerance(ctx, _desc(p, backend, multipass))
+    s_mid = torch.full(first.s_shape(), float("nan"), device="cuda")
+    _, y1, _ = run(ctx, first, desc=_desc(first, backend, multipass), s1_gpu=s_mid)
+    _, y2, s1 = run(ctx, second, desc=_desc(second, backend, multipass), s0_gpu=s_mid)
+    _, y_full, s1_full = run(ctx, p, desc=_desc(p, backend, multipass))
     y_split = np.concatenate([y1, y2], axis=1)
     gate = _gate(label)
     e_ref, es_ref = _rel(y_split, y_ref), _rel(s1, s_ref)
@@ -108,8 +108,7 @@ def test_state_splitting(gpu, split_problem, path, split):
           flush=True)
     assert np.all(np.isfinite(y_split)) and np.all(np.isfinite(s1))
     assert e_ref <= gate and e_self <= gate
-    # The carried state never passes through bf16 on any path (fp32 bound, or
-    # the bf16x3 bound of the walking bf16 path's default Pass A).
+    # The carried state never passes through bf16 on any path: fp32 bound.
     assert es_ref <= F32_GATE and _rel(s1, s1_full) <= F32_GATE
     assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
 
@@ -128,8 +127,7 @@ def test_ids_permutation(gpu, path):
     y_ref, s_ref = po.scan(p, use_ids=True)
     y_plain, _ = po.scan(p, use_ids=False)
     assert _rel(y_plain, y_ref) > 1e-2      # the permutation is visible in y
-    with env(**extra):
-        _, y, s1 = run(gpu, p, desc=_desc(p, backend, multipass), use_ids=True)
+    _, y, s1 = run(ctx_for(gpu, **extra), p, desc=_desc(p, backend, multipass), use_ids=True)
     ey, es = _rel(y, y_ref), _rel(s1, s_ref)
     print(f"{label} ids {p.ids.tolist()}: y {ey:.2e} s1 {es:.2e}", flush=True)
     assert ey <= _gate(label) and es <= F32_GATE
@@ -218,18 +216,18 @@ def test_strided_views(gpu, path):
     y_ref, s_ref = _dense_y(p, y_buf), _dense_s(p, s_buf)
     y_dense, s_dense = po.scan(base, use_ids=False)
     assert _rel(y_ref, y_dense) < 1e-6 and _rel(s_ref, s_dense) < 1e-6
-    with env(**extra):
-        assert gpu.supported(d), gpu.backend_desc(d)
-        dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
-        y_gpu = torch.full((y_len,), float("nan"), device="cuda")
-        s_gpu = torch.full((s_len,), float("nan"), device="cuda")
-        nbytes = gpu.scratch_size(d)
-        scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
-        rc = gpu.encode(torch.cuda.current_stream().cuda_stream, d, T(dev["s0"]), T(dev["x"]),
-                        T(dev["dt"]), T(dev["A"]), T(dev["B"]), T(dev["C"]), HELIX_TENSOR_NULL,
-                        T(y_gpu), T(s_gpu), T(scratch))
-        assert rc == HELIX_OK, gpu.last_error()
-        torch.cuda.synchronize()
+    ctx = ctx_for(gpu, **extra)
+    assert ctx.supported(d), ctx.backend_desc(d)
+    dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+    y_gpu = torch.full((y_len,), float("nan"), device="cuda")
+    s_gpu = torch.full((s_len,), float("nan"), device="cuda")
+    nbytes = ctx.scratch_size(d)
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    rc = ctx.encode(torch.cuda.current_stream().cuda_stream, d, T(dev["s0"]), T(dev["x"]),
+                    T(dev["dt"]), T(dev["A"]), T(dev["B"]), T(dev["C"]), HELIX_TENSOR_NULL,
+                    T(y_gpu), T(s_gpu), T(scratch))
+    assert rc == HELIX_OK, ctx.last_error()
+    torch.cuda.synchronize()
     y_out, s_out = y_gpu.cpu().numpy(), s_gpu.cpu().numpy()
     y, s1 = _dense_y(p, y_out), _dense_s(p, s_out)
     ey, es = _rel(y, y_ref), _rel(s1, s_ref)
@@ -252,9 +250,9 @@ def test_deterministic_and_encode_into(gpu, path):
     label, backend, multipass, extra = path
     p = po.problem_harness(700, 2, 8, 64, 128, 2, 99, "long")
     d = _desc(p, backend, multipass)
-    with env(**extra):
-        _, y1, s1a = run(gpu, p, desc=d)
-        _, y2, s1b = run(gpu, p, desc=d, into=True)
+    ctx = ctx_for(gpu, **extra)
+    _, y1, s1a = run(ctx, p, desc=d)
+    _, y2, s1b = run(ctx, p, desc=d, into=True)
     assert y1.tobytes() == y2.tobytes() and s1a.tobytes() == s1b.tobytes(), label
 
 

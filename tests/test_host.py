@@ -181,6 +181,13 @@ def test_diagonal_a_runs_the_single_pass_walk(host):
                 assert (k.launches, k.total_bytes, k.kernel_a) == (1, 0, None)
 
 
+def tuned(**kv):
+    """A host-only context created under these environment settings: the
+    tuning knobs are read once, when a context is created."""
+    with env(**kv):
+        return abi.Context(host_only=True)
+
+
 @pytest.mark.parametrize("io,name", [(HELIX_BF16, "bf16"), (HELIX_F16, "f16")])
 def test_16bit_storage_selection(host, io, name):
     # 16-bit x/B/C/y: a bf16 multipass request walks segments (Pass A's
@@ -190,20 +197,16 @@ def test_16bit_storage_selection(host, io, name):
     d = mp(shape)
     d.io_dtype = io
     assert host.supported(d)
-    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x3, {name} storage (d_state<=128)"
+    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_x3agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_chunk_state_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
-    with env(HELIX_PASSA_SPLIT="6"):       # Pass A on six split products
-        assert host.plan_info(d).kernel_a == f"helix_chunk_state_x6agg_{name}io_n128".encode()
-        assert host.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage "
-                                        "(d_state<=128)")
+    x3 = tuned(HELIX_PASSA_SPLIT="3")       # Pass A on three split products: opt-in
+    assert x3.plan_info(d).kernel_a == f"helix_chunk_state_x3agg_{name}io_n128".encode()
+    assert x3.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in), "
+                                  f"{name} storage (d_state<=128)")
     assert k.total_bytes == host.scratch_size(d) > 0 and k.s_local_bytes == 0
-    with env(HELIX_BF16_PASSC="tile"):     # only the walk reads 16-bit operands
-        assert host.plan_info(d).kernel_c == f"helix_scan_walk16_bf16_{name}io_n128".encode()
-    with env(HELIX_WALK="32"):             # the 32 x 32 tile walk
-        assert host.plan_info(d).kernel_c == f"helix_scan_walk_bf16_{name}io_n128".encode()
     for backend, multipass in ((HELIX_BACKEND_SGMMA, True), (HELIX_BACKEND_AUTO, False),
                                (HELIX_BACKEND_SGMMA, False)):
         d = mp((300, 2, 4, 64, 256, 2), backend)
@@ -213,10 +216,9 @@ def test_16bit_storage_selection(host, io, name):
         assert host.backend_desc(d) == f"mfma fp32, single pass, {name} storage (d_state<=256)"
         assert host.scratch_size(d) == 0
         assert host.plan_info(d).kernel_1pass == f"helix_scan_1pass_{name}io_n256".encode()
-    with env(HELIX_FORCE_BACKEND="sgmma"):
-        d = mp(shape)
-        d.io_dtype = io
-        assert host.plan_info(d).kernel_1pass == f"helix_scan_1pass_{name}io_n128".encode()
+    d = mp(shape)
+    d.io_dtype = io
+    assert tuned(HELIX_FORCE_BACKEND="sgmma").plan_info(d).kernel_1pass == f"helix_scan_1pass_{name}io_n128".encode()
 
 
 def test_null_context_and_desc():
@@ -228,6 +230,23 @@ def test_null_context_and_desc():
     assert L.helix_scan_scratch_size(None, None) == 0
 
 
+def test_tuning_read_once_per_context():
+    # A context keeps the tuning it was created with: changing the environment
+    # afterwards changes neither its kernels nor its scratch layout, so
+    # helix_scan_scratch_size and helix_scan_encode always agree.
+    shape = CONFIG_SHAPES["cfg2"]
+    c = tuned()
+    k0 = c.plan_info(mp(shape))
+    with env(HELIX_PASSA_SPLIT="3", HELIX_SCRATCH_MB="1", HELIX_SEG_LEN="2", HELIX_WALK_BCCOPY="0",
+             HELIX_FORCE_BACKEND="sgmma", HELIX_FUSE_B="1"):
+        k1 = c.plan_info(mp(shape))
+        assert c.select_backend(mp(shape)) == HELIX_BACKEND_MPP
+        assert c.scratch_size(mp(shape)) == k0.total_bytes
+    for f in ("kernel_a", "kernel_b", "kernel_c", "total_bytes", "seg_len", "n_groups", "launches"):
+        assert getattr(k0, f) == getattr(k1, f), f
+    c.close()
+
+
 # ---------------------------------------------------------------------------
 # Backend selection (reference caps.mm:79-110)
 # ---------------------------------------------------------------------------
@@ -237,29 +256,26 @@ def test_backend_selection(host):
     assert host.select_backend(mp(shape, HELIX_BACKEND_AUTO)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_SGMMA)) == HELIX_BACKEND_SGMMA
-    # bf16x6 split products by default: Pass A on every path, and the fp32
-    # path's Pass C up to d_state 128.
+    # bf16x6 split products: Pass A on every path, and the fp32 path's Pass C
+    # up to d_state 128.
     assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
-    # The bf16 path walks segments in Pass C up to d_state 128, and at d_state
-    # 256 when Pass A can write bf16 copies of B and C; chunk-parallel
-    # otherwise.
-    # Its Pass A runs three split products (bf16x3); HELIX_PASSA_SPLIT=6 six.
-    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)"
+    # The bf16 path walks segments in Pass C at every d_state; its Pass A runs
+    # six split products (the carried state stays fp32-accurate, reference
+    # caps.mm:65-73) unless HELIX_PASSA_SPLIT=3 opts into three.
+    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)")
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
     assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=256)")
-    with env(HELIX_PASSA_SPLIT="6"):
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
-        assert host.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_x6agg_bc_n128"
-    with env(HELIX_BF16_PASSC="tile"):
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, pass A bf16x6 (d_state<=128)"
-    assert host.backend_desc(mp((64, 1, 1, 64, 256, 1))) == "mfma bf16 pass C, pass A bf16x6 (d_state<=256)"
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
+    assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1)))
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
+    x3 = tuned(HELIX_PASSA_SPLIT="3")
+    assert x3.backend_desc(mp(shape)) == ("mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in) "
+                                          "(d_state<=128)")
+    assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_x3agg_bc_n128"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
-    with env(HELIX_BF16_PASSC="walk"):
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x3 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
     # The plan names the kernels each pass launches.
@@ -268,57 +284,32 @@ def test_backend_selection(host):
     # Config 2 plans eight segments: Pass B keeps its own launch; HELIX_FUSE_B=1
     # runs it in the walk's prologue instead.
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x3agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+        b"helix_chunk_state_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
     assert k.segs_per_group == 8 and k.launches == 3
-    with env(HELIX_FUSE_B="1"):
-        kf = host.plan_info(mp(shape))
-        assert kf.kernel_b is None and kf.launches == 2
+    kf = tuned(HELIX_FUSE_B="1").plan_info(mp(shape))
+    assert kf.kernel_b is None and kf.launches == 2
     # Config 4a: one group of four segments per sequence, fused by default.
     k4 = host.plan_info(mp(CONFIG_SHAPES["cfg4a"]))
     assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2
-    with env(HELIX_SCRATCH_MB="1"):        # many groups: Pass B carries them through s1
-        km = host.plan_info(mp(shape))
-        assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
-        assert km.launches == 3 * km.n_groups
+    km = tuned(HELIX_SCRATCH_MB="1").plan_info(mp(shape))   # many groups, carried through s1
+    assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
+    assert km.launches == 3 * km.n_groups
     L, S, H, P, N, G = shape
     assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
     # Pass A writes one 16-byte decay record per (seq, chunk, head, token) for
-    # the walk and for the fp32 path's bf16x6 Pass C; no other Pass C reads one.
+    # the walk and for the fp32 path's bf16x6 Pass C.
     recs = S * (-(-L // 64)) * H * 64 * 16
     assert k.rec_bytes == recs
     assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == recs
-    with env(HELIX_X6="0"):
-        assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == 0
-    with env(HELIX_BF16_PASSC="tile"):
-        assert host.plan_info(mp(shape)).rec_bytes == 0
+    assert host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
     assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
-    with env(HELIX_WALK_BCCOPY="0"):
-        k0 = host.plan_info(mp(shape))
-        assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x3agg_n128", b"helix_scan_walk16_bf16_n128")
-        assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
-    with env(HELIX_WALK="32"):
-        k32 = host.plan_info(mp(shape))
-        assert (k32.kernel_a, k32.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk_bf16_n128")
-    with env(HELIX_BF16_PASSC="tile"):
-        k = host.plan_info(mp(shape))
-        assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-            b"helix_chunk_state_x6sbf_n128", b"helix_state_scan_f32", b"helix_chunk_out_bf16_n128")
+    k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(shape))
+    assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
+    assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
     k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n128", b"helix_chunk_out_x6_n128")
     k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
-    with env(HELIX_BF16_PASSC="walk"):
-        k = host.plan_info(mp(shape))
-        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x3agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
-    with env(HELIX_X6="0"):
-        k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
-        assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_f32_n128", b"helix_chunk_out_f32_n128")
-    # HELIX_X6=0 selects the fp32-MFMA kernels.
-    with env(HELIX_X6="0"):
-        assert host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA)) == "mfma fp32 (d_state<=128)"
-        assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk (d_state<=128)"
-        with env(HELIX_BF16_PASSC="tile"):
-            assert host.backend_desc(mp(shape)) == "mfma bf16 pass C (d_state<=128)"
     # multipass=false (the descriptor default) runs the fp32 single-pass
     # kernel under AUTO and SGMMA; an explicit MPP request is declined there
     # (reference caps.mm:66,145-147).
@@ -338,8 +329,7 @@ def test_backend_selection(host):
         assert k.kernel_1pass == b"helix_scan_1pass_f32_n%d" % want
         assert k.kernel_a is None and k.kernel_b is None and k.kernel_c is None
     assert host.plan_info(mp(shape)).kernel_1pass is None
-    with env(HELIX_FORCE_BACKEND="sgmma"):
-        assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_SGMMA
+    assert tuned(HELIX_FORCE_BACKEND="sgmma").select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_SGMMA
 
 
 # ---------------------------------------------------------------------------
@@ -350,33 +340,23 @@ def test_bc_copy_condition(host):
     # The copies need the K = heads_per_group * n_pslab workgroups of a chunk
     # to cover its 64 rows with two quads of four state indices per thread:
     # ceil(64 / K) * d_state / 4 <= 512.
-    with env(HELIX_BF16_PASSC="walk"):
-        for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), False),
-                                   ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((1, 192, 128, 1), False),
-                                   ((2, 192, 128, 1), True), ((2, 64, 64, 1), True), ((1, 64, 64, 1), False)]:
-            d = mp((4096, 1, H, P, N, G))
-            k = host.plan_info(d)
-            assert (k.bccopy_bytes > 0) == copy, (H, P, N, G)
-            assert k.kernel_c.endswith(b"_n%d" % k.np)
-            assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
-    # Not with 16-bit storage (Pass C reads the caller's 16-bit B and C), nor
-    # with the fp32-MFMA Pass A.
+    for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), False),
+                               ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((1, 192, 128, 1), False),
+                               ((2, 192, 128, 1), True), ((2, 64, 64, 1), True), ((1, 64, 64, 1), False)]:
+        d = mp((4096, 1, H, P, N, G))
+        k = host.plan_info(d)
+        assert (k.bccopy_bytes > 0) == copy, (H, P, N, G)
+        assert k.kernel_c.endswith(b"_n%d" % k.np)
+        assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
+    # Not with 16-bit storage (Pass C reads the caller's 16-bit B and C).
     d = mp((4096, 1, 64, 64, 128, 8))
     d.io_dtype = HELIX_BF16
     assert host.plan_info(d).bccopy_bytes == 0
-    with env(HELIX_X6="0"):
-        assert host.plan_info(mp((4096, 1, 64, 64, 128, 8))).bccopy_bytes == 0
 
 
-@pytest.mark.parametrize("passc", [None, "walk"])
 @pytest.mark.parametrize("name", list(CONFIG_SHAPES))
 @pytest.mark.parametrize("backend", [HELIX_BACKEND_SGMMA, HELIX_BACKEND_MPP])
-def test_plan_invariants(host, name, backend, passc):
-    with env(HELIX_BF16_PASSC=passc):
-        _plan_invariants(host, name, backend)
-
-
-def _plan_invariants(host, name, backend):
+def test_plan_invariants(host, name, backend):
     shape = CONFIG_SHAPES[name]
     L, S, H, P, N, G = shape
     d = mp(shape, backend)
@@ -393,25 +373,20 @@ def _plan_invariants(host, name, backend):
     # State scratch is stored as padded 64 x np slab tiles (helix_params.h).
     state = S * H * (-(-P // 64)) * 64 * info.np
     assert info.np == (64 if N <= 64 else 128 if N <= 128 else 256)
-    es = 2 if backend == HELIX_BACKEND_MPP else 4
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
     # The walking Pass C keeps the chunk-local states in registers, so its
-    # plan holds no s_local region; it runs only on the bf16 path.
+    # plan holds no s_local region; it is the bf16 path's Pass C.
     walk = b"walk" in info.kernel_c
-    assert not walk or backend == HELIX_BACKEND_MPP
-    if os.environ.get("HELIX_BF16_PASSC") == "walk" and backend == HELIX_BACKEND_MPP and N <= 128:
-        assert walk
-    if os.environ.get("HELIX_BF16_PASSC") == "tile":
-        assert not walk
-    want_sl = state * info.chunks_per_group * es if (info.seg_len > 1 and not walk) else 0
+    assert walk == (backend == HELIX_BACKEND_MPP)
+    want_sl = state * info.chunks_per_group * 4 if (info.seg_len > 1 and not walk) else 0
     assert info.s_local_bytes == want_sl
     assert info.s_seg_bytes == state * info.segs_per_group * 4
     # every region 256-byte aligned and the total covers them all
     assert info.total_bytes % 256 == 0
     assert info.total_bytes >= want_sl + info.s_seg_bytes
-    # The 16 x 16 walk runs Pass B's segment scan in its prologue when the plan
-    # has one group of at most four segments: no Pass B launch.
-    fused = b"walk16" in info.kernel_c and info.n_groups == 1 and info.segs_per_group <= 4
+    # The walk runs Pass B's segment scan in its prologue when the plan has one
+    # group of at most four segments: no Pass B launch.
+    fused = walk and info.n_groups == 1 and info.segs_per_group <= 4
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
 
@@ -425,15 +400,13 @@ def test_plan_single_group_for_baseline_configs(host):
 
 def test_tiny_budget_forces_many_groups(host):
     shape = (2048, 1, 8, 64, 128, 2)
-    with env(HELIX_SCRATCH_MB=1):
-        info = host.plan_info(mp(shape))
-        assert info.n_groups > 1
-        # 1 MiB admits at least one chunk; never more than the budget unless
-        # a single chunk alone exceeds it.
-        one_chunk = 8 * 64 * 128 * 2
-        assert info.total_bytes <= max(1 << 20, 2 * one_chunk + 4096) or info.chunks_per_group == 1
-    with env(HELIX_SCRATCH_MB=None):
-        assert host.plan_info(mp(shape)).n_groups == 1
+    info = tuned(HELIX_SCRATCH_MB=1).plan_info(mp(shape))
+    assert info.n_groups > 1
+    # 1 MiB admits at least one chunk; never more than the budget unless
+    # a single chunk alone exceeds it.
+    one_chunk = 8 * 64 * 128 * 2
+    assert info.total_bytes <= max(1 << 20, 2 * one_chunk + 4096) or info.chunks_per_group == 1
+    assert tuned(HELIX_SCRATCH_MB=None).plan_info(mp(shape)).n_groups == 1
 
 
 def test_scratch_zero_for_single_pass(host):
@@ -444,9 +417,8 @@ def test_scratch_zero_for_single_pass(host):
 
 def test_seg_len_and_hblk_overrides(host):
     shape = CONFIG_SHAPES["cfg2"]
-    with env(HELIX_SEG_LEN=4, HELIX_HBLK=8):
-        info = host.plan_info(mp(shape))
-        assert info.seg_len == 4 and info.hblk == 8 and info.n_hblk == 1
+    info = tuned(HELIX_SEG_LEN=4, HELIX_HBLK=8).plan_info(mp(shape))
+    assert info.seg_len == 4 and info.hblk == 8 and info.n_hblk == 1
 
 
 # ---------------------------------------------------------------------------
