@@ -26,7 +26,9 @@ ABI_SYMBOLS = (
     "helix_scan_encode",
     "helix_scan_encode_into",
 )
-HOST_SYMBOLS = ("helix_ctx_create_host", "helix_scan_plan_info")
+HOST_SYMBOLS = ("helix_ctx_create_host", "helix_scan_plan_info", "helix_scan_encode_noalloc")
+# include/helix/helix_host.h HELIX_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class HelixPlanInfo(ctypes.Structure):
@@ -95,6 +97,8 @@ def lib():
     L.helix_scan_encode.restype = c_int
     L.helix_scan_encode_into.argtypes = enc
     L.helix_scan_encode_into.restype = c_int
+    L.helix_scan_encode_noalloc.argtypes = [c_void_p, c_void_p, dp] + [T] * 9
+    L.helix_scan_encode_noalloc.restype = c_int
     L.helix_scan_plan_info.argtypes = [c_void_p, dp, POINTER(HelixPlanInfo)]
     L.helix_scan_plan_info.restype = c_int
     _lib = L
@@ -158,6 +162,11 @@ class Context:
         if st != HELIX_OK:
             raise HelixError(st, "descriptor declined")
         return info
+
+    def encode_noalloc(self, stream: int, d: HelixScanDesc, s0, x, dt, A, B, C, ids, y, s1) -> int:
+        """helix_scan_encode_noalloc: the scan on the library's fixed scratch."""
+        return int(lib().helix_scan_encode_noalloc(self.handle, c_void_p(stream), ctypes.byref(d), s0, x, dt,
+                                                   A, B, C, ids, y, s1))
 
     def encode(self, stream: int, d: HelixScanDesc, s0, x, dt, A, B, C, ids, y, s1, scratch,
                into: bool = False) -> int:

@@ -38,10 +38,13 @@ inline void* dptr(helix_tensor t) {
     return t.buf ? static_cast<char*>(t.buf) + t.offset : nullptr;
 }
 
+// scratch_sized: the scratch is the library's own fixed array, already known
+// to hold the plan (helix_scan_encode_noalloc), so its allocation is not
+// queried.
 helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
                          helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
                          helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
-                         helix_tensor s1, helix_tensor scratch) {
+                         helix_tensor s1, helix_tensor scratch, bool scratch_sized = false) {
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
@@ -129,7 +132,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         set_error(ctx, "empty problem");
         return HELIX_ERR_INVALID_ARG;
     }
-    if (plan.total_bytes > 0) {
+    if (plan.total_bytes > 0 && !scratch_sized) {
         if (!scratch.buf) {
             set_error(ctx, "multipass requires a scratch buffer of helix_scan_scratch_size() bytes");
             return HELIX_ERR_SCRATCH_TOO_SMALL;
@@ -303,6 +306,39 @@ extern "C" helix_status helix_scan_encode_into(helix_ctx* ctx, void* encoder, co
     if (!ctx || !d) return HELIX_ERR_INVALID_ARG;
     return encode_core(ctx, static_cast<hipStream_t>(encoder), d, s0, x, dt, A, B, C, ids, y, s1,
                        scratch);
+}
+
+extern "C" helix_status helix_scan_encode_noalloc(helix_ctx* ctx, void* stream, const helix_scan_desc* d,
+                                                  helix_tensor s0, helix_tensor x, helix_tensor dt,
+                                                  helix_tensor A, helix_tensor B, helix_tensor C,
+                                                  helix_tensor ids, helix_tensor y, helix_tensor s1) {
+    if (!ctx || !d) return HELIX_ERR_INVALID_ARG;
+    if (!helix_scan_supported(ctx, d)) {
+        set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
+        return HELIX_ERR_UNSUPPORTED_SHAPE;
+    }
+    const size_t need = helix_scan_scratch_size(ctx, d);
+    if (need > HELIX_NOALLOC_SCRATCH_BYTES) {
+        set_error(ctx, "plan needs " + std::to_string(need) + " bytes of scratch, more than the " +
+                           std::to_string((size_t)HELIX_NOALLOC_SCRATCH_BYTES) +
+                           " of the fixed scratch (HELIX_NOALLOC_SCRATCH_BYTES); use helix_scan_encode");
+        return HELIX_ERR_SCRATCH_TOO_SMALL;
+    }
+    helix_tensor scratch = HELIX_TENSOR_NULL;
+    if (need > 0) {
+        if (!ctx->module) {
+            set_error(ctx, "context has no device (host-only context)");
+            return HELIX_ERR_NO_DEVICE;
+        }
+        std::string why;
+        scratch.buf = helix::rt::noalloc_scratch(ctx->device, &why);
+        if (!scratch.buf) {
+            set_error(ctx, why);
+            return HELIX_ERR_NO_DEVICE;
+        }
+    }
+    return encode_core(ctx, static_cast<hipStream_t>(stream), d, s0, x, dt, A, B, C, ids, y, s1, scratch,
+                       /*scratch_sized=*/true);
 }
 
 extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,

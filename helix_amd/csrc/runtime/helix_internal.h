@@ -131,4 +131,10 @@ bool build_params(const helix_scan_desc& d, HelixScanParams* out, std::string* w
 // Thread-local last-error bookkeeping.
 void set_error(const helix_ctx* ctx, const std::string& msg);
 
+// The fixed scratch of helix_scan_encode_noalloc (noalloc.hip): resolve its
+// device address once per device, with that device current (called by
+// helix_ctx_create), and look it up (null, with *why set, if unavailable).
+void noalloc_setup(int device);
+void* noalloc_scratch(int device, std::string* why);
+
 }  // namespace helix::rt

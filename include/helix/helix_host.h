@@ -1,8 +1,9 @@
 /* helix_host.h -- host-side extras of the MI355X HELIX build.
  *
- * Neither entry point has a counterpart in the reference ABI; both exist for
- * callers that plan without a GPU (build machines, schedulers sizing scratch
- * pools ahead of time) and for the CPU test suite.
+ * None of these entry points has a counterpart in the reference ABI. The
+ * host-only context and plan_info exist for callers that plan without a GPU
+ * (build machines, schedulers sizing scratch pools ahead of time) and for the
+ * CPU test suite; helix_scan_encode_noalloc for callers that cannot allocate.
  */
 #ifndef HELIX_HOST_H
 #define HELIX_HOST_H
@@ -47,6 +48,31 @@ typedef struct {
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */
 helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
                                   helix_plan_info* out);
+
+/* Size of the fixed scratch helix_scan_encode_noalloc uses on each GPU. */
+#define HELIX_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* helix_scan_encode without a scratch argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. It has no counterpart in the reference ABI.
+ *
+ * Same descriptor, tensors, plan, kernels and results as helix_scan_encode;
+ * the scratch is a fixed device array of HELIX_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends (its address
+ * is resolved when a context is created on that GPU). The call allocates and
+ * frees nothing. A plan needing more scratch than that
+ * (helix_scan_scratch_size(ctx, d) > HELIX_NOALLOC_SCRATCH_BYTES) returns
+ * HELIX_ERR_SCRATCH_TOO_SMALL before anything is enqueued; the single pass
+ * needs none. No part of the array needs to start at zero: every region a
+ * kernel reads is written earlier in the same encode.
+ *
+ * Every call on one GPU shares that GPU's array and it keeps the last call's
+ * contents: calls whose work overlaps on one GPU (other streams, other
+ * threads, other contexts) race and must be serialised by the caller. */
+helix_status helix_scan_encode_noalloc(helix_ctx* ctx, void* stream, const helix_scan_desc* desc,
+                                       helix_tensor s0, helix_tensor x, helix_tensor dt,
+                                       helix_tensor A, helix_tensor B, helix_tensor C,
+                                       helix_tensor ids, helix_tensor y, helix_tensor s1);
 
 #ifdef __cplusplus
 }

@@ -230,6 +230,26 @@ def test_null_context_and_desc():
     assert L.helix_scan_scratch_size(None, None) == 0
 
 
+def test_noalloc_host_checks(host):
+    # helix_scan_encode_noalloc refuses, before anything is enqueued, a plan
+    # whose scratch exceeds its fixed array (config 2 on the fp32 path needs
+    # 280 MiB), and a host-only context has no device for one that fits.
+    t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
+    big = mp(CONFIG_SHAPES["cfg2"], HELIX_BACKEND_SGMMA)
+    assert host.scratch_size(big) > abi.NOALLOC_SCRATCH_BYTES
+    assert host.encode_noalloc(0, big, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
+    assert "HELIX_NOALLOC_SCRATCH_BYTES" in host.last_error()
+    fits = mp(CONFIG_SHAPES["cfg2"])
+    assert 0 < host.scratch_size(fits) <= abi.NOALLOC_SCRATCH_BYTES
+    assert host.encode_noalloc(0, fits, *t) == HELIX_ERR_NO_DEVICE
+    bad = mp((64, 1, 2, 64, 260, 1))
+    assert host.encode_noalloc(0, bad, *t) == HELIX_ERR_UNSUPPORTED_SHAPE
+    assert abi.lib().helix_scan_encode_noalloc(None, None, None, *t) == HELIX_ERR_INVALID_ARG
+    header = open(os.path.join(ROOT, "include", "helix", "helix_host.h")).read()
+    assert re.search(r"#define HELIX_NOALLOC_SCRATCH_BYTES \(64u << 20\)", header)
+    assert abi.NOALLOC_SCRATCH_BYTES == 64 << 20
+
+
 def test_tuning_read_once_per_context():
     # A context keeps the tuning it was created with: changing the environment
     # afterwards changes neither its kernels nor its scratch layout, so
