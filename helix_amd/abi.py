@@ -28,7 +28,7 @@ ABI_SYMBOLS = (
 )
 HOST_SYMBOLS = ("helix_ctx_create_host", "helix_scan_plan_info", "helix_scan_encode_noalloc")
 # include/helix/helix_host.h HELIX_NOALLOC_SCRATCH_BYTES
-NOALLOC_SCRATCH_BYTES = 64 << 20
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 
 class HelixPlanInfo(ctypes.Structure):
@@ -52,6 +52,8 @@ class HelixPlanInfo(ctypes.Structure):
         ("kernel_1pass", ctypes.c_char_p),
         ("bccopy_bytes", c_uint64),
         ("rec_bytes", c_uint64),
+        ("walk_len", c_int32),
+        ("walks_per_group", c_int32),
     ]
 
 

@@ -163,19 +163,41 @@ HELIX_DEV int tile_unit(int NT, int pt, int nt, int r4, int lane) {
 // Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
 HELIX_DEV __bf16 to_bf16(float v) { return (__bf16)v; }
 
+// a * b with 0 * x = 0 for every x, NaN and infinity included
+// (v_mul_legacy_f32); otherwise the IEEE product. For a weight that is exactly
+// zero on padding rows whose loaded value is not under the kernel's control.
+HELIX_DEV float mul_legacy(float a, float b) {
+    float r;
+    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // Raw buffer access. The resource (base and byte range) sits in four SGPRs,
 // the lane's byte offset is one 32-bit VGPR, and a compile-time byte offset
 // goes to the instruction's soffset/immediate fields, so a run of loads from
 // one wave-uniform region costs no per-load address VGPRs (flat/global loads
 // need a 64-bit VGPR address each once offsets exceed the 4 KiB immediate).
 // `base` must be wave-uniform. Raw buffer range checking (stride 0) returns 0
-// for a read at or past `bytes` and drops such a write.
+// for a read at or past `bytes` and drops such a write; the checked offset is
+// the lane's offset plus the scalar offset (measured on gfx950: a read whose
+// scalar offset alone passes the range returns 0).
 typedef __amdgpu_buffer_rsrc_t helix_rsrc;
 
 HELIX_DEV helix_rsrc make_rsrc(const void* base, unsigned bytes) {
     // Dword 3 = 0x00020000: DATA_FORMAT 32, the value gfx9-family untyped
     // buffer instructions are used with.
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// The same with the base and range read from the first active lane: for a
+// resource built from values the compiler cannot prove wave-uniform (a select
+// on a wave-uniform flag, for one), which it would otherwise address through a
+// waterfall loop around every access.
+HELIX_DEV helix_rsrc make_rsrc_u(const void* base, unsigned bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    return make_rsrc(reinterpret_cast<const void*>(((unsigned long long)hi << 32) | lo),
+                     __builtin_amdgcn_readfirstlane(bytes));
 }
 HELIX_DEV float buf_f32(helix_rsrc r, int voff, int soff) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
@@ -349,6 +371,25 @@ HELIX_DEV void x6_write8(__bf16* planes, int r, int c, const float* v) {
     *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, NCH>(2, r, c)]) = q2;
 }
 
+// Split eight fp32 values v[0..7] into NS bf16 planes (NS = 3: split3_pair,
+// NS = 2: split2_pair) and store them as chunk c of row r.
+template <int ROWS, int NS>
+HELIX_DEV void stage_split8(__bf16* planes, int r, int c, const float* v) {
+    u32x4 q[NS];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        unsigned w[3];
+        if constexpr (NS == 3)
+            split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
+        else
+            split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+#pragma unroll
+        for (int k = 0; k < NS; ++k) q[k][e] = w[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(k, r, c)]) = q[k];
+}
+
 // Raw-register form of an element of T: a float stays a float, a bf16 stays
 // its 16 bits zero-extended in a 32-bit register. Loads into this form carry
 // no data dependence (nothing packs two 16-bit results into one register), so
@@ -497,6 +538,14 @@ HELIX_DEV int store_off_if_lt(int off, int a, int la, int b, int lb) {
 // instead, which costs no vector issue slots.
 HELIX_DEV int sgpr_fresh(int v) {
     asm volatile("" : "+s"(v));
+    return v;
+}
+
+// The same for a per-lane value: expressions built on it inside a loop are
+// recomputed there instead of being hoisted out as dozens of loop-invariant
+// VGPRs (one per unrolled load address) that would stay live across the loop.
+HELIX_DEV int vgpr_fresh(int v) {
+    asm volatile("" : "+v"(v));
     return v;
 }
 

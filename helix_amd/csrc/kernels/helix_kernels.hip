@@ -2,6 +2,7 @@
 // object embedded in libhelix.so. Kernel names are resolved by the runtime
 // (helix_amd/csrc/runtime/caps.cpp traits tables).
 #include "pass_a_x6.hip"
+#include "pass_a_hb.hip"
 #include "pass_b.hip"
 #include "pass_c_f32.hip"
 #include "pass_c_x6.hip"

@@ -69,6 +69,10 @@
  * head per workgroup, two workgroups per CU, measured slower at config 2:
  * the B and C staging is then done for every head). */
 #define HELIX_WALK16_HPW(np) HELIX_WALK_HPW(np)
+/* Items ((head, P slab) pairs of one B/C group) per workgroup of the
+ * head-block Pass A (pass_a_hb.hip), two waves each, d_state <= 128. */
+#define HELIX_HB 4
+#define HELIX_HB_THREADS (128 * HELIX_HB)
 
 typedef struct HelixScanParams {
     int n_tok;
@@ -97,8 +101,12 @@ typedef struct HelixScanParams {
     /* Super-chunk group currently encoded. */
     int chunk_base;       /* global index of the group's first chunk */
     int n_cg;             /* chunks in this group */
-    int seg_len;          /* chunks per segment */
+    int seg_len;          /* chunks per segment (Pass A, Pass B, chunk-parallel Pass C) */
     int n_seg;            /* segments in this group = ceil(n_cg / seg_len) */
+    int walk_len;         /* chunks per walking Pass C workgroup, a multiple of
+                             seg_len: walk segment w starts at segment
+                             w * walk_len / seg_len */
+    int n_walk;           /* walk segments in this group = ceil(n_cg / walk_len) */
     int hblk;             /* heads per Pass C workgroup */
     int n_hblk;           /* head blocks per B/C group */
     int np;               /* d_state padded to the kernels' tile width (64/128/256) */

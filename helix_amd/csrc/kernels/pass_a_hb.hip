@@ -1,0 +1,541 @@
+// pass_a_hb.hip -- Pass A over head blocks: B is split once per workgroup and
+// shared by HELIX_HB (head, P slab) items of one B/C group.
+//
+// Same computation and outputs as pass_a_x6.hip (reference helix_chunk_state_f32,
+// src/kernels/helix_scan_multipass.metal:51-149, walked over a segment):
+//     R <- exp(L_end_c) R + B_c^T . (decay . dt . x)_c
+// with the GEMM on v_mfma_f32_32x32x16_bf16 over operands split into NS bf16
+// planes (NS = 3: six products, fp32 accuracy; NS = 2: three products, the
+// opt-in narrower state), issued smallest term first. The operand values, the
+// K order and the product order are those of pass_a_x6.hip, so the two kernels
+// produce the same segment aggregates.
+//
+// What differs is how the work is laid out:
+//   - One workgroup of 2 * HELIX_HB waves owns HELIX_HB items that share a B/C
+//     group: the B operand of a chunk (64 tokens x d_state) is split into its
+//     bf16 planes once, in LDS, for all of them. Items are (head, P slab)
+//     pairs, so a group's heads and a head's slabs are tiled alike.
+//   - Each wave owns one item's 32-channel P tile and every state index: it
+//     loads its x values from global memory straight into the MFMA operand
+//     layout (lane lo = channel, tokens 16 s + 8 hi + e), scales and splits
+//     them in registers. x never touches LDS and no value is split twice.
+//   - The B planes are double-buffered: the next chunk's are written while
+//     this chunk's are read, so a chunk costs one barrier.
+//   - The decay preamble of each item runs in one of its two waves, a chunk
+//     ahead, and reaches the other through LDS (double-buffered, so the one
+//     barrier per chunk covers it).
+//   - Every memory instruction of the chunk loop runs on every path (masked
+//     stores go through a zero-range resource or an out-of-range offset): on
+//     gfx950 the vmcnt counter counts stores too, and a store on one path only
+//     would make the compiler's waits cover the next chunk's loads.
+//   - The bf16 copies of B and C for the walking Pass C are written by one
+//     wave per 8-token block per group: wave w of item block ib copies its
+//     block when ib == w % (item blocks per group).
+// Grid: one workgroup per (seq, B/C group, item block, segment), 1-D and
+// decoded XCD-aware so a segment's item blocks (which read the same B rows)
+// run on one XCD.
+#include "helix_common.h"
+
+// x of the wave's P tile for one chunk, in storage form: channel 32 pt + lo,
+// tokens 16 s + 8 hi + e.
+template <typename IO>
+struct HbX {
+    typename IoWord<IO>::type v[4][8];
+};
+
+// This thread's share of a chunk's B rows, and of its C rows for the copies:
+// lane (q, r) = (lane % NQ, lane / NQ), NQ = NP / 4 quads of four state
+// indices per row, holds state indices 4 q .. 4 q + 3 of the L = 8 / (64 / NQ)
+// consecutive tokens 8 wave + L r + i, one 16-byte run (8 bytes in 16-bit
+// storage) per token. Few, wide loads: a chunk step stays under the vmcnt
+// counter's 63 outstanding operations.
+template <int NP, typename IO>
+struct HbRows {
+    static constexpr int NQ = NP / 4;                       // quads per row
+    static constexpr int L = 8 * NQ / 64;                   // tokens per lane (4 at NP 128, 2 at 64)
+    static constexpr int W = sizeof(IO) == 4 ? 4 : 2;       // 32-bit words per run
+    unsigned b[L][W];
+    unsigned c[L][4];
+};
+
+template <typename IO>
+HELIX_DEV typename IoWord<IO>::type io_load_at(helix_rsrc r, int voff_bytes, int soff_bytes) {
+    if constexpr (sizeof(IO) == 4)
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff_bytes, soff_bytes, 0));
+    else
+        return (unsigned)__builtin_bit_cast(unsigned short,
+                                            __builtin_amdgcn_raw_buffer_load_b16(r, voff_bytes, soff_bytes, 0));
+}
+
+// K step s (tokens 16 s + 8 hi + e) of chunk c's x. Branch-free: the row goes
+// in the scalar offset and the lane's half (8 hi rows) in its own offset. In a
+// ragged last chunk, rows past tlen fall outside the resource's range and read
+// 0 when tokens are the outer dimension of x's layout; in any layout their
+// weight is exactly 0 and the weighting is a legacy multiply (mul_legacy), so
+// whatever such a row reads contributes nothing.
+template <typename IO>
+__device__ __forceinline__ void hb_load_xs(typename IoWord<IO>::type (&v)[8], const HelixScanParams& p,
+                                           const IO* __restrict__ x_w, int c, int s, int lane, int pt, int pw) {
+    constexpr int ES = (int)sizeof(IO);
+    const int t0 = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sx2 = (int)p.s_x[2];
+    const int sx0 = sgpr_fresh((int)p.s_x[0]);
+    const helix_rsrc rx = make_rsrc(x_w + (long long)t0 * p.s_x[0],
+                                    ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)ES);
+    const int lo = lane & 31, hi = lane >> 5;
+    const int xc = min(32 * pt + lo, pw - 1) * sx2;
+    const int vx = (xc + 8 * hi * sx0) * ES;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = io_load_at<IO>(rx, vx, (16 * s + e) * sgpr_fresh(sx0) * ES);
+}
+
+// dt of token lane of chunk c.
+HELIX_DEV float hb_load_dt(const HelixScanParams& p, const float* __restrict__ dt_h, int c, int lane) {
+    const int t0 = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sdt = (int)p.s_dt[0];
+    const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+    return buf_f32(rdt, min(lane, tlen - 1) * sdt * 4, 0);
+}
+
+// Scheduling fence for the vector memory instructions only: loads and stores
+// stay where the program puts them (so a refill never moves above the last use
+// of the registers it overwrites, and the in-order vmcnt waits keep their
+// distance), while ALU, MFMA and LDS work may still be interleaved across it.
+HELIX_DEV void vmem_fence() { __builtin_amdgcn_sched_barrier(0x0001 | 0x0002 | 0x0004 | 0x0008 | 0x0080 | 0x0400); }
+
+// B rows (and C rows, for a copying wave) of chunk c. Rows clamp to the last
+// valid token and state indices to d_state, so every load is in bounds; a wave
+// that does not copy issues its C loads past the resource's range, which
+// returns zeros without touching memory (the loads stay on every path, so the
+// vmcnt waits are the same for every wave).
+template <int NP, typename IO, bool BCC>
+__device__ __forceinline__ void hb_load_rows(HbRows<NP, IO>& st, const HelixScanParams& p,
+                                             const IO* __restrict__ B_g, const float* __restrict__ C_g, int c,
+                                             int lane, int wave, int N, bool copier) {
+    constexpr int ES = (int)sizeof(IO);
+    constexpr int NQ = HbRows<NP, IO>::NQ, L = HbRows<NP, IO>::L;
+    const int t0 = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sb0 = sgpr_fresh((int)p.s_b[0]);
+    const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
+    const int q = lane % NQ, r = lane / NQ;
+    const int n0 = min(4 * q, N - 4);
+    const int j0 = 8 * wave + L * r;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        const int jr = min(j0 + i, tlen - 1);
+        const int off = (jr * sb0 + n0) * ES;
+        if constexpr (ES == 4) {
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) st.b[i][k] = w[k];
+        } else {
+            const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rb, off, 0, 0);
+            st.b[i][0] = w[0];
+            st.b[i][1] = w[1];
+        }
+    }
+    if constexpr (BCC) {
+        const int sc0 = sgpr_fresh((int)p.s_c[0]);
+        const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * 4u);
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const int jr = min(j0 + i, tlen - 1);
+            const int off = (int)((unsigned)((jr * sc0 + n0) * 4) | (copier ? 0u : 0x80000000u));
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) st.c[i][k] = w[k];
+        }
+    }
+}
+
+// State index k (< 4) of token i of this thread's B rows, as fp32.
+template <int NP, typename IO>
+HELIX_DEV float hb_b(const HbRows<NP, IO>& st, int i, int k) {
+    if constexpr (sizeof(IO) == 4) {
+        return as_f32(st.b[i][k]);
+    } else {
+        const unsigned w = st.b[i][k >> 1];
+        return io_f32<IO>((unsigned short)((k & 1) ? (w >> 16) : (w & 0xffffu)));
+    }
+}
+
+// B planes in LDS: [plane][row n][64 tokens], rows padded to HB_RS elements
+// (36 dwords). An MFMA operand read takes 16 consecutive rows of one 16-byte
+// chunk per 16 lanes; at a row stride of 4 mod 16 dwords those rows start on
+// 16 distinct 4-bank groups, so the read is conflict-free. With padding rather
+// than a swizzle, every read and write is one per-lane base plus an immediate
+// offset, so the addresses cost a few registers instead of one per operand.
+constexpr int HB_RS = HELIX_CS + 8;
+template <int NP>
+HELIX_DEV int hb_off(int k, int r, int c) {
+    return (k * NP + r) * HB_RS + c * 8;
+}
+
+// Split the L consecutive tokens' values v[0..L-1] of state index n into NS
+// planes and store them at tokens t .. t + L - 1 of row n (hb_off layout).
+template <int NP, int NS, int L>
+HELIX_DEV void hb_stage_run(__bf16* planes, int n, int t, const float* v) {
+    static_assert(L == 2 || L == 4, "runs of two or four tokens");
+    unsigned q[NS][L / 2];
+#pragma unroll
+    for (int e = 0; e < L / 2; ++e) {
+        unsigned w[3];
+        if constexpr (NS == 3)
+            split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
+        else
+            split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+#pragma unroll
+        for (int k = 0; k < NS; ++k) q[k][e] = w[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        __bf16* dst = &planes[(k * NP + n) * HB_RS + t];
+        if constexpr (L == 4)
+            *reinterpret_cast<u32x2*>(dst) = u32x2{q[k][0], q[k][1]};
+        else
+            *reinterpret_cast<unsigned*>(dst) = q[k][0];
+    }
+}
+
+// The decay preamble of chunk c (lane = token): the weight w_lane = exp(L_end -
+// Lcum_lane) dt_lane (0 past tlen) of the chunk's GEMM, L_end, and the token's
+// decay record for Pass C (the forms of store_decay_record / store_decay_record64).
+struct HbPre {
+    float w;
+    float lend;
+    u32x4 rec;
+};
+
+template <int MODE>
+__device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtraw, float A_h, int c, int lane) {
+    const int t0 = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const float dtv = keep_if_lt(helix_dt(p, dtraw), lane, tlen);
+    const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+    const double lend = bcast(lcum, 63);
+    HbPre r;
+    r.w = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
+    r.lend = (float)lend;
+    if constexpr (MODE == 2) {
+        const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
+        const float l2 = (float)(lcum * 1.4426950408889634074);
+        const float e = expf((float)lcum);
+        r.rec = u32x4{as_u32(dtv), as_u32(sdec), as_u32(l2), as_u32(e)};
+    } else {
+        const float e = expf((float)lcum);
+        const unsigned long long u = __builtin_bit_cast(unsigned long long, lcum);
+        r.rec = u32x4{as_u32(dtv), as_u32(e), (unsigned)u, (unsigned)(u >> 32)};
+    }
+    return r;
+}
+
+// MODE 0: store the in-segment prefix R_c (fp32) before each chunk, and the
+// fp64 decay records of the fp32 path's Pass C; MODE 2: segment aggregates only,
+// and the walk's decay records. IO: the caller's storage type of x and B. BCC:
+// write the bf16 copies of B and C (fp32 storage). NS: split planes per operand.
+template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3>
+__device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(NP == 64 || NP == 128, "the double-buffered B planes of d_state 256 exceed the LDS");
+    static_assert(NS == 2 || NS == 3, "two or three split planes");
+    static_assert(MODE == 0 || MODE == 2, "per-chunk fp32 prefixes or aggregates only");
+    constexpr int HB = HELIX_HB;
+    constexpr int NTN = NP / 32;        // 32-row n tiles per wave
+    constexpr int PLANES = NS * NP * HB_RS;
+    __shared__ __attribute__((aligned(16))) __bf16 sB[2 * PLANES];   // two chunks' planes
+    // Per chunk parity and item: w_j of the chunk's 64 tokens, and L_end at [64].
+    __shared__ __attribute__((aligned(16))) float sW[2][HB][HELIX_CS + 4];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
+    // Wave w owns P tile w / HB of item w % HB: each SIMD (waves s and s + 4)
+    // holds one wave of each P tile, so the preamble waves (P tile 0) are
+    // spread over the SIMDs.
+    const int is = wave % HB, pt = wave / HB;
+
+    const int ipg = p.heads_per_group * p.n_pslab;        // items per group
+    const int nib = (ipg + HB - 1) / HB;                  // item blocks per group
+    const unsigned total = (unsigned)(p.n_seq * p.n_group * nib * p.n_seg);
+    unsigned wid = xcd_logical_id(blockIdx.x, total);
+    const int ib = (int)(wid % (unsigned)nib);      wid /= (unsigned)nib;
+    const int seg = (int)(wid % (unsigned)p.n_seg); wid /= (unsigned)p.n_seg;
+    const int g = (int)(wid % (unsigned)p.n_group);
+    const int seq = (int)(wid / (unsigned)p.n_group);
+
+    // Item of this wave; a block's spare waves repeat its last item and store nothing.
+    const int ii_raw = ib * HB + is;
+    const bool item_ok = ii_raw < ipg;
+    const int ii = min(ii_raw, ipg - 1);
+    const int h = g * p.heads_per_group + ii / p.n_pslab;
+    const int slab = ii % p.n_pslab;
+    const int p0 = slab * HELIX_HD;
+    const int pw = min(HELIX_HD, p.head_dim - p0);
+    const int N = p.d_state;
+
+    const int c_begin = seg * p.seg_len;
+    const int c_end = min(c_begin + p.seg_len, p.n_cg);
+    if (c_begin >= c_end) return;
+
+    const float A_h = b.A[(long long)h * p.s_a];
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const IO* __restrict__ x_w = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
+    const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
+    const bool copier = BCC && (wave % nib) == ib;
+    const bool leader = item_ok && slab == 0 && pt == 0;   // stores the head's records
+    const long long tile_off = state_tile_off(p, h, slab);
+    const unsigned tile_bytes = item_ok ? 64u * NP * 4u : 0u;   // spare waves store nothing
+
+    f32x16 acc[NTN];
+#pragma unroll
+    for (int i = 0; i < NTN; ++i) acc[i] = zero16();
+    float lam = 0.0f;   // log-decay of this segment before chunk c
+
+    // B planes of chunk c into `planes`, and the bf16 copies of its B and C rows.
+    constexpr int NQ = HbRows<NP, IO>::NQ, L = HbRows<NP, IO>::L;
+    const int q4 = 4 * (lane % NQ), tr = 8 * wave + L * (lane / NQ);   // this thread's state indices, tokens
+    auto stage_b = [&](const HbRows<NP, IO>& rows, int c, __bf16* planes) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float v[L];
+#pragma unroll
+            for (int i = 0; i < L; ++i) v[i] = hb_b<NP, IO>(rows, i, k);
+            hb_stage_run<NP, NS, L>(planes, q4 + k, tr, v);
+        }
+        if constexpr (BCC) {
+            const int t0 = (p.chunk_base + c) * HELIX_CS;
+            const int tlen = min(HELIX_CS, p.n_tok - t0);
+            const long long gn = (long long)p.n_group * N;
+            const long long base = ((long long)seq * p.cpg * HELIX_CS + (long long)c * HELIX_CS) * gn + (long long)g * N;
+            const unsigned bytes = copier ? (unsigned)((HELIX_CS - 1) * gn + N) * 2u : 0u;
+            const helix_rsrc rb = make_rsrc_u(static_cast<__bf16*>(b.bcopy) + base, bytes);
+            const helix_rsrc rc = make_rsrc_u(static_cast<__bf16*>(b.ccopy) + base, bytes);
+            const int gni = (int)gn;
+#pragma unroll
+            for (int i = 0; i < L; ++i) {
+                const int j = tr + i;
+                const int off = store_off_if_lt((j * gni + q4) * 2, j, tlen, q4, N);
+                const u32x2 wb = {pk_bf16(as_f32(rows.b[i][0]), as_f32(rows.b[i][1])),
+                                  pk_bf16(as_f32(rows.b[i][2]), as_f32(rows.b[i][3]))};
+                const u32x2 wc = {pk_bf16(as_f32(rows.c[i][0]), as_f32(rows.c[i][1])),
+                                  pk_bf16(as_f32(rows.c[i][2]), as_f32(rows.c[i][3]))};
+                __builtin_amdgcn_raw_buffer_store_b64(wb, rb, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b64(wc, rc, off, 0, 0);
+            }
+        }
+    };
+
+    HbX<IO> xs;
+    HbRows<NP, IO> rows;
+    float dtraw;   // dt of token lane of the chunk the next preamble forms
+
+    // The preamble of chunk c in the P-tile-0 wave of each item, into the
+    // chunk's weight buffer (the branch holds no vector-memory instruction),
+    // then the chunk's record and ld[c] = lam_c from every wave, cancelled by a
+    // zero range on all but the head's leader wave, and on every wave when the
+    // call only repeats the segment's last chunk (`live` false: ld[c] already
+    // holds the log-decay before it). Every vector-memory instruction of the
+    // chunk loop thus runs on every path.
+    auto preamble = [&](int c, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
+        HbPre pr{0.0f, 0.0f, u32x4{0u, 0u, 0u, 0u}};
+        if (pt == 0) {
+            pr = hb_preamble<MODE>(p, dtraw, A_h, c, lane);
+            wdst[is][lane] = pr.w;
+            if (lane == 0) wdst[is][HELIX_CS] = pr.lend;
+        }
+        const bool rec = live && leader && b.pre != nullptr;
+        const float* recp = rec ? b.pre + (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 4) : b.s_seg;
+        __builtin_amdgcn_raw_buffer_store_b128(pr.rec, make_rsrc_u(recp, rec ? HELIX_CS * 16u : 0u), lane * 16,
+                                               0, 0);
+        const float* ldp = b.ld + seq * p.ld_seq + (long long)c * p.n_head + h;
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && leader ? 4u : 0u),
+                                              lane == 0 ? 0 : (int)0x80000000, 0, 0);
+    };
+
+    // One chunk. Its B planes are in `cur` and its weights in `wcur` (both
+    // staged a step earlier), its x in xs; `rows` holds chunk c + 1's B (and C)
+    // rows and dtraw chunk c + 1's dt. Every memory instruction runs on every
+    // path; past the segment's last chunk the loads and the staging repeat
+    // that chunk (nothing reads the result). The loop is not unrolled: the
+    // loop-carried registers then keep one assignment, with no copies at the
+    // back edge.
+    auto step = [&](int c, const __bf16* cur, __bf16* nxt, float (*wcur)[HELIX_CS + 4],
+                    float (*wnxt)[HELIX_CS + 4]) {
+        const int cn = min(c + 1, c_end - 1);
+        const float* __restrict__ wrow = wcur[is];
+        const float lendf = wrow[HELIX_CS];
+        if constexpr (MODE == 0) {
+            // R_c, the state entering chunk c from this segment's own chunks
+            // (none for its first chunk: a zero range stores nothing).
+            const float* dst = static_cast<const float*>(b.s_local) + seq * p.sl_seq + (long long)c * p.sl_cg +
+                               tile_off;
+            const helix_rsrc rd = make_rsrc_u(dst, c > c_begin ? tile_bytes : 0u);
+#pragma unroll
+            for (int i = 0; i < NTN; ++i)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    buf_store_unit<float>(rd, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2],
+                                          acc[i][4 * r4 + 3], lane, tile_unit(NTN, pt, i, r4, 0));
+        }
+        const float a_c = expf(lendf);
+#pragma unroll
+        for (int i = 0; i < NTN; ++i) acc[i] *= a_c;
+
+        // R[n][p] += sum_j B^T[n][j] (w_j x[j][p]) over four K steps of 16 tokens,
+        // in groups of two n tiles. The B planes of the next group and the
+        // weights of the next K step are read from LDS while the current
+        // group's MFMAs run, so no MFMA waits on the LDS.
+        constexpr int NG = NTN / 2;                 // groups of two n tiles per K step
+        auto read_group = [&](int s, int i0, bf16x8 (&bp)[2][NS]) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int k = 0; k < NS; ++k)
+                    bp[i][k] = *reinterpret_cast<const bf16x8*>(&cur[hb_off<NP>(k, 32 * (i0 + i) + lo, 2 * s + hi)]);
+        };
+        auto read_w = [&](int s, f32x4& w0, f32x4& w1) {
+            w0 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi]);
+            w1 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi + 4]);
+        };
+        // Smallest terms first, the two accumulators interleaved so no MFMA
+        // waits on the one before it.
+        auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NS], const bf16x8 (&xp)[NS]) {
+            if constexpr (NS == 3) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][2], xp[0], acc[i0 + i]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[1], acc[i0 + i]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[2], acc[i0 + i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[0], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[1], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[0], acc[i0 + i]);
+        };
+        bf16x8 bq[2][2][NS];        // the B planes of two groups, in turn
+        f32x4 w0, w1;
+        read_group(0, 0, bq[0]);
+        read_w(0, w0, w1);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = mul_legacy(w0[e], io_widen<IO>(xs.v[s][e]));
+                v[4 + e] = mul_legacy(w1[e], io_widen<IO>(xs.v[s][4 + e]));
+            }
+            u32x4 xq[NS];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                unsigned w[3];
+                if constexpr (NS == 3)
+                    split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
+                else
+                    split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+#pragma unroll
+                for (int k = 0; k < NS; ++k) xq[k][e] = w[k];
+            }
+            bf16x8 xp[NS];
+#pragma unroll
+            for (int k = 0; k < NS; ++k) xp[k] = __builtin_bit_cast(bf16x8, xq[k]);
+            if (s + 1 < 4) read_w(s + 1, w0, w1);
+            // K step s of the next chunk's x into the registers just split:
+            // it has a whole chunk step to arrive.
+            vmem_fence();
+            hb_load_xs<IO>(xs.v[s], p, x_w, cn, s, lane, pt, pw);
+            vmem_fence();
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) {
+                const int q = (s * NG + gi) & 1;          // buffer of this group
+                const int s_n = gi + 1 < NG ? s : s + 1;  // the next group's K step
+                const int g_n = gi + 1 < NG ? gi + 1 : 0;
+                if (s_n < 4) read_group(s_n, 2 * g_n, bq[q ^ 1]);
+                mfma_group(2 * gi, bq[q], xp);
+            }
+        }
+        // The next chunk's weights and B planes, then its successor's rows and dt.
+        lam += lendf;
+        preamble(cn, lam, wnxt, c + 1 < c_end);
+        stage_b(rows, cn, nxt);
+        vmem_fence();
+        hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, min(c + 2, c_end - 1), lane, wave, N, copier);
+        dtraw = hb_load_dt(p, dt_h, min(c + 2, c_end - 1), lane);
+        __syncthreads();
+    };
+
+    // Prologue: chunk c_begin's weights and B planes in buffer 0, its x in
+    // flight, chunk c_begin + 1's rows and dt in flight.
+    dtraw = hb_load_dt(p, dt_h, c_begin, lane);
+    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c_begin, lane, wave, N, copier);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) hb_load_xs<IO>(xs.v[s], p, x_w, c_begin, s, lane, pt, pw);
+    preamble(c_begin, 0.0f, sW[0], true);
+    stage_b(rows, c_begin, sB);
+    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, min(c_begin + 1, c_end - 1), lane, wave, N, copier);
+    dtraw = hb_load_dt(p, dt_h, min(c_begin + 1, c_end - 1), lane);
+    __syncthreads();
+#pragma unroll 1
+    for (int c = c_begin; c < c_end; ++c) {
+        const int par = (c - c_begin) & 1;
+        step(c, sB + par * PLANES, sB + (PLANES - par * PLANES), sW[par], sW[par ^ 1]);
+    }
+
+    // Segment aggregate D_s and the segment's log-decay.
+    {
+        const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
+        const helix_rsrc rs = make_rsrc_u(sg, tile_bytes);
+#pragma unroll
+        for (int i = 0; i < NTN; ++i)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                buf_store_unit<float>(rs, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2], acc[i][4 * r4 + 3],
+                                      lane, tile_unit(NTN, pt, i, r4, 0));
+    }
+    if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
+}
+
+#define HELIX_PASS_A_HB(NP)                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6f32_n##NP(    \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 0>(p, b);                                                             \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_n##NP(    \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2>(p, b);                                                             \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_bc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, true>(p, b);                                                \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, __bf16>(p, b);                                                     \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_f16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, _Float16>(p, b);                                                   \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_n##NP(    \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, false, 2>(p, b);                                            \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_bc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, true, 2>(p, b);                                             \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, __bf16, false, 2>(p, b);                                           \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_f16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, _Float16, false, 2>(p, b);                                         \
+    }
+
+HELIX_PASS_A_HB(64)
+HELIX_PASS_A_HB(128)

@@ -165,25 +165,6 @@ __device__ __forceinline__ void store_copy_bc(const CopyBC& cp, const CopyMap& m
     }
 }
 
-// Split eight fp32 values v[0..7] into NS bf16 planes (NS = 3: split3_pair,
-// NS = 2: split2_pair) and store them as chunk c of row r.
-template <int ROWS, int NS>
-HELIX_DEV void stage_split8(__bf16* planes, int r, int c, const float* v) {
-    u32x4 q[NS];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        unsigned w[3];
-        if constexpr (NS == 3)
-            split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
-        else
-            split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
-#pragma unroll
-        for (int k = 0; k < NS; ++k) q[k][e] = w[k];
-    }
-#pragma unroll
-    for (int k = 0; k < NS; ++k) *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, 8>(k, r, c)]) = q[k];
-}
-
 // Stage 16 consecutive tokens (chunks c0, c0 + 1) of row r of an NS-plane
 // operand from fp32 values v[0..15].
 template <int ROWS, int NS>
@@ -442,12 +423,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         chunk_state_x6_impl<NP, 2, _Float16>(p, b);                                             \
     }
 
-HELIX_PASS_A_X6(64)
-HELIX_PASS_A_X6(128)
+// d_state 256 only: up to 128 the head-block kernels (pass_a_hb.hip) serve.
 HELIX_PASS_A_X6(256)
-HELIX_PASS_A_X6_IO(64)
-HELIX_PASS_A_X6_IO(128)
 HELIX_PASS_A_X6_IO(256)
-HELIX_PASS_A_X3(64)
-HELIX_PASS_A_X3(128)
 HELIX_PASS_A_X3(256)

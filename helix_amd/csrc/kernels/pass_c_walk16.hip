@@ -1,9 +1,10 @@
 // pass_c_walk16.hip -- the chunk-walking bf16 Pass C on 16 x 16 x 32 MFMA tiles.
 //
-// Same contract as the 32 x 32 walk (pass_c_walk.hip): one workgroup owns
-// (seq, segment, HELIX_WALK_HPW heads of one B/C group, 64-wide P slab),
-// starts each head from S_seg (fp32: from Pass B, or, with p.fuse_b, scanned
-// here from s0 and Pass A's segment aggregates) and walks the segment's chunks,
+// One workgroup owns (seq, walk segment of walk_len chunks, HELIX_WALK_HPW
+// heads of one B/C group, 64-wide P slab), starts each head from S_seg (fp32:
+// from Pass B at the Pass A segment the walk segment starts at, or, with
+// p.fuse_b, scanned here from s0 and Pass A's segment aggregates) and walks
+// the segment's chunks,
 // producing per chunk
 //     y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C R)        (G1, G2, G3)
 //     R <- exp(L_end) R + B^T . (decay . dt . x)                  (G4)
@@ -218,10 +219,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
 
     // 1-D grid, a group's head blocks consecutive in the logical order so they
     // share an XCD (and the chunk's B and C in its L2).
-    const unsigned total = (unsigned)(p.n_seg * p.n_group * npair * p.n_pslab * p.n_seq);
+    const unsigned total = (unsigned)(p.n_walk * p.n_group * npair * p.n_pslab * p.n_seq);
     unsigned wid = xcd_logical_id(blockIdx.x, total);
-    const int pair = (int)(wid % (unsigned)npair);   wid /= (unsigned)npair;
-    const int seg  = (int)(wid % (unsigned)p.n_seg); wid /= (unsigned)p.n_seg;
+    const int pair = (int)(wid % (unsigned)npair);    wid /= (unsigned)npair;
+    const int seg  = (int)(wid % (unsigned)p.n_walk); wid /= (unsigned)p.n_walk;
     const int g    = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
     const int slab = (int)(wid % (unsigned)p.n_pslab);
     const int seq  = (int)(wid / (unsigned)p.n_pslab);
@@ -233,8 +234,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     const int p0 = slab * HELIX_HD;
     const int pw = min(HELIX_HD, P - p0);
 
-    const int c_begin = seg * p.seg_len;
-    const int c_end   = min(c_begin + p.seg_len, p.n_cg);
+    const int c_begin = seg * p.walk_len;
+    const int c_end   = min(c_begin + p.walk_len, p.n_cg);
     if (c_begin >= c_end) return;
 
     // Decay records of this head, chunk stride n_head * 64 records.
@@ -296,9 +297,11 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 T[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
         };
         if (!p.fuse_b) {
-            load_tile(seg, R);      // S_seg(seg), from Pass B
+            // S_seg of the Pass A segment this walk segment starts at, from Pass B.
+            load_tile(seg * (p.walk_len / p.seg_len), R);
         } else {
-            // Pass B folded in (single-group plans): the tiles hold Pass A's
+            // Pass B folded in (single-group plans whose walk segments are Pass
+            // A's segments): the tiles hold Pass A's
             // segment aggregates D_s, and this workgroup runs Pass B's
             // recurrence (helix_state_scan_f32, same operation order) up to
             // its own segment:

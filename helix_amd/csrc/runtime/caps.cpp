@@ -20,10 +20,13 @@ namespace {
 // Kernel families (helix_amd/csrc/kernels). d_state is padded to np = 64, 128
 // or 256 and every family is instantiated at each np it serves.
 //
+//   Pass A runs the head-block kernels (pass_a_hb.hip: B split once per
+//   workgroup of four items, helix_chunk_state_hb_*) up to d_state 128 and the
+//   per-item kernels (pass_a_x6.hip, helix_chunk_state_x*) at d_state 256.
 //   fp32 path (SGMMA, or HELIX_FORCE_BACKEND=s..., multipass, fp32 storage):
-//     Pass A helix_chunk_state_x6f32_n*  bf16x6 split products, stores the
-//                                        per-chunk prefix states R_c (fp32) and
-//                                        fp64 decay records
+//     Pass A helix_chunk_state{_hb}_x6f32_n*  bf16x6 split products, stores
+//                                        the per-chunk prefix states R_c (fp32)
+//                                        and fp64 decay records
 //     Pass B helix_state_scan_f32
 //     Pass C helix_chunk_out_x6_n{64,128}  bf16x6 split products
 //            helix_chunk_out_f32_n256      fp32 MFMA (the bf16x6 planes of a
@@ -33,10 +36,10 @@ namespace {
 //   aggregates only, on six split products (fp32 accuracy, the reference's
 //   contract for the carried state) or, opted into with HELIX_PASSA_SPLIT=3,
 //   on three.
-//     Pass A helix_chunk_state_x{6,3}agg_n*        fp32 storage
-//            helix_chunk_state_x{6,3}agg_bc_n*     ... also writes bf16 copies of
-//                                                  B and C for the walk
-//            helix_chunk_state_x{6,3}agg_{bf16,f16}io_n*   16-bit storage
+//     Pass A helix_chunk_state{_hb}_x{6,3}agg_n*     fp32 storage
+//            helix_chunk_state{_hb}_x{6,3}agg_bc_n*  ... also writes bf16 copies
+//                                                    of B and C for the walk
+//            helix_chunk_state{_hb}_x{6,3}agg_{bf16,f16}io_n*   16-bit storage
 //     Pass B helix_state_scan_f32 (or the walk's prologue, fuse_b)
 //     Pass C helix_scan_walk16_bf16{,_bc,_bf16io,_f16io}_n*
 //   single pass (multipass = false): helix_scan_1pass_{f32,bf16io,f16io}_n*,
@@ -104,7 +107,9 @@ struct TraitTable {
                 const bool x6c = kNps[k] <= 128;
                 t.name = keep(std::string(x6c ? "mfma fp32, passes A and C bf16x6" : "mfma fp32, pass A bf16x6") +
                               upto);
-                t.k_chunk_state = kernel("helix_chunk_state_x6f32_n" + np);
+                t.k_chunk_state = kernel(std::string(kNps[k] <= 128 ? "helix_chunk_state_hb_x6f32_n"
+                                                                    : "helix_chunk_state_x6f32_n") + np);
+                t.a_hb = kNps[k] <= 128;
                 t.k_state_scan = kernel("helix_state_scan_f32");
                 t.k_chunk_out = kernel(x6c ? "helix_chunk_out_x6_n" + np : "helix_chunk_out_f32_n" + np);
                 t.mfma_a = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
@@ -123,8 +128,10 @@ struct TraitTable {
                         t.name = keep(std::string("mfma bf16 pass C, chunk walk, pass A ") +
                                       (s6 ? "bf16x6" : "bf16x3 (narrower state: opt-in)") +
                                       (io == 1 ? ", bf16 storage" : io == 2 ? ", f16 storage" : "") + upto);
-                        t.k_chunk_state = kernel(std::string("helix_chunk_state_") + split + "agg_" +
-                                                 (bc ? "bc_" : kIoTag[io]) + "n" + np);
+                        const bool hb = kNps[k] <= 128;
+                        t.k_chunk_state = kernel(std::string(hb ? "helix_chunk_state_hb_" : "helix_chunk_state_") +
+                                                 split + "agg_" + (bc ? "bc_" : kIoTag[io]) + "n" + np);
+                        t.a_hb = hb;
                         t.k_state_scan = kernel("helix_state_scan_f32");
                         t.k_chunk_out = kernel(std::string("helix_scan_walk16_bf16_") + (bc ? "bc_" : kIoTag[io]) +
                                                "n" + np);
@@ -154,6 +161,9 @@ const TraitTable& table() {
 // copy_map); the tuning's bccopy = 0 (HELIX_WALK_BCCOPY=0) switches them off.
 bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d) {
     if (tu.bccopy == 0) return false;
+    // The head-block Pass A (d_state <= 128) copies at every shape: one wave
+    // per 8-token block of a chunk and group (pass_a_hb.hip).
+    if (d.d_state <= 128) return true;
     const long K = (long)(d.n_head / d.n_group) * ((d.head_dim + HELIX_HD - 1) / HELIX_HD);
     return (64 + K - 1) / K * (d.d_state / 4) <= 2 * 256;
 }
@@ -240,7 +250,9 @@ const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_de
 constexpr int kFuseBMaxSegs = 4;
 
 bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const MultipassPlan& plan) {
-    if (!tr.walk_fuse_b || plan.n_groups != 1) return false;
+    // The walk's prologue scans whole walk segments: only when they are Pass
+    // A's segments too.
+    if (!tr.walk_fuse_b || plan.n_groups != 1 || plan.walk_len != plan.seg_len) return false;
     const helix_tuning& tu = tuning_of(ctx);
     if (tu.fuse_b >= 0) return tu.fuse_b == 1;
     return plan.segs_per_group <= kFuseBMaxSegs;
@@ -248,15 +260,18 @@ bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const Multipas
 
 namespace {
 
-// Chunks per segment for a group of `cpg` chunks: enough segments that Pass A
-// has ~kTargetWgA workgroups, and no more (a longer walk keeps more of the
-// chunk recurrence in registers and shortens Pass B), up to kMaxSegLen (past
-// that the walks get too long to fill the chip: at config 4a, 64-chunk
-// segments took 1.03 ms and 16-chunk ones 0.95 ms).
+// Chunks per walk segment for a group of `cpg` chunks (the walking Pass C;
+// also Pass A's segment on the per-item kernels): enough segments that there
+// are ~kTargetWgA (seq, head, P slab) items x segments, and no more (a longer
+// walk keeps more of the chunk recurrence in registers and shortens Pass B), up
+// to kMaxSegLen (past that the walks get too long to fill the chip: at config
+// 4a, 64-chunk segments took 1.03 ms and 16-chunk ones 0.95 ms).
 constexpr long kMaxSegLen = 16;
+// The head-block Pass A runs one 512-thread workgroup per CU (its LDS holds
+// two chunks of split B planes): ~256 workgroups fill the chip.
+constexpr long kTargetWgHb = 256;
 
-int choose_seg_len(const helix_tuning& tu, const helix_scan_desc& d, int cpg) {
-    if (tu.seg_len > 0) return std::min(tu.seg_len, cpg);
+int choose_walk_len(const helix_scan_desc& d, int cpg) {
     const long n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
     const long items = (long)d.n_seq * d.n_head * n_pslab;
     const long segs = std::max<long>(1, (kTargetWgA + items - 1) / items);
@@ -264,14 +279,46 @@ int choose_seg_len(const helix_tuning& tu, const helix_scan_desc& d, int cpg) {
     return (int)std::max<long>(1, std::min<long>(len, cpg));
 }
 
-void layout(const helix_tuning& tu, const helix_scan_desc& d, bool bf16_state, bool walk, bool bccopy, bool rec,
-            int np, int cpg, MultipassPlan* pl) {
+// Pass A's segment (seg_len) and the walk's (walk_len, a multiple of it). The
+// head-block Pass A takes the longest divisor of walk_len that still gives
+// ~kTargetWgHb workgroups, so its segments nest in the walk's. HELIX_SEG_LEN
+// sets seg_len, and walk_len is then rounded to a multiple of it.
+void choose_lengths(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg,
+                    int* seg_len, int* walk_len) {
+    int w = choose_walk_len(d, cpg);
+    int a = w;
+    if (tu.seg_len > 0) {
+        a = std::min(tu.seg_len, cpg);
+        w = std::max(a, (w / a) * a);
+    } else if (tr.a_hb) {
+        const long n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
+        const long ipg = (long)(d.n_head / d.n_group) * n_pslab;
+        const long per_seg = (long)d.n_seq * d.n_group * ((ipg + HELIX_HB - 1) / HELIX_HB);
+        a = 1;
+        for (int cand = w; cand >= 1; --cand) {
+            if (w % cand) continue;
+            if (per_seg * ((cpg + cand - 1) / cand) >= kTargetWgHb) {
+                a = cand;
+                break;
+            }
+        }
+    }
+    if (!tr.walk) w = a;
+    *seg_len = a;
+    *walk_len = w;
+}
+
+void layout(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg,
+            MultipassPlan* pl) {
+    const bool bf16_state = tr.bf16_state, walk = tr.walk, bccopy = tr.bccopy, rec = tr.rec_kind != 0;
+    const int np = tr.np;
     // State scratch is stored as padded slab tiles of 64 x np (helix_params.h).
     const size_t n_pslab = (size_t)(d.head_dim + HELIX_HD - 1) / HELIX_HD;
     const size_t state = (size_t)d.n_seq * d.n_head * n_pslab * 64 * (size_t)np;
     pl->chunks_per_group = cpg;
-    pl->seg_len = choose_seg_len(tu, d, cpg);
+    choose_lengths(tu, d, tr, cpg, &pl->seg_len, &pl->walk_len);
     pl->segs_per_group = (cpg + pl->seg_len - 1) / pl->seg_len;
+    pl->walks_per_group = (cpg + pl->walk_len - 1) / pl->walk_len;
     pl->sl_elem_bytes = bf16_state ? 2 : 4;
     pl->sl_elems = (pl->seg_len > 1 && !walk) ? state * (size_t)cpg : 0;
     pl->sg_elems = state * (size_t)pl->segs_per_group;
@@ -315,7 +362,7 @@ MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, con
     long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
     cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
     for (;;) {
-        layout(tu, d, bf16_state, tr.walk, tr.bccopy, tr.rec_kind != 0, tr.np, (int)cpg, &pl);
+        layout(tu, d, tr, (int)cpg, &pl);
         if (pl.total_bytes <= budget || cpg == 1) break;
         cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
     }

@@ -12,11 +12,13 @@
 // (n_seq * n_head * n_pslab) x 256 threads, no scratch.
 //
 // Otherwise, per super-chunk group, in stream order:
-//   Pass A  grid (segments, n_head, n_seq * n_pslab)    x 256 threads
+//   Pass A  grid (n_seq * n_group * item blocks * segments) x 512 threads (the
+//           head-block kernel, d_state <= 128; 1-D, decoded XCD-aware), or
+//           grid (segments, n_head, n_seq * n_pslab) x 256 threads
 //   Pass B  grid (ceil(n_pslab*16*np/256), n_head, n_seq) x 256 threads
 //   Pass C  grid (chunks * n_group * n_hblk * n_seq)    x 256 threads (1-D,
 //           decoded XCD-aware in the kernel); the walking variant runs one
-//           workgroup of 256 * HELIX_WALK_HPW(np) threads per (segment,
+//           workgroup of 256 * HELIX_WALK_HPW(np) threads per (walk segment,
 //           block of that many heads of a group, P slab, seq) instead
 // The ragged-tail padding and the bf16 staging of B and C that the reference
 // runs as separate passes (dispatch.mm:218-245) happen inside the Pass A/C
@@ -163,6 +165,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     const long long HT = (long long)d->n_head * params.n_pslab * 64 * tr.np;
     params.np      = tr.np;
     params.seg_len = plan.seg_len;
+    params.walk_len = plan.walk_len;
     params.hblk    = plan.hblk;
     params.n_hblk  = plan.n_hblk;
     params.sl_cg   = HT;
@@ -202,15 +205,20 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     const unsigned hpg = (unsigned)(d->n_head / d->n_group);
     const unsigned hpw = tr.walk_hpw > 0 ? (unsigned)tr.walk_hpw : HELIX_WALK_HPW(tr.np);
     const unsigned pairs = (hpg + hpw - 1) / hpw;
-    auto pass_c_groups = [&](int n_cg, int n_seg) -> long long {
-        return tr.walk ? (long long)n_seg * d->n_group * pairs * params.n_pslab * d->n_seq
+    auto pass_c_groups = [&](int n_cg, int n_walk) -> long long {
+        return tr.walk ? (long long)n_walk * d->n_group * pairs * params.n_pslab * d->n_seq
                        : (long long)n_cg * d->n_group * plan.n_hblk * d->n_seq;
     };
+    // Head-block Pass A: item blocks of HELIX_HB (head, P slab) pairs per group.
+    const long long ipg = (long long)hpg * params.n_pslab;
+    const long long nib = (ipg + HELIX_HB - 1) / HELIX_HB;
+    auto pass_a_groups = [&](int n_seg) -> long long { return (long long)d->n_seq * d->n_group * nib * n_seg; };
     {
         const int n_cg = std::min(plan.chunks_per_group, plan.n_chunks);
-        const long long wg_c = pass_c_groups(n_cg, (n_cg + plan.seg_len - 1) / plan.seg_len);
-        if (wg_c > 0xffffffffLL) {
-            set_error(ctx, "Pass C launch grid exceeds 2^32 workgroups");
+        const long long wg_c = pass_c_groups(n_cg, (n_cg + plan.walk_len - 1) / plan.walk_len);
+        const long long wg_a = tr.a_hb ? pass_a_groups((n_cg + plan.seg_len - 1) / plan.seg_len) : 0;
+        if (wg_c > 0xffffffffLL || wg_a > 0xffffffffLL) {
+            set_error(ctx, "launch grid exceeds 2^32 workgroups");
             return HELIX_ERR_INVALID_ARG;
         }
     }
@@ -239,10 +247,14 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         params.chunk_base  = base;
         params.n_cg        = std::min(plan.chunks_per_group, plan.n_chunks - base);
         params.n_seg       = (params.n_cg + plan.seg_len - 1) / plan.seg_len;
+        params.n_walk      = (params.n_cg + plan.walk_len - 1) / plan.walk_len;
         params.first_group = base == 0 ? 1 : 0;
 
         hipError_t e = hipSuccess;
-        if (do_a)
+        if (do_a && tr.a_hb)
+            e = hipModuleLaunchKernel(fA, (unsigned)pass_a_groups(params.n_seg), 1, 1, HELIX_HB_THREADS, 1, 1, 0,
+                                      stream, args, nullptr);
+        else if (do_a)
             e = hipModuleLaunchKernel(fA, (unsigned)params.n_seg, (unsigned)d->n_head,
                                       (unsigned)(d->n_seq * params.n_pslab), HELIX_WG, 1, 1, 0,
                                       stream, args, nullptr);
@@ -250,7 +262,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             e = hipModuleLaunchKernel(fB, (PN + HELIX_WG - 1) / HELIX_WG, (unsigned)d->n_head,
                                       (unsigned)d->n_seq, HELIX_WG, 1, 1, 0, stream, args, nullptr);
         if (e == hipSuccess && do_c) {
-            const unsigned n_wg = (unsigned)pass_c_groups(params.n_cg, params.n_seg);
+            const unsigned n_wg = (unsigned)pass_c_groups(params.n_cg, params.n_walk);
             const unsigned threads = tr.walk ? HELIX_WG * hpw : HELIX_WG;
             // With bf16 copies, Pass C reads B and C from them: dense
             // [seq][t][group][n] rows counted from the group's first token.
@@ -353,6 +365,8 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->n_groups = 1;
         out->seg_len = out->n_chunks;
         out->segs_per_group = 1;
+        out->walk_len = out->n_chunks;
+        out->walks_per_group = 1;
         out->hblk = 1;
         out->n_hblk = d->n_head / d->n_group;
         out->launches = 1;
@@ -366,6 +380,8 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->n_groups = pl.n_groups;
     out->seg_len = pl.seg_len;
     out->segs_per_group = pl.segs_per_group;
+    out->walk_len = pl.walk_len;
+    out->walks_per_group = pl.walks_per_group;
     out->hblk = pl.hblk;
     out->n_hblk = pl.n_hblk;
     out->bf16_state = tr.bf16_state ? 1 : 0;

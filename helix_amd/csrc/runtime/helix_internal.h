@@ -71,6 +71,10 @@ struct HelixMatmulTraits {
     // (HelixScanParams::fuse_b); the encoder then skips Pass B's launch
     // whenever the plan has a single group.
     bool          walk_fuse_b;
+    // Pass A is the head-block kernel (pass_a_hb.hip): a 1-D grid of
+    // HELIX_HB_THREADS-thread workgroups, one per (seq, group, item block,
+    // segment); otherwise one 256-thread workgroup per (segment, head, seq x slab).
+    bool          a_hb;
     // Pass A stores per-token decay records (HelixScanBuffers::pre) that Pass
     // C reads instead of recomputing its decay preamble: 0 none, 1 the
     // walk's form (store_decay_record), 2 the fp64 form of the fp32 path's
@@ -101,8 +105,10 @@ struct MultipassPlan {
     int    n_chunks         = 0;
     int    chunks_per_group = 0;
     int    n_groups         = 0;
-    int    seg_len          = 0;
+    int    seg_len          = 0;   // chunks per Pass A segment
     int    segs_per_group   = 0;
+    int    walk_len         = 0;   // chunks per walking Pass C segment (multiple of seg_len)
+    int    walks_per_group  = 0;
     int    hblk             = 0;
     int    n_hblk           = 0;
     size_t sl_elems         = 0;   // s_local elements (0 when seg_len == 1)

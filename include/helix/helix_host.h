@@ -43,6 +43,9 @@ typedef struct {
     const char* kernel_1pass;   /* the single-pass kernel, else NULL             */
     uint64_t bccopy_bytes;      /* bf16 copies of B and C Pass A writes for C    */
     uint64_t rec_bytes;         /* per-token decay records Pass A writes for C   */
+    int32_t  walk_len;          /* chunks per walking Pass C workgroup (a
+                                   multiple of seg_len; seg_len off the walk)    */
+    int32_t  walks_per_group;
 } helix_plan_info;
 
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */
@@ -50,7 +53,7 @@ helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
                                   helix_plan_info* out);
 
 /* Size of the fixed scratch helix_scan_encode_noalloc uses on each GPU. */
-#define HELIX_NOALLOC_SCRATCH_BYTES (64u << 20)
+#define HELIX_NOALLOC_SCRATCH_BYTES (128u << 20)
 
 /* helix_scan_encode without a scratch argument, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,

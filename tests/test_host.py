@@ -200,10 +200,10 @@ def test_16bit_storage_selection(host, io, name):
     assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_chunk_state_hb_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
     x3 = tuned(HELIX_PASSA_SPLIT="3")       # Pass A on three split products: opt-in
-    assert x3.plan_info(d).kernel_a == f"helix_chunk_state_x3agg_{name}io_n128".encode()
+    assert x3.plan_info(d).kernel_a == f"helix_chunk_state_hb_x3agg_{name}io_n128".encode()
     assert x3.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in), "
                                   f"{name} storage (d_state<=128)")
     assert k.total_bytes == host.scratch_size(d) > 0 and k.s_local_bytes == 0
@@ -246,8 +246,8 @@ def test_noalloc_host_checks(host):
     assert host.encode_noalloc(0, bad, *t) == HELIX_ERR_UNSUPPORTED_SHAPE
     assert abi.lib().helix_scan_encode_noalloc(None, None, None, *t) == HELIX_ERR_INVALID_ARG
     header = open(os.path.join(ROOT, "include", "helix", "helix_host.h")).read()
-    assert re.search(r"#define HELIX_NOALLOC_SCRATCH_BYTES \(64u << 20\)", header)
-    assert abi.NOALLOC_SCRATCH_BYTES == 64 << 20
+    assert re.search(r"#define HELIX_NOALLOC_SCRATCH_BYTES \(128u << 20\)", header)
+    assert abi.NOALLOC_SCRATCH_BYTES == 128 << 20
 
 
 def test_tuning_read_once_per_context():
@@ -293,7 +293,7 @@ def test_backend_selection(host):
     x3 = tuned(HELIX_PASSA_SPLIT="3")
     assert x3.backend_desc(mp(shape)) == ("mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in) "
                                           "(d_state<=128)")
-    assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_x3agg_bc_n128"
+    assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x3agg_bc_n128"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
@@ -301,13 +301,19 @@ def test_backend_selection(host):
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     # Pass A writes bf16 copies of B and C that the walking Pass C reads.
-    # Config 2 plans eight segments: Pass B keeps its own launch; HELIX_FUSE_B=1
-    # runs it in the walk's prologue instead.
+    # Pass B keeps its own launch: the walk's prologue scans only walk
+    # segments that are Pass A's segments too (HELIX_FUSE_B=1 with
+    # HELIX_SEG_LEN=16 runs it there).
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
-    assert k.segs_per_group == 8 and k.launches == 3
-    kf = tuned(HELIX_FUSE_B="1").plan_info(mp(shape))
-    assert kf.kernel_b is None and kf.launches == 2
+        b"helix_chunk_state_hb_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+    # Pass A (head blocks of four heads) runs 8-chunk segments, 16 per
+    # sequence; the walk runs 16-chunk ones, each starting at every other
+    # Pass A segment.
+    assert (k.seg_len, k.segs_per_group, k.walk_len, k.walks_per_group) == (8, 16, 16, 8)
+    assert k.launches == 3
+    assert tuned(HELIX_FUSE_B="1").plan_info(mp(shape)).kernel_b == b"helix_state_scan_f32"
+    kf = tuned(HELIX_FUSE_B="1", HELIX_SEG_LEN="16").plan_info(mp(shape))
+    assert kf.kernel_b is None and kf.launches == 2 and kf.seg_len == kf.walk_len == 16
     # Config 4a: one group of four segments per sequence, fused by default.
     k4 = host.plan_info(mp(CONFIG_SHAPES["cfg4a"]))
     assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2
@@ -324,10 +330,10 @@ def test_backend_selection(host):
     assert host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
     assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
     k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(shape))
-    assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_x6agg_n128", b"helix_scan_walk16_bf16_n128")
+    assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_hb_x6agg_n128", b"helix_scan_walk16_bf16_n128")
     assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
     k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
-    assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n128", b"helix_chunk_out_x6_n128")
+    assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6f32_n128", b"helix_chunk_out_x6_n128")
     k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
     # multipass=false (the descriptor default) runs the fp32 single-pass
@@ -357,17 +363,21 @@ def test_backend_selection(host):
 # ---------------------------------------------------------------------------
 
 def test_bc_copy_condition(host):
-    # The copies need the K = heads_per_group * n_pslab workgroups of a chunk
-    # to cover its 64 rows with two quads of four state indices per thread:
-    # ceil(64 / K) * d_state / 4 <= 512.
-    for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), False),
-                               ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((1, 192, 128, 1), False),
-                               ((2, 192, 128, 1), True), ((2, 64, 64, 1), True), ((1, 64, 64, 1), False)]:
+    # Up to d_state 128 the head-block Pass A writes the copies at every shape
+    # (one wave per 8-token block of a chunk and group). At d_state 256 the
+    # per-item Pass A needs the K = heads_per_group * n_pslab workgroups of a
+    # chunk to cover its 64 rows with two quads of four state indices per
+    # thread: ceil(64 / K) * d_state / 4 <= 512.
+    for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), True),
+                               ((1, 192, 128, 1), True), ((1, 64, 64, 1), True), ((1, 64, 128, 1), True),
+                               ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((2, 128, 256, 1), False),
+                               ((4, 128, 256, 1), True)]:
         d = mp((4096, 1, H, P, N, G))
         k = host.plan_info(d)
         assert (k.bccopy_bytes > 0) == copy, (H, P, N, G)
         assert k.kernel_c.endswith(b"_n%d" % k.np)
         assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
+        assert (b"_hb_" in k.kernel_a) == (N <= 128)
     # Not with 16-bit storage (Pass C reads the caller's 16-bit B and C).
     d = mp((4096, 1, 64, 64, 128, 8))
     d.io_dtype = HELIX_BF16
@@ -404,9 +414,14 @@ def test_plan_invariants(host, name, backend):
     # every region 256-byte aligned and the total covers them all
     assert info.total_bytes % 256 == 0
     assert info.total_bytes >= want_sl + info.s_seg_bytes
+    # Pass A's segments nest in the walk's; off the walk they are the same.
+    assert info.walk_len % info.seg_len == 0
+    assert info.walks_per_group == -(-info.chunks_per_group // info.walk_len)
+    assert walk or info.walk_len == info.seg_len
     # The walk runs Pass B's segment scan in its prologue when the plan has one
-    # group of at most four segments: no Pass B launch.
-    fused = walk and info.n_groups == 1 and info.segs_per_group <= 4
+    # group of at most four segments that are also its walk segments: no Pass
+    # B launch.
+    fused = walk and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
 
