@@ -32,8 +32,14 @@ HELIX_DEV int wave_id() { return threadIdx.x >> 6; }
 
 // softplus with the v > 20 shortcut the reference and ggml use
 // (reference src/kernels/helix_common.h:14-16). log1p keeps full relative
-// precision for the strongly negative dt of long-memory models.
-HELIX_DEV float helix_softplus(float v) { return v > 20.0f ? v : log1pf(expf(v)); }
+// precision for the strongly negative dt of long-memory models. Both sides are
+// formed and one selected (the log1p side on min(v, 20), so it is the same
+// value as before for every v <= 20): a branch here would split the chunk loops
+// that form the decay preamble among their MFMAs.
+HELIX_DEV float helix_softplus(float v) {
+    const float s = log1pf(expf(fminf(v, 20.0f)));
+    return v > 20.0f ? v : s;
+}
 
 HELIX_DEV float helix_dt(const HelixScanParams& p, float raw) {
     return fminf(fmaxf(helix_softplus(raw), p.dt_min), p.dt_max);

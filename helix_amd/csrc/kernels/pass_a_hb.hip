@@ -205,20 +205,23 @@ HELIX_DEV void hb_stage_run(__bf16* planes, int n, int t, const float* v) {
 // decay record for Pass C (the forms of store_decay_record / store_decay_record64).
 struct HbPre {
     float w;
-    float lend;
+    double lend;
     u32x4 rec;
 };
 
+// `shift` (<= 0) is the log-decay from the chunk's end to where the weighted
+// sum is taken (0: the chunk's end), folded into the weight.
 template <int MODE>
-__device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtraw, float A_h, int c, int lane) {
+__device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtraw, float A_h, int c, int lane,
+                                             double shift) {
     const int t0 = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const float dtv = keep_if_lt(helix_dt(p, dtraw), lane, tlen);
     const double lcum = wave_incl_sum((double)A_h * (double)dtv);
     const double lend = bcast(lcum, 63);
     HbPre r;
-    r.w = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
-    r.lend = (float)lend;
+    r.w = keep_if_lt(exp_diff(lend + shift, lcum) * dtv, lane, tlen);
+    r.lend = lend;
     if constexpr (MODE == 2) {
         const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
         const float l2 = (float)(lcum * 1.4426950408889634074);
@@ -291,19 +294,33 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     f32x16 acc[NTN];
 #pragma unroll
     for (int i = 0; i < NTN; ++i) acc[i] = zero16();
-    float lam = 0.0f;   // log-decay of this segment before chunk c
 
-    // B planes of chunk c into `planes`, and the bf16 copies of its B and C rows.
+    // Chunk order. MODE 0 walks the segment forward: R_c is the prefix of the
+    // chunks before c, and the accumulators take each chunk's decay. MODE 2
+    // walks it backward: the log-decay from a chunk's end to the segment's end
+    // (mu, the sum over the chunks already done) is known when the chunk's
+    // weights are formed and is folded into them, so the accumulators are
+    // never rescaled and end as the segment aggregate.
+    const int n_ch = c_end - c_begin;
+    auto nth = [&](int it) { return MODE == 0 ? min(c_begin + it, c_end - 1) : max(c_end - 1 - it, c_begin); };
+    float lam = 0.0f;    // MODE 0: log-decay of the segment before the current chunk
+    double mu = 0.0;     // MODE 2: log-decay from the current chunk's end to the segment's end
+    double lend = 0.0;   // L_end of the current chunk, from its preamble a step earlier
+
+    // B planes of chunk c into `planes` (state indices q4 + k, k0 <= k < k1, of
+    // this thread's rows), and the bf16 copies of its B and C rows.
     constexpr int NQ = HbRows<NP, IO>::NQ, L = HbRows<NP, IO>::L;
     const int q4 = 4 * (lane % NQ), tr = 8 * wave + L * (lane / NQ);   // this thread's state indices, tokens
-    auto stage_b = [&](const HbRows<NP, IO>& rows, int c, __bf16* planes) {
+    auto stage_planes = [&](const HbRows<NP, IO>& rows, __bf16* planes, int k0, int k1) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = k0; k < k1; ++k) {
             float v[L];
 #pragma unroll
             for (int i = 0; i < L; ++i) v[i] = hb_b<NP, IO>(rows, i, k);
             hb_stage_run<NP, NS, L>(planes, q4 + k, tr, v);
         }
+    };
+    auto copy_rows = [&](const HbRows<NP, IO>& rows, int c) {
         if constexpr (BCC) {
             const int t0 = (p.chunk_base + c) * HELIX_CS;
             const int tlen = min(HELIX_CS, p.n_tok - t0);
@@ -331,41 +348,44 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     HbRows<NP, IO> rows;
     float dtraw;   // dt of token lane of the chunk the next preamble forms
 
-    // The preamble of chunk c in the P-tile-0 wave of each item, into the
-    // chunk's weight buffer (the branch holds no vector-memory instruction),
-    // then the chunk's record and ld[c] = lam_c from every wave, cancelled by a
-    // zero range on all but the head's leader wave, and on every wave when the
-    // call only repeats the segment's last chunk (`live` false: ld[c] already
-    // holds the log-decay before it). Every vector-memory instruction of the
-    // chunk loop thus runs on every path.
-    auto preamble = [&](int c, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
-        HbPre pr{0.0f, 0.0f, u32x4{0u, 0u, 0u, 0u}};
-        if (pt == 0) {
-            pr = hb_preamble<MODE>(p, dtraw, A_h, c, lane);
-            wdst[is][lane] = pr.w;
-            if (lane == 0) wdst[is][HELIX_CS] = pr.lend;
-        }
+    // The preamble of chunk c (weights shifted by `shift`), into the chunk's
+    // weight buffer; returns its L_end. Then the chunk's record and (MODE 0)
+    // ld[c] = lam_c, cancelled by a zero range on all but the head's leader
+    // wave, and on every wave when the call only repeats the segment's last
+    // chunk (`live` false: they are already stored). Both waves of an item form
+    // it and write the same weights: the work is balanced over the SIMD's two
+    // waves and the chunk loop has no branch, so the preamble's ALU work can be
+    // scheduled among the MFMAs.
+    auto preamble = [&](int c, double shift, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
+        const HbPre pr = hb_preamble<MODE>(p, dtraw, A_h, c, lane, shift);
+        wdst[is][lane] = pr.w;
+        // The record's address is formed unconditionally (a select of two
+        // pointers becomes a branch); without records its range is zero.
         const bool rec = live && leader && b.pre != nullptr;
-        const float* recp = rec ? b.pre + (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 4) : b.s_seg;
-        __builtin_amdgcn_raw_buffer_store_b128(pr.rec, make_rsrc_u(recp, rec ? HELIX_CS * 16u : 0u), lane * 16,
-                                               0, 0);
-        const float* ldp = b.ld + seq * p.ld_seq + (long long)c * p.n_head + h;
-        __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && leader ? 4u : 0u),
-                                              lane == 0 ? 0 : (int)0x80000000, 0, 0);
+        const unsigned long long recp =
+            (unsigned long long)b.pre + (unsigned long long)((((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 16));
+        __builtin_amdgcn_raw_buffer_store_b128(pr.rec, make_rsrc_u((const void*)recp, rec ? HELIX_CS * 16u : 0u),
+                                               lane * 16, 0, 0);
+        if constexpr (MODE == 0) {
+            const float* ldp = b.ld + seq * p.ld_seq + (long long)c * p.n_head + h;
+            __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && leader ? 4u : 0u),
+                                                  lane == 0 ? 0 : (int)0x80000000, 0, 0);
+        }
+        return pr.lend;
     };
 
-    // One chunk. Its B planes are in `cur` and its weights in `wcur` (both
-    // staged a step earlier), its x in xs; `rows` holds chunk c + 1's B (and C)
-    // rows and dtraw chunk c + 1's dt. Every memory instruction runs on every
-    // path; past the segment's last chunk the loads and the staging repeat
-    // that chunk (nothing reads the result). The loop is not unrolled: the
-    // loop-carried registers then keep one assignment, with no copies at the
-    // back edge.
-    auto step = [&](int c, const __bf16* cur, __bf16* nxt, float (*wcur)[HELIX_CS + 4],
+    // Chunk nth(it). Its B planes are in `cur` and its weights in `wcur` (both
+    // staged a step earlier), its x in xs; `rows` holds the B (and C) rows and
+    // dtraw the dt of the chunk after it, cn. Every memory instruction runs on
+    // every path; past the segment's last chunk the loads and the staging
+    // repeat that chunk (nothing reads the result). The loop is not unrolled:
+    // the loop-carried registers then keep one assignment, with no copies at
+    // the back edge.
+    auto step = [&](int it, const __bf16* cur, __bf16* nxt, float (*wcur)[HELIX_CS + 4],
                     float (*wnxt)[HELIX_CS + 4]) {
-        const int cn = min(c + 1, c_end - 1);
+        const int c = nth(it), cn = nth(it + 1);
         const float* __restrict__ wrow = wcur[is];
-        const float lendf = wrow[HELIX_CS];
+        const float lendf = (float)lend;
         if constexpr (MODE == 0) {
             // R_c, the state entering chunk c from this segment's own chunks
             // (none for its first chunk: a zero range stores nothing).
@@ -379,9 +399,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                     buf_store_unit<float>(rd, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2],
                                           acc[i][4 * r4 + 3], lane, tile_unit(NTN, pt, i, r4, 0));
         }
-        const float a_c = expf(lendf);
-#pragma unroll
-        for (int i = 0; i < NTN; ++i) acc[i] *= a_c;
+        const float a_c = MODE == 0 ? expf(lendf) : 1.0f;
 
         // R[n][p] += sum_j B^T[n][j] (w_j x[j][p]) over four K steps of 16 tokens,
         // in groups of two n tiles. The B planes of the next group and the
@@ -421,6 +439,12 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         f32x4 w0, w1;
         read_group(0, 0, bq[0]);
         read_w(0, w0, w1);
+        // MODE 0: the decay of the state carried in, on each group's
+        // accumulators just before their first products of the chunk.
+        if constexpr (MODE == 0) {
+            acc[0] *= a_c;
+            acc[1] *= a_c;
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             float v[8];
@@ -448,6 +472,21 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
             // it has a whole chunk step to arrive.
             vmem_fence();
             hb_load_xs<IO>(xs.v[s], p, x_w, cn, s, lane, pt, pw);
+            // The next chunk's preamble (K step 1) and B planes and copies
+            // (K steps 2 and 3): ALU and LDS work with no dependence on this
+            // chunk's products, written among them so it overlaps the MFMAs.
+            if (s == 1) {
+                if constexpr (MODE == 0) {
+                    lam += lendf;
+                    lend = preamble(cn, 0.0, lam, wnxt, it + 1 < n_ch);
+                } else {
+                    mu += lend;
+                    lend = preamble(cn, mu, 0.0f, wnxt, it + 1 < n_ch);
+                }
+            }
+            vmem_fence();
+            if (s >= 2) stage_planes(rows, nxt, 2 * (s - 2), 2 * (s - 2) + 2);
+            if (s == 3) copy_rows(rows, cn);
             vmem_fence();
 #pragma unroll
             for (int gi = 0; gi < NG; ++gi) {
@@ -455,34 +494,38 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 const int s_n = gi + 1 < NG ? s : s + 1;  // the next group's K step
                 const int g_n = gi + 1 < NG ? gi + 1 : 0;
                 if (s_n < 4) read_group(s_n, 2 * g_n, bq[q ^ 1]);
+                if (MODE == 0 && s == 0 && gi > 0) {
+                    acc[2 * gi] *= a_c;
+                    acc[2 * gi + 1] *= a_c;
+                }
                 mfma_group(2 * gi, bq[q], xp);
             }
         }
-        // The next chunk's weights and B planes, then its successor's rows and dt.
-        lam += lendf;
-        preamble(cn, lam, wnxt, c + 1 < c_end);
-        stage_b(rows, cn, nxt);
+        // The rows and dt of the chunk after cn.
         vmem_fence();
-        hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, min(c + 2, c_end - 1), lane, wave, N, copier);
-        dtraw = hb_load_dt(p, dt_h, min(c + 2, c_end - 1), lane);
+        const int cnn = nth(it + 2);
+        hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, cnn, lane, wave, N, copier);
+        dtraw = hb_load_dt(p, dt_h, cnn, lane);
         __syncthreads();
     };
 
-    // Prologue: chunk c_begin's weights and B planes in buffer 0, its x in
-    // flight, chunk c_begin + 1's rows and dt in flight.
-    dtraw = hb_load_dt(p, dt_h, c_begin, lane);
-    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c_begin, lane, wave, N, copier);
+    // Prologue: the first chunk's weights and B planes in buffer 0, its x in
+    // flight, the second chunk's rows and dt in flight.
+    const int c0 = nth(0), c1 = nth(1);
+    dtraw = hb_load_dt(p, dt_h, c0, lane);
+    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c0, lane, wave, N, copier);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) hb_load_xs<IO>(xs.v[s], p, x_w, c_begin, s, lane, pt, pw);
-    preamble(c_begin, 0.0f, sW[0], true);
-    stage_b(rows, c_begin, sB);
-    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, min(c_begin + 1, c_end - 1), lane, wave, N, copier);
-    dtraw = hb_load_dt(p, dt_h, min(c_begin + 1, c_end - 1), lane);
+    for (int s = 0; s < 4; ++s) hb_load_xs<IO>(xs.v[s], p, x_w, c0, s, lane, pt, pw);
+    lend = preamble(c0, 0.0, 0.0f, sW[0], true);
+    stage_planes(rows, sB, 0, 4);
+    copy_rows(rows, c0);
+    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c1, lane, wave, N, copier);
+    dtraw = hb_load_dt(p, dt_h, c1, lane);
     __syncthreads();
 #pragma unroll 1
-    for (int c = c_begin; c < c_end; ++c) {
-        const int par = (c - c_begin) & 1;
-        step(c, sB + par * PLANES, sB + (PLANES - par * PLANES), sW[par], sW[par ^ 1]);
+    for (int it = 0; it < n_ch; ++it) {
+        const int par = it & 1;
+        step(it, sB + par * PLANES, sB + (PLANES - par * PLANES), sW[par], sW[par ^ 1]);
     }
 
     // Segment aggregate D_s and the segment's log-decay.
@@ -496,7 +539,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 buf_store_unit<float>(rs, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2], acc[i][4 * r4 + 3],
                                       lane, tile_unit(NTN, pt, i, r4, 0));
     }
-    if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
+    if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = MODE == 0 ? lam : (float)mu;
 }
 
 #define HELIX_PASS_A_HB(NP)                                                                           \
