@@ -9,17 +9,21 @@
 // so this walk is seg_len times shorter than the reference's. One thread per
 // tile unit (four consecutive n of one p, helix_params.h layout) of one
 // (seq, head): every segment row moves as 16-byte lane accesses, 1 KiB
-// contiguous per wave. The D loads of a block of segments are issued before
-// the dependent FMA chain so the loads overlap.
+// contiguous per wave. The D loads of a block of up to 16 segments are all
+// issued before the dependent FMA chain, so a thread waits on memory once per
+// block.
 //
 //   carry = s0[ids[seq]] (first group) or s1[seq] (later groups)
-//   for s: S_seg(s) = carry (in place over D_s); carry = exp(segld_s) carry + D_s
+//   for s: S_seg(s) = carry (in place over D_s) if s starts a walk;
+//          carry = exp(segld_s) carry + D_s
 //   s1[seq] = carry
+// Pass C starts a walk every walk_len / seg_len segments and reads the start
+// states of those segments only; the others are not stored.
 #include "helix_common.h"
 
 extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(HelixScanParams p,
                                                                            HelixScanBuffers b) {
-    constexpr int BLK = 8;
+    constexpr int BLK = 16;
     const int units_tile = 16 * p.np;                    // 64 * np / 4
     const int per_head = p.n_pslab * units_tile;
     const int u   = blockIdx.x * HELIX_WG + threadIdx.x; // unit within (seq, head)
@@ -52,6 +56,7 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
         reinterpret_cast<f32x4*>(b.s_seg + seq * p.sg_seq + (long long)h * per_head * 4) + u;
     const long long seg_stride = p.sg_seg / 4;           // in units
     const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
+    const int ratio = p.walk_len / p.seg_len;            // segments per walk
 
     for (int s0 = 0; s0 < p.n_seg; s0 += BLK) {
         const int nb = min(BLK, p.n_seg - s0);
@@ -67,7 +72,7 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
 #pragma unroll
         for (int k = 0; k < BLK; ++k) {
             if (k < nb) {
-                base[(long long)(s0 + k) * seg_stride] = carry;
+                if ((s0 + k) % ratio == 0) base[(long long)(s0 + k) * seg_stride] = carry;
                 carry = a[k] * carry + d[k];
             }
         }
