@@ -309,21 +309,42 @@ HELIX_DEV unsigned pk_bf16(float a, float b) {
 HELIX_DEV float pk_lo(unsigned w) { return __builtin_bit_cast(float, w << 16); }
 HELIX_DEV float pk_hi(unsigned w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
+// a - lo(w) and a - hi(w) for a packed bf16 pair w, each one v_dot2_f32_bf16:
+// w . (-1, 0) + a. Where w is a's own bf16 rounding (or that of a residual of
+// it) the difference is exactly representable in fp32, and the bf16 products
+// are exact, so the result is exact: the same value as unpacking the half and
+// subtracting, in one operation instead of two. The (-1, 0) and (0, -1) pairs
+// reach the instruction in a scalar register: the compiler would otherwise
+// encode the first as the inline constant -1.0, which the hardware applies as
+// the fp32 bit pattern 0xbf800000, i.e. the pair (0, -1) (measured).
+HELIX_DEV unsigned bf16_pair_reg(unsigned k) {
+    asm("" : "+s"(k));
+    return k;
+}
+HELIX_DEV float sub_lo(float a, unsigned w) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                           __builtin_bit_cast(bf16x2, bf16_pair_reg(0x0000bf80u)), a, false);
+}
+HELIX_DEV float sub_hi(float a, unsigned w) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                           __builtin_bit_cast(bf16x2, bf16_pair_reg(0xbf800000u)), a, false);
+}
+
 // Three-way bf16 split of the pair (a, b), each part packed as a pair:
-// 11 VALU operations for two values.
+// 7 VALU operations for two values.
 HELIX_DEV void split3_pair(float a, float b, unsigned& w0, unsigned& w1, unsigned& w2) {
     w0 = pk_bf16(a, b);
-    const float ra = a - pk_lo(w0), rb = b - pk_hi(w0);
+    const float ra = sub_lo(a, w0), rb = sub_hi(b, w0);
     w1 = pk_bf16(ra, rb);
-    w2 = pk_bf16(ra - pk_lo(w1), rb - pk_hi(w1));
+    w2 = pk_bf16(sub_lo(ra, w1), sub_hi(rb, w1));
 }
 
 // Two-way bf16 split of the pair (a, b): v = v0 + v1 + e with |e| <= 2^-18 |v|,
-// 6 VALU operations for two values. Three products a0b0 + a0b1 + a1b0 leave
+// 4 VALU operations for two values. Three products a0b0 + a0b1 + a1b0 leave
 // out terms of at most 3 * 2^-18 of |ab| (about 1.1e-5).
 HELIX_DEV void split2_pair(float a, float b, unsigned& w0, unsigned& w1) {
     w0 = pk_bf16(a, b);
-    w1 = pk_bf16(a - pk_lo(w0), b - pk_hi(w0));
+    w1 = pk_bf16(sub_lo(a, w0), sub_hi(b, w0));
 }
 
 // Six-product MFMA of split operands a[3] x b[3], smallest terms first.

@@ -29,8 +29,8 @@
 //     gfx950 the vmcnt counter counts stores too, and a store on one path only
 //     would make the compiler's waits cover the next chunk's loads.
 //   - The bf16 copies of B and C for the walking Pass C are written by one
-//     wave per 8-token block per group: wave w of item block ib copies its
-//     block when ib == w % (item blocks per group).
+//     wave per block of its rows per group: wave w of item block ib copies
+//     its block when ib == w % (item blocks per group).
 // Grid: one workgroup per (seq, B/C group, item block, segment), 1-D and
 // decoded XCD-aware so a segment's item blocks (which read the same B rows)
 // run on one XCD.
@@ -44,19 +44,37 @@ struct HbX {
 };
 
 // This thread's share of a chunk's B rows, and of its C rows for the copies:
-// lane (q, r) = (lane % NQ, lane / NQ), NQ = NP / 4 quads of four state
-// indices per row, holds state indices 4 q .. 4 q + 3 of the L = 8 / (64 / NQ)
-// consecutive tokens 8 wave + L r + i, one 16-byte run (8 bytes in 16-bit
-// storage) per token. Few, wide loads: a chunk step stays under the vmcnt
-// counter's 63 outstanding operations.
+// state indices n .. n + 3 (a quad) of the L consecutive tokens t .. t + L - 1,
+// one 16-byte run (8 bytes in 16-bit storage) per token, (n, t) = hb_rows_at.
+// Few, wide loads: a chunk step stays under the vmcnt counter's 63
+// outstanding operations.
 template <int NP, typename IO>
 struct HbRows {
-    static constexpr int NQ = NP / 4;                       // quads per row
-    static constexpr int L = 8 * NQ / 64;                   // tokens per lane (4 at NP 128, 2 at 64)
+    static constexpr int L = NP / 32;                       // tokens per lane (4 at NP 128, 2 at 64)
     static constexpr int W = sizeof(IO) == 4 ? 4 : 2;       // 32-bit words per run
     unsigned b[L][W];
     unsigned c[L][4];
 };
+
+// The first state index and token of this thread's rows. NP 128: wave w owns
+// tokens 16 (w % 4) .. + 15 and state indices 64 (w / 4) .. + 63; lane bits
+// (1:0) and (5:4) pick the quad, bits (3:2) the run of four tokens. A load
+// instruction then reads four rows of 256 contiguous bytes, and the staging
+// writes of 16 consecutive lanes (four tokens of one state index each, at
+// dword 36 n + t / 2 of the plane) cover the 16 bank pairs 16 (q % 4) + 2 r:
+// no bank conflicts. NP 64: wave w owns tokens 8 w .. 8 w + 7, lane (q, r) =
+// (lane % 16, lane / 16) quad q of tokens 8 w + 2 r.
+template <int NP>
+HELIX_DEV void hb_rows_at(int lane, int wave, int& n, int& t) {
+    if constexpr (NP == 128) {
+        const int q = (lane & 3) | ((lane >> 4) << 2);
+        n = 64 * (wave >> 2) + 4 * q;
+        t = 16 * (wave & 3) + 4 * ((lane >> 2) & 3);
+    } else {
+        n = 4 * (lane & 15);
+        t = 8 * wave + 2 * (lane >> 4);
+    }
+}
 
 template <typename IO>
 HELIX_DEV typename IoWord<IO>::type io_load_at(helix_rsrc r, int voff_bytes, int soff_bytes) {
@@ -115,14 +133,14 @@ __device__ __forceinline__ void hb_load_rows(HbRows<NP, IO>& st, const HelixScan
                                              const IO* __restrict__ B_g, const float* __restrict__ C_g, int c,
                                              int lane, int wave, int N, bool copier) {
     constexpr int ES = (int)sizeof(IO);
-    constexpr int NQ = HbRows<NP, IO>::NQ, L = HbRows<NP, IO>::L;
+    constexpr int L = HbRows<NP, IO>::L;
     const int t0 = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sb0 = sgpr_fresh((int)p.s_b[0]);
     const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
-    const int q = lane % NQ, r = lane / NQ;
-    const int n0 = min(4 * q, N - 4);
-    const int j0 = 8 * wave + L * r;
+    int nq, j0;
+    hb_rows_at<NP>(lane, wave, nq, j0);
+    const int n0 = min(nq, N - 4);
 #pragma unroll
     for (int i = 0; i < L; ++i) {
         const int jr = min(j0 + i, tlen - 1);
@@ -309,8 +327,9 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
 
     // B planes of chunk c into `planes` (state indices q4 + k, k0 <= k < k1, of
     // this thread's rows), and the bf16 copies of its B and C rows.
-    constexpr int NQ = HbRows<NP, IO>::NQ, L = HbRows<NP, IO>::L;
-    const int q4 = 4 * (lane % NQ), tr = 8 * wave + L * (lane / NQ);   // this thread's state indices, tokens
+    constexpr int L = HbRows<NP, IO>::L;
+    int q4, tr;   // this thread's first state index and token
+    hb_rows_at<NP>(lane, wave, q4, tr);
     auto stage_planes = [&](const HbRows<NP, IO>& rows, __bf16* planes, int k0, int k1) {
 #pragma unroll
         for (int k = k0; k < k1; ++k) {
