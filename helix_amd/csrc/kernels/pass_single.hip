@@ -2,8 +2,8 @@
 // scratch.
 //
 // Reference counterpart: helix_scan_sgmma_f32 (src/kernels/
-// helix_scan_sgmma.metal:32-249). One workgroup per (P slab, head, seq) walks
-// every chunk of the sequence in order:
+// helix_scan_sgmma.metal:32-249). One workgroup per (16-channel block, head,
+// seq) walks every chunk of the sequence in order:
 //   y_t = sum_{j<=t} (C_t . B_j) exp(Lcum_t - Lcum_j) dt_j x_j     (G1, G2)
 //       + exp(Lcum_t) C_t . S                                     (G3)
 //   S  <- exp(L_end) S + sum_j B_j^T exp(L_end - Lcum_j) dt_j x_j   (G4)
@@ -12,23 +12,26 @@
 // registers for the whole sequence: s0 is read once at the start and s1
 // written once at the end.
 //
-// MI355X layout: four waves on v_mfma_f32_16x16x4_f32, fp32 throughout.
-// Wave w owns the 16 channels p = 16w .. 16w+15 of the slab and every state
-// index n, so the y tile it produces (all 64 tokens of its channels) and the
-// state it advances are both its own: G3 takes its B operand straight from
-// the state registers, with no cross-wave reduction.
+// MI355X layout: one workgroup of four waves per (seq, head, 16-channel
+// block of a P slab), on v_mfma_f32_16x16x4_f32, fp32 throughout. Four
+// blocks per slab give four times the workgroups of a slab-wide walk (256 at
+// 64 heads), so a single sequence fills the chip. Wave w produces y's t block
+// w (all 16 channels) and advances state tiles NT/4 w .. NT/4 (w + 1) - 1 (all
+// channels); the state is shared through LDS (sR, 16 x d_state fp32) once per
+// chunk, for every wave's G3. G1 (C B^T, shared by the block's channels) is
+// split over the waves by tile.
 //   16x16x4 layouts: A[i][k]: lane holds A[lane%16][lane/16];
 //                    B[k][j]: lane holds B[lane/16][lane%16];
 //                    D[i][j]: lane, reg r holds D[4*(lane/16) + r][lane%16].
 // The state tile nt is R[n][p] for n = 16 nt .. 16 nt + 15 (M = n, N = p).
 // K order: G1 and G3 step s of a 16-wide K block takes k = 4*(lane/16) + s,
-// so the A operand's four k of a block are one 16-byte LDS read and G3's B
-// operand at step s is state register s; G2 and G4 take token j = 4 s +
-// lane/16. Both operands of a product use the same order.
+// so the A operand's four k of a block are one 16-byte LDS read, and so are
+// G3's four state values (sR row p); G2 and G4 take token j = 4 s + lane/16.
+// Both operands of a product use the same order.
 //
-// LDS: C and B rows (fp32, 64 x (np+4)), dtX (64 x 80), the chunk's Lcum in
-// fp64 and two 64-vectors: 151 KiB at d_state 256. M reuses B's rows once
-// G1 and G4 are done with them.
+// LDS: C and B rows (fp32, 64 x (np+4)), dtX (64 x 16), the state (16 x
+// (np+4)), the chunk's Lcum in fp64 and two 64-vectors: 150 KiB at d_state
+// 256. M reuses B's rows once G1 and G4 are done with them.
 #include "helix_common.h"
 
 #include "pass_c_stage.h"
@@ -43,14 +46,15 @@ HELIX_DEV f32x4 zero4() {
 }
 
 // One chunk's global inputs for this thread, loaded for chunk c+1 while chunk
-// c runs: dt of token `lane`, x of tokens 16 w + i at channel `lane`, and the
-// C and B rows wave + 4 i at columns lane + 64 m. Every address is clamped in
-// bounds; the masks are applied when the registers are staged into LDS.
+// c runs: dt of token `lane`, x of tokens tid / 16 + 16 i at channel tid % 16
+// of the block, and the C and B rows wave + 4 i at columns lane + 64 m. Every
+// address is clamped in bounds; the masks are applied when the registers are
+// staged into LDS.
 template <int NP, typename IO>
 struct StageS {
     typedef typename IoWord<IO>::type W;    // x, C, B in storage form
     float dtraw;
-    W x[16];
+    W x[4];
     W c[16][NP / 64];
     W b[16][NP / 64];
 };
@@ -65,10 +69,11 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScan
     const helix_rsrc rx = make_rsrc(x_h + (long long)t0 * p.s_x[0],
                                     ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
     st.dtraw = buf_elem<float>(rdt, min(lane, tlen - 1) * sdt, 0);
-    const int xc = min(lane, pw - 1) * sx2;
+    const int tid = 64 * wave + lane;
+    const int xc = min(tid & 15, pw - 1) * sx2;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int jr = min(16 * wave + i, tlen - 1);
+    for (int i = 0; i < 4; ++i) {
+        const int jr = min((tid >> 4) + 16 * i, tlen - 1);
         st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
     }
     load_cb_rows<NP, IO>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
@@ -92,14 +97,16 @@ HELIX_DEV int tri_jb(int idx) {
 // IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
 template <int NP, bool DIAG, typename IO = float>
 __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
-    constexpr int NT  = NP / 16;           // 16-row state tiles (all of them live in every wave)
+    constexpr int NT  = NP / 16;           // 16-row state tiles
+    constexpr int NTW = NT / 4;            // state tiles wave w advances: NTW w .. NTW w + NTW - 1
     constexpr int RSC = NP + 4;            // C and B rows
     constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
-    constexpr int RSX = HELIX_HD + 16;     // dtX rows
+    constexpr int RSR = NP + 4;            // state rows, one per channel of the block
     static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
     __shared__ __attribute__((aligned(16))) float sC[HELIX_CS * RSC];
     __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSC];
-    __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * RSX];
+    __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * 16];   // dtX[token][channel]
+    __shared__ __attribute__((aligned(16))) float sR[16 * RSR];        // S[channel][state index]
     __shared__ double sL[HELIX_CS];        // Lcum_t (scalar A) or cs_t (DIAG), fp64
     __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
     __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
@@ -109,23 +116,27 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
     const int lane = threadIdx.x & 63, wave = wave_uniform();
     const int l16 = lane & 15, g4 = lane >> 4;
+    const int tid = (int)threadIdx.x;
 
-    // 1-D grid, slab then head fastest in the logical order, so the heads of
-    // one B/C group (consecutive heads) share an XCD's L2.
-    const unsigned total = (unsigned)p.n_seq * (unsigned)p.n_head * (unsigned)p.n_pslab;
-    const unsigned wid = xcd_logical_id(blockIdx.x, total);
-    const int slab = (int)(wid % (unsigned)p.n_pslab);
-    const int h    = (int)((wid / (unsigned)p.n_pslab) % (unsigned)p.n_head);
-    const int seq  = (int)(wid / ((unsigned)p.n_pslab * (unsigned)p.n_head));
+    // 1-D grid over (seq, head, P slab, 16-channel block), block fastest in
+    // the logical order, so a head's blocks and a group's heads (which read
+    // the same B and C rows) run on one XCD.
+    const unsigned total = (unsigned)p.n_seq * (unsigned)p.n_head * (unsigned)p.n_pslab * 4u;
+    unsigned wid = xcd_logical_id(blockIdx.x, total);
+    const int pb   = (int)(wid % 4u);                wid /= 4u;
+    const int slab = (int)(wid % (unsigned)p.n_pslab); wid /= (unsigned)p.n_pslab;
+    const int h    = (int)(wid % (unsigned)p.n_head);
+    const int seq  = (int)(wid / (unsigned)p.n_head);
     const int g  = h / p.heads_per_group;
     const int N  = p.d_state;
-    const int p0 = slab * HELIX_HD;
-    const int pw = min(HELIX_HD, p.head_dim - p0);
-    const int pc = 16 * wave + l16;       // this lane's channel in the slab (result column)
+    const int p0 = slab * HELIX_HD + 16 * pb;          // the block's first channel
+    const int pw = min(16, p.head_dim - p0);           // its channels
+    if (pw <= 0) return;   // a block past a short last slab: uniform, before any barrier
+    const int tb = wave;   // the t block of y this wave produces
 
     const float A_h = DIAG ? 0.0f : b.A[(long long)h * p.s_a];
     if constexpr (DIAG) {
-        for (int n = threadIdx.x; n < NP; n += HELIX_WG)
+        for (int n = tid; n < NP; n += HELIX_WG)
             sA2[n] = n < N ? (double)b.A[(long long)h * p.s_a + n] * 1.4426950408889634074 : 0.0;
     }
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
@@ -133,22 +144,30 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                                  (long long)p0 * p.s_x[2];
 
     // State entering the sequence, s0[ids[seq]] in the caller's [P][N] rows
-    // (s_s[1] == d_state): register r of tile nt holds n = 16 nt + 4 g4 + r,
-    // p = pc. Channels past the slab read 0 through the range check; n past
-    // d_state is masked (it would read the next row).
+    // (s_s[1] == d_state): register r of tile i holds n = 16 (NTW wave + i) +
+    // 4 g4 + r at channel p0 + l16. Channels past the block read 0 through the
+    // range check; n past d_state is masked (it would read the next row).
     const int src = p.has_ids ? b.ids[seq] : seq;
-    f32x4 R[NT];
+    f32x4 R[NTW];
     {
         const helix_rsrc rs = make_rsrc(b.s0 + src * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
                                         (unsigned)(pw * N) * 4u);
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+        for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int n = 16 * nt + 4 * g4 + r;
-                R[nt][r] = keep_if_lt(buf_f32(rs, (pc * N + n) * 4, 0), n, N);
+                const int n = 16 * (NTW * wave + i) + 4 * g4 + r;
+                R[i][r] = keep_if_lt(buf_f32(rs, (l16 * N + n) * 4, 0), n, N);
             }
     }
+    // Every wave's G3 reads the whole state: it is shared through sR, written
+    // by the wave that advances each tile.
+    auto publish_state = [&]() {
+#pragma unroll
+        for (int i = 0; i < NTW; ++i)
+            *reinterpret_cast<f32x4*>(&sR[l16 * RSR + 16 * (NTW * wave + i) + 4 * g4]) = R[i];
+    };
+    publish_state();
 
     const int n_ch = (p.n_tok + HELIX_CS - 1) / HELIX_CS;
     const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
@@ -173,9 +192,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int j = 16 * wave + i;
-            sX[j * RSX + lane] = keep_if_lt(bcast(dtv, j) * io_widen<IO>(st.x[i]), lane, pw);
+        for (int i = 0; i < 4; ++i) {
+            const int j = (tid >> 4) + 16 * i;
+            sX[j * 16 + (tid & 15)] = keep_if_lt(__shfl(dtv, j, 64) * io_widen<IO>(st.x[i]), tid & 15, pw);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -200,7 +219,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const int j = 4 * s + g4;
-            xb[s] = sX[j * RSX + pc];
+            xb[s] = sX[j * 16 + l16];
             xs[s] = DIAG ? xb[s] : xb[s] * sCs[j];
         }
 
@@ -212,7 +231,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             // Past d_state C and B are zero, so n runs to d_state only. Each
             // exponent is formed in fp64 and rounded once, as the scalar
             // path's exp(Lcum_t - Lcum_j) is.
-            const int t = threadIdx.x >> 2, q = threadIdx.x & 3;
+            const int t = tid >> 2, q = tid & 3;
             const double ct = sL[t];
             double dcs[16];
             float acc[16];
@@ -242,7 +261,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             // C rows by exp(A_n cs_t), B rows by exp(A_n (cs_end - cs_j)).
 #pragma unroll 4
             for (int i = 0; i < HELIX_CS * NP / HELIX_WG; ++i) {
-                const int idx = (int)threadIdx.x + HELIX_WG * i;
+                const int idx = tid + HELIX_WG * i;
                 const int row = idx / NP, n = idx % NP;
                 const double cr = sL[row];
                 const double a = sA2[n];
@@ -256,11 +275,11 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             mt[q] = zero4();
             const int idx = wave + 4 * q;
             if (!DIAG && idx < 10) {
-                const int tb = tri_tb(idx), jb = tri_jb(idx);
+                const int gtb = tri_tb(idx), jb = tri_jb(idx);
                 f32x4 acc = zero4();
 #pragma unroll 4
                 for (int kb = 0; kb < NP / 16; ++kb) {
-                    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * kb + 4 * g4]);
+                    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * gtb + l16) * RSC + 16 * kb + 4 * g4]);
                     const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sB[(16 * jb + l16) * RSC + 16 * kb + 4 * g4]);
 #pragma unroll
                     for (int s = 0; s < 4; ++s) acc = mfma16(a4[s], b4[s], acc);
@@ -269,7 +288,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 const double lj = sL[j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int t = 16 * tb + 4 * g4 + r;
+                    const int t = 16 * gtb + 4 * g4 + r;
                     // j > t: exp of a positive difference may overflow; the
                     // bitwise mask clears the product whatever it is.
                     mt[q][r] = keep_if_le(acc[r] * exp_diff(sL[t], lj), j, t);
@@ -277,66 +296,59 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
 
-        // ---- G3: y = exp(Lcum_t) . (C S), S from this wave's registers ------
-        f32x4 ya[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) ya[tb] = zero4();
+        // ---- G3: y = exp(Lcum_t) . (C S) for this wave's t block; S from sR --
+        f32x4 ya = zero4();
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
+            const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * nt + 4 * g4]);
+            const f32x4 r4 = *reinterpret_cast<const f32x4*>(&sR[l16 * RSR + 16 * nt + 4 * g4]);
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * nt + 4 * g4]);
-#pragma unroll
-                for (int s = 0; s < 4; ++s) ya[tb] = mfma16(a4[s], R[nt][s], ya[tb]);
-            }
+            for (int s = 0; s < 4; ++s) ya = mfma16(a4[s], r4[s], ya);
         }
         if constexpr (!DIAG) {
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) ya[tb][r] *= sE[16 * tb + 4 * g4 + r];
+            for (int r = 0; r < 4; ++r) ya[r] *= sE[16 * tb + 4 * g4 + r];
         }
 
-        // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x) -------------
+        // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x), own tiles --
         if constexpr (DIAG) {
-            // Per state index: register r of tile nt holds n = 16 nt + 4 g4 + r.
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int i = 0; i < NTW; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    R[nt][r] *= __builtin_amdgcn_exp2f((float)(sA2[16 * nt + 4 * g4 + r] * lend));
+                    R[i][r] *= __builtin_amdgcn_exp2f((float)(sA2[16 * (NTW * wave + i) + 4 * g4 + r] * lend));
         } else {
             const float a_c = expf((float)lend);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) R[nt] *= a_c;
+            for (int i = 0; i < NTW; ++i) R[i] *= a_c;
         }
 #pragma unroll 4
         for (int s = 0; s < 16; ++s) {
             const int j = 4 * s + g4;
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) R[nt] = mfma16(sB[j * RSC + 16 * nt + l16], xs[s], R[nt]);
+            for (int i = 0; i < NTW; ++i)
+                R[i] = mfma16(sB[j * RSC + 16 * (NTW * wave + i) + l16], xs[s], R[i]);
         }
+        // Every wave is done with the B rows and with sR: M takes over B's
+        // rows, and the advanced state replaces the old one.
+        __syncthreads();
         if constexpr (!DIAG) {
-            __syncthreads();   // every wave is done with the B rows: M takes them over
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
                 const int idx = wave + 4 * q;
                 if (idx < 10) {
-                    const int tb = tri_tb(idx), jb = tri_jb(idx);
+                    const int gtb = tri_tb(idx), jb = tri_jb(idx);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) sM[(16 * tb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
+                    for (int r = 0; r < 4; ++r) sM[(16 * gtb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
                 }
             }
-            __syncthreads();
         }
+        publish_state();
+        __syncthreads();
 
-        // ---- G2: y += M dtX over the causal K range of each t block ---------
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-#pragma unroll
-            for (int s = 0; s < 4 * (tb + 1); ++s)
-                ya[tb] = mfma16(sM[(16 * tb + l16) * RSM + 4 * s + g4], xb[s], ya[tb]);
-        }
+        // ---- G2: y += M dtX over the causal K range of this t block --------
+        for (int s = 0; s < 4 * (tb + 1); ++s)
+            ya = mfma16(sM[(16 * tb + l16) * RSM + 4 * s + g4], xb[s], ya);
 
         // ---- y rows t < tlen, channels < pw ---------------------------------
         {
@@ -346,13 +358,10 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                                                 (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                             bytes);
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = 16 * tb + 4 * g4 + r;
-                    const float v = ya[tb][r];
-                    io_store<IO, HELIX_NT>(ry, v, store_off_if_lt((t * sy0 + pc * sy2) * ES, t, tlen, pc, pw), 0);
-                }
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tb + 4 * g4 + r;
+                io_store<IO, HELIX_NT>(ry, ya[r], store_off_if_lt((t * sy0 + l16 * sy2) * ES, t, tlen, l16, pw), 0);
+            }
         }
         __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX
     }
@@ -360,13 +369,12 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     // Final state to s1[seq], same register layout as the s0 read.
     const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * N, (unsigned)(pw * N) * 4u);
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int i = 0; i < NTW; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int n = 16 * nt + 4 * g4 + r;
-            const float v = R[nt][r];
-            __builtin_amdgcn_raw_buffer_store_b32(as_u32(v), ro, store_off_if_lt((pc * N + n) * 4, n, N, pc, pw),
-                                                  0, 0);
+            const int n = 16 * (NTW * wave + i) + 4 * g4 + r;
+            __builtin_amdgcn_raw_buffer_store_b32(as_u32(R[i][r]), ro,
+                                                  store_off_if_lt((l16 * N + n) * 4, n, N, l16, pw), 0, 0);
         }
 }
 

@@ -85,7 +85,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     };
 
     // Single pass (reference dispatch.mm:122-138): one launch, one workgroup
-    // per (seq, head, P slab), the state carried in registers; no scratch.
+    // per (seq, head, 16-channel block of a P slab), the state carried in
+    // registers; no scratch.
     // Diagonal A always takes this path.
     if (tr.k_single) {
         hipFunction_t f1 = fn(tr.k_single);
@@ -93,9 +94,9 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             set_error(ctx, "kernel not resolved in code object");
             return HELIX_ERR_PIPELINE;
         }
-        const long long n_wg = (long long)d->n_seq * d->n_head * params.n_pslab;
+        const long long n_wg = (long long)d->n_seq * d->n_head * params.n_pslab * 4;
         if (n_wg > 0xffffffffLL) {
-            set_error(ctx, "launch grid exceeds 2^32 workgroups (n_seq * n_head * n_pslab)");
+            set_error(ctx, "launch grid exceeds 2^32 workgroups (n_seq * n_head * n_pslab * 4)");
             return HELIX_ERR_INVALID_ARG;
         }
         params.np = tr.np;
