@@ -164,6 +164,45 @@ def time_passes(v: Variant, steps: int, stream):
     return {k: [step[i][0].elapsed_time(step[i][1]) for step in evs] for i, k in enumerate("ABCX")}
 
 
+def time_in_scan(v: Variant, steps: int, stream):
+    """Each pass's time inside whole scans (ms per step): every step encodes
+    the whole scan and then the scan without one pass (HELIX_ONLY_PASS=BC, AC,
+    AB), each between two events, and a pass's time is the difference of the
+    two means. Unlike the single-pass split this keeps each pass in the cache
+    state the scan leaves it (what rocprofv3's kernel trace of the same run
+    averages, since whole scans dominate its calls); it includes the pass's
+    launch gap."""
+    drop = {"A": "BC", "B": "AC", "C": "AB"}
+    live = [k for k in "ABC" if k != "B" or v.plan.kernel_b]
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(2)]
+           for _ in range(steps * len(live))]
+    try:
+        torch.cuda.synchronize()
+        i = 0
+        for _ in range(steps):
+            for k in live:
+                for j, only in enumerate((None, drop[k])):
+                    if only:
+                        os.environ["HELIX_ONLY_PASS"] = only
+                    else:
+                        os.environ.pop("HELIX_ONLY_PASS", None)
+                    a, b = evs[i][j]
+                    a.record(stream)
+                    v.encode(stream)
+                    b.record(stream)
+                i += 1
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("HELIX_ONLY_PASS", None)
+    out = {}
+    for n, k in enumerate(live):
+        pairs = evs[n::len(live)]
+        full = statistics.fmean(p[0][0].elapsed_time(p[0][1]) for p in pairs)
+        part = statistics.fmean(p[1][0].elapsed_time(p[1][1]) for p in pairs)
+        out[k] = (full - part) * 1e3
+    return out
+
+
 def pass_us(passes, stat="median"):
     """Per-pass kernel time (us): the pass's event-bracketed time less that
     of an empty encode between the same two events."""
@@ -187,11 +226,14 @@ def pass_algorithmic_bytes(plan):
     # writes the per-token decay records, which Pass C reads instead of dt.
     fused = not plan.kernel_b
     rec = plan.rec_bytes
+    # Pass B stores, and a walking Pass C reads, the start states of the walks
+    # only (one per walk_len chunks); off the walk, every segment's.
+    starts = state * plan.walks_per_group if plan.walk_len != plan.seg_len else plan.s_seg_bytes
     return {
         "A": x + dt + bc + plan.s_local_bytes + plan.s_seg_bytes + ((bc + cp) if cp else 0) + rec,
-        "B": 0 if fused else 2 * plan.s_seg_bytes + 2 * state,
-        "C": x + (rec if rec else dt) + (cp if cp else 2 * bc) + plan.s_local_bytes + plan.s_seg_bytes + y
-             + (2 * state if fused else 0),
+        "B": 0 if fused else plan.s_seg_bytes + starts + 2 * state,
+        "C": x + (rec if rec else dt) + (cp if cp else 2 * bc) + plan.s_local_bytes
+             + (plan.s_seg_bytes if fused else starts) + y + (2 * state if fused else 0),
     }
 
 
@@ -263,7 +305,7 @@ def cpu_baseline(budget_s: float = 20.0):
     return out
 
 
-def config_report(ctx, stream, dev, steps: int, warm_ms: float):
+def config_report(ctx, stream, dev, steps: int, warm_ms: float, names=None):
     """Every BASELINE config on each path it is quoted on: tokens/s, GFLOP/s,
     fraction of the op roofline and the per-pass split (medians of `steps`
     event-timed encodes after `warm_ms` of warm-up). The roofline rule is the
@@ -271,6 +313,8 @@ def config_report(ctx, stream, dev, steps: int, warm_ms: float):
     peak on the bf16 path and the fp32 peak on the fp32 path."""
     out = {}
     for i, cfg in enumerate(CONFIGS):
+        if names and cfg["name"] not in names:
+            continue
         L, S, H, P, N, G = (cfg[k] for k in "LSHPNG")
         tensors = make_inputs(1000 + i, dev, cfg)
         F = algorithmic_flops(L, S, H, P, N)
@@ -315,6 +359,9 @@ def main():
     ap.add_argument("--config-steps", type=int, default=20,
                     help="event-timed encodes per config and path in the per-config report "
                          "(0 skips the report)")
+    ap.add_argument("--only-config", default=None, metavar="NAME",
+                    help="run only the per-config report of this BASELINE config (0 1 2 3 4a 4b) and "
+                         "print it: a process of its own for profiling one configuration")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
                     help="also run a plain device copy of this size (a known-traffic kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -328,6 +375,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     ctx = Context(0)
+    if args.only_config:
+        stream = torch.cuda.current_stream(dev)
+        rep = config_report(ctx, stream, dev, max(1, args.config_steps), args.warmup_ms, {args.only_config})
+        if not rep:
+            print(f"bench.py: no config named {args.only_config!r}", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({"configs": rep}), flush=True)
+        return
     # One device allocation for the whole workload, as a serving runtime's
     # arena: torch's caching allocator keeps this block and carves the
     # inputs, outputs and scratch out of it. Separate allocations made the
@@ -379,37 +434,42 @@ def main():
         wall = (time.perf_counter() - w0) / args.steps * 1e3
         # Per-pass split (HELIX_ONLY_PASS) exists only for the multipass path.
         passes = time_passes(v, args.steps, stream) if v.multipass else None
+        in_scan = time_in_scan(v, args.steps, stream) if v.multipass and v.name == "bf16" else None
         d = dist(ts)
         ms = statistics.fmean(ts)
         peak_c = PEAK_BF16_MFMA if v.name == "bf16" else PEAK_FP32_MFMA
         t_roof = max(F_A / PEAK_FP32_MFMA + F_C / peak_c, bytes_alg / PEAK_HBM)
-        results[v.name] = dict(ms=ms, d=d, wall_ms=wall, passes=passes, t_roof=t_roof,
+        results[v.name] = dict(ms=ms, d=d, wall_ms=wall, passes=passes, in_scan=in_scan, t_roof=t_roof,
                                kernel=v.kernel, plan=v.plan)
 
     # Dominant kernel of the headline (bf16) path and its roofline. Every pass
     # is HBM-bound at this shape (Pass C: ~0.49 GB against ~6 us of bf16 MFMA
     # work; Pass A: ~0.32 GB against ~20 us of bf16x6 MFMA work), so each is
-    # priced on its algorithmic bytes: what it must read and write once.
+    # priced on its algorithmic bytes: what it must read and write once. The
+    # dominant kernel and its duration come from the passes' times inside
+    # whole scans (time_in_scan, means), the statistic rocprofv3 --stats
+    # averages over a run of this script.
     r = results["bf16"]
-    pa = pass_us(r["passes"])                   # median kernel time per pass, us
-    pmean = pass_us(r["passes"], "mean")        # mean, as rocprofv3 --stats averages
+    pa = pass_us(r["passes"])                   # median kernel time per pass (split encodes), us
+    pin = r["in_scan"]                          # mean time per pass inside whole scans, us
     plan = r["plan"]
     pass_bytes = pass_algorithmic_bytes(plan)
     # Pass B has no kernel of its own when the walking Pass C runs its scan
     # (plan.kernel_b is null): its bytes and time are then Pass C's.
     kernels = {"A": plan.kernel_a, "B": plan.kernel_b, "C": plan.kernel_c}
     live = [k for k in "ABC" if kernels[k]]
-    dom = max(live, key=lambda k: pa[k])
+    dom = max(live, key=lambda k: pin[k])
     kname = kernels[dom].decode()
-    t = pmean[dom] * 1e-6          # average launch duration, as rocprofv3 --stats reports it
+    t = pin[dom] * 1e-6
     roof = {"kernel": f"{kname} (Pass {dom})", "bound": "hbm",
             "achieved": pass_bytes[dom] / t / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "algorithmic_bytes": pass_bytes[dom]}
+            "algorithmic_bytes": pass_bytes[dom], "duration_us": pin[dom],
+            "duration_stat": "mean time inside whole scans (whole scan less the scan without the pass)"}
     roof["frac"] = roof["achieved"] / roof["peak"]
     roof["traffic"] = profiled_traffic(kname)
     passes_roof = {k: {"kernel": kernels[k].decode(),
-                       "us": pa[k], "algorithmic_bytes": pass_bytes[k],
-                       "hbm_frac": pass_bytes[k] / (pa[k] * 1e-6) / PEAK_HBM} for k in live}
+                       "us_in_scan": pin[k], "us_split": pa[k], "algorithmic_bytes": pass_bytes[k],
+                       "hbm_frac": pass_bytes[k] / (pin[k] * 1e-6) / PEAK_HBM} for k in live}
 
     ms = r["ms"]
     value = S * L / (ms * 1e-3)
@@ -443,8 +503,10 @@ def main():
         "passes_roofline": passes_roof,
         "timing_ms": {k: round(vv, 5) for k, vv in r["d"].items()},
         # Per-pass kernel times: event-bracketed single-pass encodes less an
-        # empty encode between the same events (event_pair_us).
+        # empty encode between the same events (event_pair_us), and the
+        # passes' times inside whole scans (time_in_scan).
         "passes_us": {k: pa[k] for k in live},
+        "passes_in_scan_us": {k: pin[k] for k in live},
         "event_pair_us": dist(r["passes"]["X"])["median"] * 1e3,
         "fp32_path": {
             "tok_s": S * L / (results["fp32"]["ms"] * 1e-3),

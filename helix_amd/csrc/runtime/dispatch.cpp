@@ -225,13 +225,14 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     }
 
     // Debug-only per-pass timing split (reference dispatch.mm:207-216):
-    // HELIX_ONLY_PASS=A|B|C enqueues just that pass; the output is then
-    // meaningless. 'X' (the reference's pad/cast passes) enqueues nothing,
-    // because that work is fused into the Pass A/C staging here.
+    // HELIX_ONLY_PASS=A|B|C enqueues just that pass, and a set of letters
+    // (AB, AC, BC) just those passes; the output is then meaningless. 'X' (the
+    // reference's pad/cast passes) enqueues nothing, because that work is
+    // fused into the Pass A/C staging here.
     const char* only = std::getenv("HELIX_ONLY_PASS");
-    const bool do_a = !only || *only == 'A';
-    const bool do_b = !only || *only == 'B';
-    const bool do_c = !only || *only == 'C';
+    const bool do_a = !only || std::strchr(only, 'A');
+    const bool do_b = !only || std::strchr(only, 'B');
+    const bool do_c = !only || std::strchr(only, 'C');
 
     int prev = -1;
     (void)hipGetDevice(&prev);
