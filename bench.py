@@ -401,8 +401,6 @@ def main():
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
         variants.append(Variant("bf16-passA-x3-optin", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_PASSA_SPLIT": "3"}))
-        variants.append(Variant("bf16-passB-launch", ctx, HELIX_BACKEND_MPP, tensors,
-                                env={"HELIX_FUSE_B": "0"}))
 
     def warm_up(v, ms):
         """W steps, then more until the wall clock has run `ms` (the
