@@ -7,4 +7,5 @@
 #include "pass_c_f32.hip"
 #include "pass_c_x6.hip"
 #include "pass_c_walk16.hip"
+#include "pass_c_walk_x6.hip"
 #include "pass_single.hip"

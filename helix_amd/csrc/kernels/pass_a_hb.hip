@@ -228,8 +228,9 @@ struct HbPre {
 };
 
 // `shift` (<= 0) is the log-decay from the chunk's end to where the weighted
-// sum is taken (0: the chunk's end), folded into the weight.
-template <int MODE>
+// sum is taken (0: the chunk's end), folded into the weight. R64: the record
+// in the fp32 path's form (store_decay_record64), whatever the MODE.
+template <int MODE, bool R64 = false>
 __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtraw, float A_h, int c, int lane,
                                              double shift) {
     const int t0 = (p.chunk_base + c) * HELIX_CS;
@@ -240,7 +241,7 @@ __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtr
     HbPre r;
     r.w = keep_if_lt(exp_diff(lend + shift, lcum) * dtv, lane, tlen);
     r.lend = lend;
-    if constexpr (MODE == 2) {
+    if constexpr (MODE == 2 && !R64) {
         const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
         const float l2 = (float)(lcum * 1.4426950408889634074);
         const float e = expf((float)lcum);
@@ -257,7 +258,8 @@ __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtr
 // fp64 decay records of the fp32 path's Pass C; MODE 2: segment aggregates only,
 // and the walk's decay records. IO: the caller's storage type of x and B. BCC:
 // write the bf16 copies of B and C (fp32 storage). NS: split planes per operand.
-template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3>
+// R64: MODE 2 with the fp32 path's records, for its bf16x6 walk.
+template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3, bool R64 = false>
 __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     static_assert(NP == 64 || NP == 128, "the double-buffered B planes of d_state 256 exceed the LDS");
     static_assert(NS == 2 || NS == 3, "two or three split planes");
@@ -376,7 +378,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // waves and the chunk loop has no branch, so the preamble's ALU work can be
     // scheduled among the MFMAs.
     auto preamble = [&](int c, double shift, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
-        const HbPre pr = hb_preamble<MODE>(p, dtraw, A_h, c, lane, shift);
+        const HbPre pr = hb_preamble<MODE, R64>(p, dtraw, A_h, c, lane, shift);
         wdst[is][lane] = pr.w;
         // The record's address is formed unconditionally (a select of two
         // pointers becomes a branch); without records its range is zero.
@@ -573,6 +575,10 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_bc_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                      \
         chunk_state_hb_impl<NP, 2, float, true>(p, b);                                                \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_r64_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, false, 3, true>(p, b);                                      \
     }                                                                                                 \
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_bf16io_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                      \

@@ -145,30 +145,6 @@ HELIX_DEV void store16_nat(__bf16* buf, int row, int col0, const float (&v)[16])
     *reinterpret_cast<bf16x8*>(&buf[swz_off<RSX>(row, col0 + 8)]) = b;
 }
 
-// Store the wave's y tile of one chunk: acc[tb] register r holds
-// y[t = 16 tb + 4 q + r][pp]. Rows past tlen and columns past the slab width
-// are dropped by the range check; with tlen <= 0 nothing is stored.
-template <typename IO>
-__device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScanParams& p,
-                                          const HelixScanBuffers& b, int seq, int h, int t0, int tlen,
-                                          int p0, int pw, int pp, int q) {
-    constexpr int ES = (int)sizeof(IO);
-    const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
-    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * (unsigned)ES : 0u;
-    const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
-                                        (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
-                                    bytes);
-    const int voff = (4 * q * sy0 + pp * sy2) * ES;
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = 16 * tb + 4 * q + r;
-            const float v = acc[tb][r];
-            io_store<IO, HELIX_NT>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (16 * tb + r) * sy0 * ES);
-        }
-}
-
 // IO: the caller's storage type of x, B, C and y (dt, A and the states are
 // fp32). BIO: the type B and C are read in; __bf16 with fp32 storage when
 // they come from Pass A's bf16 copies (the host points B and C there).

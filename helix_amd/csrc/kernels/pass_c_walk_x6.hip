@@ -1,0 +1,447 @@
+// pass_c_walk_x6.hip -- the fp32 path's Pass C: the chunk walk on bf16x6 products.
+//
+// Reference counterpart: helix_chunk_out_f32 (src/kernels/
+// helix_scan_multipass.metal:225-361). Like the bf16 path's walk
+// (pass_c_walk16.hip), one workgroup walks a segment of chunks from the
+// segment's start state S_seg (Pass B) and forms every chunk's own start
+// state R on the way, producing per chunk
+//     y = tril(C B^T . decay) (dt x) + exp(Lcum) . (C R)        (G1, G2, G3)
+//     R <- exp(L_end) R + B^T . (decay . dt . x)                  (G4)
+// Here every product keeps fp32 accuracy: v_mfma_f32_16x16x32_bf16 over
+// operands split into three bf16 parts (six products, fp32 accumulation),
+// and R stays in fp32 registers. Against the chunk-parallel bf16x6 Pass C
+// (pass_c_x6.hip), whose per-chunk start states Pass A writes and Pass C
+// reads back, the walk moves half the bytes.
+//
+// Workgroup: (seq, walk segment, two heads of one B/C group, 64-wide P slab),
+// eight waves; wave (hw, w4) owns P columns 16 w4 .. 16 w4 + 15 of head hw:
+//   - R[n][p] for its 16 columns: NP/16 result tiles, register r of tile nb
+//     holding R[16 nb + 4 (lane/16) + r][p];
+//   - G3 and G4 on those tiles, G2 on its columns;
+//   - G1 (C B^T, the same for both heads) split over the eight waves by
+//     16 x 16 block; each head's M = C B^T . decay shared through LDS.
+// K order: within each group of 32 state indices, index 16 h + 4 q + r sits at
+// K position 8 q + 4 h + r (perm32) in the C and B rows, so R's registers are
+// G3's operand as they stand (the layout of the bf16 walk).
+//
+// LDS, three bf16 planes per operand in the x6_off layout (no padding):
+//   C    [64 t][NP n]   perm32 n order             G1, G3
+//   B    [64 j][NP n]   perm32 n order             G1; afterwards the region
+//   M    [64 t][64 j]   one per head               holds the heads' M (G2)
+//   B^T  [NP n][64 j]   natural n order            G4
+// and the heads' decay records: 145 KiB at d_state 128, one workgroup per CU.
+// The B operands of G2 and G4 (dt x and decay dt x at the lane's own column
+// and K tokens) and of G3 (R) are split in registers.
+#include "helix_common.h"
+
+#include "pass_c_stage.h"
+
+// Six 16 x 16 x 32 products of split operands a[3] x b[3], smallest terms first.
+HELIX_DEV f32x4 wx6_mfma(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+    return acc;
+}
+
+// Eight fp32 values as the three split planes of one MFMA operand.
+HELIX_DEV void wx6_split8(const float (&v)[8], bf16x8 (&o)[3]) {
+    u32x4 q0, q1, q2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        unsigned w0, w1, w2;
+        split3_pair(v[2 * e], v[2 * e + 1], w0, w1, w2);
+        q0[e] = w0;
+        q1[e] = w1;
+        q2[e] = w2;
+    }
+    o[0] = __builtin_bit_cast(bf16x8, q0);
+    o[1] = __builtin_bit_cast(bf16x8, q1);
+    o[2] = __builtin_bit_cast(bf16x8, q2);
+}
+
+// v, opaque to the optimizer (it stays in a VGPR and is not known to be
+// loop-invariant).
+HELIX_DEV int vgpr_opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// K position of state index i inside its group of 32: 16 h + 4 q + r -> 8 q + 4 h + r.
+HELIX_DEV int wx6_perm32(int i) {
+    return (i & ~31) | (8 * ((i >> 2) & 3) + 4 * ((i >> 4) & 1) + (i & 3));
+}
+
+// G1 block idx (0..9) of the lower triangle of the 4 x 4 grid of 16 x 16
+// blocks: (tb, jb) = (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) ...
+HELIX_DEV int wx6_tb(int idx) { return (idx >= 1) + (idx >= 3) + (idx >= 6); }
+HELIX_DEV int wx6_jb(int idx) {
+    const int tb = wx6_tb(idx);
+    return idx - tb * (tb + 1) / 2;
+}
+
+// This lane's B and C runs of one chunk (fp32): state indices 8u .. 8u+7 of
+// rows j0 and j0 + 1, two 16-byte words each.
+struct RunsWX6 {
+    u32x4 b[2][2], c[2][2];
+};
+
+__device__ __forceinline__ void load_runs_x6(RunsWX6& r, const HelixScanParams& p, const float* __restrict__ B_g,
+                                             const float* __restrict__ C_g, int c, int N, int j0, int u) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
+    const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * 4u);
+    const helix_rsrc rc = make_rsrc(C_g + (long long)t0 * p.s_c[0], ((tlen - 1) * sc0 + N) * 4u);
+    const int n0 = min(8 * u, N - 8);   // d_state % 8 == 0: a run is all in or out
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int jr = min(j0 + k, tlen - 1);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4 + 16 * w, 0, 0);
+            r.c[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4 + 16 * w, 0, 0);
+        }
+    }
+}
+
+// The decay record of token lane (store_decay_record64: dt, exp(Lcum), Lcum
+// in fp64) and x at this lane's P column for its K tokens j = 32 s + 8 q + e
+// (s = 0, 1; e = 0..7), prefetched a chunk ahead.
+struct StageWX6 {
+    u32x4 rec;
+    float x[16];
+};
+
+__device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParams& p, const float* __restrict__ rec_h,
+                                              const float* __restrict__ x_h, int c, int lane, int q, int pp,
+                                              int pw) {
+    const int t0   = (p.chunk_base + c) * HELIX_CS;
+    const int tlen = min(HELIX_CS, p.n_tok - t0);
+    const int sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
+    const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
+    const helix_rsrc rx = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
+    st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    const int xc = min(pp, pw - 1) * sx2;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            st.x[8 * s + e] = buf_elem<float>(rx, xc + min(32 * s + 8 * q + e, tlen - 1) * sx0, 0);
+}
+
+template <int NP>
+__device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(NP == 128, "two rows per lane in the staging: d_state 128");
+    constexpr int HPW = 2;                     // heads per workgroup, four waves each
+    constexpr int NB  = NP / 16;               // 16-row state tiles of R
+    constexpr int KS  = NP / 32;               // K steps over the state
+    constexpr int NT32 = NP / 32;              // 32 x 32 tiles of the slab tile layout
+    constexpr int NCH = NP / 8;                // 16-byte chunks per C / B row
+    constexpr int PL_CB = 3 * HELIX_CS * NP;   // C (or B) planes, elements
+    constexpr int PL_M  = 3 * HELIX_CS * HELIX_CS;
+    static_assert(HPW * PL_M <= PL_CB, "the heads' M fit in B's region");
+    __shared__ __attribute__((aligned(16))) __bf16 sC[PL_CB];
+    __shared__ __attribute__((aligned(16))) __bf16 sB[PL_CB];
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];
+    __shared__ __attribute__((aligned(16))) float sDt[HPW][HELIX_CS];    // dt_j (0 past tlen)
+    __shared__ __attribute__((aligned(16))) float sSd[HPW][HELIX_CS];    // exp(L_end - Lcum_j)
+    __shared__ __attribute__((aligned(16))) float sE[HPW][HELIX_CS];     // exp(Lcum_t)
+    __shared__ __attribute__((aligned(16))) double sL[HPW][HELIX_CS];    // Lcum_t
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = wave_uniform();
+    const int hw = wave >> 2, w4 = wave & 3;   // head slot, P block within it
+    const int N = p.d_state, P = p.head_dim;
+    const int hpg = p.heads_per_group;
+    const int npair = (hpg + HPW - 1) / HPW;
+
+    // 1-D grid, a group's head pairs consecutive in the logical order so that
+    // they share an XCD (and the chunk's B and C in its L2).
+    const unsigned total = (unsigned)(p.n_walk * p.n_group * npair * p.n_pslab * p.n_seq);
+    unsigned wid = xcd_logical_id(blockIdx.x, total);
+    const int pair = (int)(wid % (unsigned)npair);    wid /= (unsigned)npair;
+    const int seg  = (int)(wid % (unsigned)p.n_walk); wid /= (unsigned)p.n_walk;
+    const int g    = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
+    const int slab = (int)(wid % (unsigned)p.n_pslab);
+    const int seq  = (int)(wid / (unsigned)p.n_pslab);
+    // A workgroup of the last pair may have one head: its spare waves walk
+    // that head again and store nothing.
+    const int hslot = HPW * pair + hw;
+    const bool head_ok = hslot < hpg;
+    const int h  = g * hpg + min(hslot, hpg - 1);
+    const int p0 = slab * HELIX_HD;
+    const int pw = min(HELIX_HD, P - p0);
+
+    const int c_begin = seg * p.walk_len;
+    const int c_end   = min(c_begin + p.walk_len, p.n_cg);
+    if (c_begin >= c_end) return;
+
+    const float* __restrict__ rec_h = b.pre + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * 4);
+    const float* __restrict__ x_h = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
+    const float* __restrict__ B_g = b.B + seq * p.seq_b + g * p.s_b[1];
+    const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
+
+    // Staging: lane (u, rr) holds state indices 8u .. 8u+7 of rows j0 and j0 + 1
+    // (the wave's eight rows, 16 lanes per row), so that a pair of B^T values
+    // (rows j0, j0 + 1 of one state index) is one 4-byte LDS store.
+    RunsWX6 runs;
+    load_runs_x6(runs, p, B_g, C_g, c_begin, N, 8 * wave + 2 * (lane >> 4), lane & 15);
+    StageWX6 st;
+    load_stage_x6(st, p, rec_h, x_h, c_begin, lane, lane >> 4, 16 * w4 + (lane & 15), pw);
+
+    // The segment's start state S_seg from Pass B (its Pass A segment is the
+    // one the walk segment starts at). R[n][pp], n = 16 nb + 4 q + r, from the
+    // slab tile: unit ((pt NT32 + nb/2) 4 + r4) 64 + lane' with pt = w4/2,
+    // r4 = 2 (nb%2) + q/2, lane' = 32 (q%2) + 16 (w4%2) + c16.
+    f32x4 R[NB];
+    {
+        const float* tiles = b.s_seg + seq * p.sg_seq + state_tile_off(p, h, slab) +
+                             (long long)(seg * (p.walk_len / p.seg_len)) * p.sg_seg;
+        const helix_rsrc rg = make_rsrc(tiles, 64u * NP * sizeof(float));
+        const int q = lane >> 4;
+        const int vunit = 64 * (q >> 1) + 32 * (q & 1) + 16 * (w4 & 1) + (lane & 15);
+        const int pt = w4 >> 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            R[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
+    }
+
+    __bf16* const sMh = sB + hw * PL_M;
+
+    // Four barriers per chunk: (1) staging done; (2) every wave's G1 has read
+    // B; (3) M written into B's region; (4) G2 has read M (the next chunk's
+    // staging overwrites it).
+    for (int c = c_begin; c < c_end; ++c) {
+        const int t0   = (p.chunk_base + c) * HELIX_CS;
+        const int tlen = min(HELIX_CS, p.n_tok - t0);
+        // On the last chunk the same chunk is loaded again: no branch.
+        const int cn = min(c + 1, c_end - 1);
+        // Lane-derived indices, formed anew in every chunk: hoisted out of the
+        // loop, the LDS addresses made from them would not fit the registers.
+        const int ln = vgpr_opaque(lane);
+        const int c16 = ln & 15, q = ln >> 4;  // MFMA operand row, K slot group
+        const int u = c16, rr = q;             // staging run and row pair
+        const int j0 = 8 * wave + 2 * rr;
+        const int cpos = wx6_perm32(8 * u);    // K position of 8u; 8u + 4 sits 8 further
+        const int pp = 16 * w4 + c16;          // this lane's P column in the slab
+
+        // ---- C, B and B^T planes -------------------------------------------
+        // C is zeroed past tlen and d_state, which is all G1 and G3 need; B
+        // rows past tlen only meet dt = 0 columns in G2 and G4.
+        {
+            unsigned bw[2][3][4];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int j = j0 + k;
+                const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * u)) >> 31);
+                float vb[8], vc[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    vb[e] = as_f32(runs.b[k][e >> 2][e & 3]);
+                    vc[e] = as_f32(runs.c[k][e >> 2][e & 3] & keep);
+                }
+                u32x2 cq[3][2], bq[3][2];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    unsigned c0, c1, c2;
+                    split3_pair(vc[2 * e], vc[2 * e + 1], c0, c1, c2);
+                    split3_pair(vb[2 * e], vb[2 * e + 1], bw[k][0][e], bw[k][1][e], bw[k][2][e]);
+                    cq[0][e >> 1][e & 1] = c0;
+                    cq[1][e >> 1][e & 1] = c1;
+                    cq[2][e >> 1][e & 1] = c2;
+                }
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        bq[pl][hh] = u32x2{bw[k][pl][2 * hh], bw[k][pl][2 * hh + 1]};
+                        const int pos = cpos + 8 * hh;
+                        const int off = x6_off<HELIX_CS, NCH>(pl, j, pos >> 3) + (pos & 7);
+                        *reinterpret_cast<u32x2*>(&sC[off]) = cq[pl][hh];
+                        *reinterpret_cast<u32x2*>(&sB[off]) = bq[pl][hh];
+                    }
+                }
+            }
+            // B^T[n][j0 .. j0 + 1], n = 8u + e: the halves of rows j0 and j0 + 1.
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
+                    const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+                    *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
+                }
+        }
+        load_runs_x6(runs, p, B_g, C_g, cn, N, j0, u);
+
+        // ---- decay records of the two heads --------------------------------
+        if (w4 == 0) {
+            const double lcum = __builtin_bit_cast(double, (unsigned long long)st.rec[2] |
+                                                               ((unsigned long long)st.rec[3] << 32));
+            const double lend = __builtin_bit_cast(
+                double, (unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[2], 63) |
+                            ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[3], 63) << 32));
+            sDt[hw][lane] = as_f32(st.rec[0]);
+            sE[hw][lane] = as_f32(st.rec[1]);
+            sSd[hw][lane] = exp2_diff(lend, lcum);
+            sL[hw][lane] = lcum;
+        }
+        // exp(L_end) = exp(Lcum) of token 63.
+        const float a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[1], 63));
+        __syncthreads();   // (1)
+
+        // dt x at (K token j = 32 s + 8 q + e, column pp); G4 scales it by the
+        // decay when it needs it.
+        float xb[2][8];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int h4 = 0; h4 < 2; ++h4) {
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sDt[hw][32 * s + 8 * q + 4 * h4]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xb[s][4 * h4 + k] = d4[k] * st.x[8 * s + 4 * h4 + k];
+            }
+        load_stage_x6(st, p, rec_h, x_h, cn, lane, q, pp, pw);
+
+        // ---- G1: D[j][t] = (B C^T) of blocks idx = wave, wave + 8 -----------
+        // Block idx: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
+        f32x4 d[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = wave + 8 * i;
+            d[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (idx < 10) {
+                const int tb = wx6_tb(idx), jb = wx6_jb(idx);
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    bf16x8 av[3], bv[3];
+                    x6_read<HELIX_CS, NCH>(sB, 16 * jb + c16, 4 * s + q, av);
+                    x6_read<HELIX_CS, NCH>(sC, 16 * tb + c16, 4 * s + q, bv);
+                    d[i] = wx6_mfma(av, bv, d[i]);
+                }
+            }
+        }
+
+        // ---- G3: y = exp(Lcum_t) . (C R), R the state before this chunk -----
+        f32x4 acc[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            float rv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                rv[e] = R[2 * s][e];
+                rv[4 + e] = R[2 * s + 1][e];
+            }
+            bf16x8 rp[3];
+            wx6_split8(rv, rp);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                bf16x8 cv[3];
+                x6_read<HELIX_CS, NCH>(sC, 16 * tb + c16, 4 * s + q, cv);
+                acc[tb] = wx6_mfma(cv, rp, acc[tb]);
+                if (tb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sE[hw][16 * tb + 4 * q]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tb][r] *= e4[r];
+        }
+        __syncthreads();   // (2) B's rows are free
+
+        // ---- M[t][j] = (C B^T)[t][j] exp(Lcum_t - Lcum_j), j <= t, per head --
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = wave + 8 * i;
+            if (idx < 10) {
+                const int tb = wx6_tb(idx), jb = wx6_jb(idx);
+                const int t = 16 * tb + c16;
+                const int jq = 16 * jb + 4 * q;
+#pragma unroll
+                for (int hh = 0; hh < HPW; ++hh) {
+                    const double lt = sL[hh][t];
+                    float m[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        m[r] = keep_if_le(d[i][r] * exp2_diff(lt, sL[hh][jq + r]), jq + r, t);
+                    u32x2 mq[3];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        unsigned w0, w1, w2;
+                        split3_pair(m[2 * e], m[2 * e + 1], w0, w1, w2);
+                        mq[0][e] = w0;
+                        mq[1][e] = w1;
+                        mq[2][e] = w2;
+                    }
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        *reinterpret_cast<u32x2*>(&sB[hh * PL_M + x6_off<HELIX_CS, 8>(pl, t, jq >> 3) + (jq & 7)]) =
+                            mq[pl];
+                }
+            }
+        }
+
+        // ---- G4: R <- exp(L_end) R + B^T . (decay dt x) (after G3 used R) ---
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) R[nb] *= a_c;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            float xs[8];
+#pragma unroll
+            for (int h4 = 0; h4 < 2; ++h4) {
+                const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sSd[hw][32 * s + 8 * q + 4 * h4]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xs[4 * h4 + k] = s4[k] * xb[s][4 * h4 + k];
+            }
+            bf16x8 xp[3];
+            wx6_split8(xs, xp);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                bf16x8 bt[3];
+                x6_read<NP, 8>(sBt, 16 * nb + c16, 4 * s + q, bt);
+                R[nb] = wx6_mfma(bt, xp, R[nb]);
+                // Operand reads run at most two tiles ahead of the MFMAs.
+                if (nb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __syncthreads();   // (3) M complete
+
+        // ---- G2: y += M . dtX (t block tb needs j < 16 (tb + 1)) -----------
+        // K step s covers j blocks 2s and 2s + 1; for tb = 0 and 2 the second
+        // lies above the diagonal (lanes q >= 2), where M was not written.
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            bf16x8 xp[3];
+            wx6_split8(xb[s], xp);
+#pragma unroll
+            for (int tb = 2 * s; tb < 4; ++tb) {
+                bf16x8 mv[3];
+                x6_read<HELIX_CS, 8>(sMh, 16 * tb + c16, 4 * s + q, mv);
+                if (tb == 2 * s) {
+                    const unsigned keep = q < 2 ? ~0u : 0u;
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        mv[pl] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, mv[pl]) & keep);
+                }
+                acc[tb] = wx6_mfma(mv, xp, acc[tb]);
+            }
+        }
+        store_y16<float>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        __syncthreads();   // (4)
+    }
+}
+
+#define HELIX_PASS_C_WALK_X6(NP)                                                                \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * 2) void helix_scan_walk_x6_n##NP(         \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk_x6_impl<NP>(p, b);                                                            \
+    }
+
+HELIX_PASS_C_WALK_X6(128)

@@ -31,6 +31,13 @@ namespace {
 //     Pass C helix_chunk_out_x6_n{64,128}  bf16x6 split products
 //            helix_chunk_out_f32_n256      fp32 MFMA (the bf16x6 planes of a
 //                                          d_state 256 tile exceed the LDS)
+//   fp32 path at d_state 65..128 (fp32 storage): Pass C walks each segment's
+//   chunks on bf16x6 products with the state in registers, so Pass A stores no
+//   per-chunk states (HELIX_F32_WALK=0 keeps the chunk-parallel Pass C):
+//     Pass A helix_chunk_state_hb_x6agg_r64_n128  segment aggregates, fp64
+//                                                 decay records
+//     Pass B helix_state_scan_f32
+//     Pass C helix_scan_walk_x6_n128
 //   bf16 path (AUTO or MPP, multipass): Pass C walks each segment's chunks on
 //   bf16 MFMA with the state in registers; Pass A computes the segment
 //   aggregates only, on six split products (fp32 accuracy, the reference's
@@ -60,9 +67,10 @@ int io_index(helix_dtype io) { return io == HELIX_BF16 ? 1 : io == HELIX_F16 ? 2
 // Traits are composed from these choices, once per process; the names live as
 // long as the process.
 struct TraitTable {
-    // [io][k]: single pass; [k]: diagonal A; [k]: fp32 path;
-    // [io][split6][bccopy][k]: bf16 path (bccopy only with fp32 storage).
-    HelixMatmulTraits single[3][3], diag[2], f32[3], bf16[3][2][2][3];
+    // [io][k]: single pass; [k]: diagonal A; [k]: fp32 path; the fp32 path's
+    // walk (d_state 128); [io][split6][bccopy][k]: bf16 path (bccopy only with
+    // fp32 storage).
+    HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk, bf16[3][2][2][3];
     std::vector<std::string> names;   // every kernel name, deduplicated
     std::deque<std::string> store;    // backing storage of the strings above
 
@@ -116,6 +124,17 @@ struct TraitTable {
                 t.mfma_c = x6c ? "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)" : "v_mfma_f32_32x32x2_f32";
                 t.np = kNps[k];
                 t.rec_kind = x6c ? 2 : 0;
+            }
+            if (kNps[k] == 128) {
+                HelixMatmulTraits& t = f32walk;
+                t = f32[k];
+                t.name = keep("mfma fp32, passes A and C bf16x6, chunk walk" + upto);
+                t.k_chunk_state = kernel("helix_chunk_state_hb_x6agg_r64_n" + np);
+                t.k_chunk_out = kernel("helix_scan_walk_x6_n" + np);
+                t.mfma_c = "v_mfma_f32_16x16x32_bf16 (bf16x6 split operands)";
+                t.walk = true;
+                t.walk_hpw = 2;
+                t.rec_kind = 2;
             }
             for (int io = 0; io < 3; ++io)
                 for (int s6 = 0; s6 < 2; ++s6)
@@ -211,6 +230,7 @@ helix_tuning tuning_from_env() {
     t.bccopy = env_switch("HELIX_WALK_BCCOPY") == 0 ? 0 : -1;
     t.seg_len = (int)env_long("HELIX_SEG_LEN", 0);
     t.hblk = (int)env_long("HELIX_HBLK", 0);
+    if (env_switch("HELIX_F32_WALK") == 0) t.f32_walk = 0;
     return t;
 }
 
@@ -238,7 +258,10 @@ const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_de
     if (!d.multipass) return tt.single[io][k];
     // HELIX_FORCE_BACKEND=s... pins the fp32 path (reference caps.mm:82-86).
     const bool bf16 = (d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP) && !tu.force_fp32;
-    if (!bf16) return io ? tt.single[io][k] : tt.f32[k];
+    if (!bf16) {
+        if (io) return tt.single[io][k];
+        return k == 1 && tu.f32_walk != 0 ? tt.f32walk : tt.f32[k];
+    }
     const int bc = io == 0 && bccopy_on(tu, d) ? 1 : 0;
     return tt.bf16[io][tu.passa_split == 3 ? 0 : 1][bc][k];
 }

@@ -66,6 +66,10 @@ MODES = [
     ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", {}, True),
     ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}, True),
     ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {}, True),
+    # The fp32 path's chunk-parallel Pass C on per-chunk states stored by
+    # Pass A, which d_state 65..128 replaces with the walk by default.
+    ("fp32/chunk/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "0"}, True),
+    ("fp32/chunk/sm", HELIX_BACKEND_SGMMA, 1, "short", {"HELIX_F32_WALK": "0"}, True),
     ("bf16", HELIX_BACKEND_MPP, None, "short", {}, True),
     ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}, True),
     ("bf16/long", HELIX_BACKEND_MPP, None, "long", {}, True),

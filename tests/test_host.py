@@ -232,10 +232,11 @@ def test_null_context_and_desc():
 
 def test_noalloc_host_checks(host):
     # helix_scan_encode_noalloc refuses, before anything is enqueued, a plan
-    # whose scratch exceeds its fixed array (config 2 on the fp32 path needs
-    # 280 MiB), and a host-only context has no device for one that fits.
+    # whose scratch exceeds its fixed array (config 2 at d_state 256 on the
+    # fp32 path, whose Pass A stores every chunk's state: 520 MiB), and a
+    # host-only context has no device for one that fits.
     t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
-    big = mp(CONFIG_SHAPES["cfg2"], HELIX_BACKEND_SGMMA)
+    big = mp((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)
     assert host.scratch_size(big) > abi.NOALLOC_SCRATCH_BYTES
     assert host.encode_noalloc(0, big, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
     assert "HELIX_NOALLOC_SCRATCH_BYTES" in host.last_error()
@@ -277,9 +278,18 @@ def test_backend_selection(host):
     assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_SGMMA)) == HELIX_BACKEND_SGMMA
     # bf16x6 split products: Pass A on every path, and the fp32 path's Pass C
-    # up to d_state 128.
+    # up to d_state 128, which at d_state 65..128 walks each segment with the
+    # state in registers (HELIX_F32_WALK=0: chunk-parallel on stored states).
     assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
+            == "mfma fp32, passes A and C bf16x6, chunk walk (d_state<=128)")
+    kw = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
+    assert (kw.kernel_a, kw.kernel_b, kw.kernel_c) == (
+        b"helix_chunk_state_hb_x6agg_r64_n128", b"helix_state_scan_f32", b"helix_scan_walk_x6_n128")
+    assert kw.s_local_bytes == 0 and kw.bf16_state == 0 and (kw.seg_len, kw.walk_len) == (8, 16)
+    f0 = tuned(HELIX_F32_WALK="0")
+    assert (f0.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
+    assert f0.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).kernel_c == b"helix_chunk_out_x6_n128"
     # The bf16 path walks segments in Pass C at every d_state; its Pass A runs
     # six split products (the carried state stays fp32-accurate, reference
     # caps.mm:65-73) unless HELIX_PASSA_SPLIT=3 opts into three.
@@ -333,6 +343,8 @@ def test_backend_selection(host):
     assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_hb_x6agg_n128", b"helix_scan_walk16_bf16_n128")
     assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
     k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
+    assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6agg_r64_n128", b"helix_scan_walk_x6_n128")
+    k = tuned(HELIX_F32_WALK="0").plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6f32_n128", b"helix_chunk_out_x6_n128")
     k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
@@ -405,9 +417,10 @@ def test_plan_invariants(host, name, backend):
     assert info.np == (64 if N <= 64 else 128 if N <= 128 else 256)
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
     # The walking Pass C keeps the chunk-local states in registers, so its
-    # plan holds no s_local region; it is the bf16 path's Pass C.
+    # plan holds no s_local region; it is the bf16 path's Pass C, and the
+    # fp32 path's at d_state 65..128.
     walk = b"walk" in info.kernel_c
-    assert walk == (backend == HELIX_BACKEND_MPP)
+    assert walk == (backend == HELIX_BACKEND_MPP or 64 < N <= 128)
     want_sl = state * info.chunks_per_group * 4 if (info.seg_len > 1 and not walk) else 0
     assert info.s_local_bytes == want_sl
     assert info.s_seg_bytes == state * info.segs_per_group * 4
@@ -418,10 +431,10 @@ def test_plan_invariants(host, name, backend):
     assert info.walk_len % info.seg_len == 0
     assert info.walks_per_group == -(-info.chunks_per_group // info.walk_len)
     assert walk or info.walk_len == info.seg_len
-    # The walk runs Pass B's segment scan in its prologue when the plan has one
-    # group of at most four segments that are also its walk segments: no Pass
-    # B launch.
-    fused = walk and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
+    # The bf16 walk runs Pass B's segment scan in its prologue when the plan
+    # has one group of at most four segments that are also its walk segments:
+    # no Pass B launch.
+    fused = walk and backend == HELIX_BACKEND_MPP and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
 

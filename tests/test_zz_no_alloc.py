@@ -63,7 +63,8 @@ def test_noalloc_matches_encode(gpu, path):
 
 
 def test_noalloc_refuses_oversized_plan(gpu):
-    p = po.problem_harness(8192, 1, 64, 64, 128, 8, 5, "short")
+    # d_state 256 on the fp32 path: Pass A stores every chunk's state.
+    p = po.problem_harness(8192, 1, 64, 64, 256, 8, 5, "short")
     d = p.d.copy()
     d.backend = HELIX_BACKEND_SGMMA
     d.multipass = True
