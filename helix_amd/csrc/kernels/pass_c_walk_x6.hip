@@ -125,12 +125,14 @@ __device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParam
     const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
     const helix_rsrc rx = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
     st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
-    const int xc = min(pp, pw - 1) * sx2;
+    // Rows past tlen read 0 (past the resource's range) or, with strides under
+    // which a token row is shorter than the slab, another element of the
+    // chunk: dt is 0 for them either way.
+    const int xv = min(pp, pw - 1) * sx2 + 8 * q * sx0;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            st.x[8 * s + e] = buf_elem<float>(rx, xc + min(32 * s + 8 * q + e, tlen - 1) * sx0, 0);
+        for (int e = 0; e < 8; ++e) st.x[8 * s + e] = buf_elem<float>(rx, xv, (32 * s + e) * sx0);
 }
 
 template <int NP>
@@ -144,6 +146,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     constexpr int PL_CB = 3 * HELIX_CS * NP;   // C (or B) planes, elements
     constexpr int PL_M  = 3 * HELIX_CS * HELIX_CS;
     static_assert(HPW * PL_M <= PL_CB, "the heads' M fit in B's region");
+    constexpr int PF = 2;                      // products an operand read runs ahead
     __shared__ __attribute__((aligned(16))) __bf16 sC[PL_CB];
     __shared__ __attribute__((aligned(16))) __bf16 sB[PL_CB];
     __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];
@@ -187,11 +190,81 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 
     // Staging: lane (u, rr) holds state indices 8u .. 8u+7 of rows j0 and j0 + 1
     // (the wave's eight rows, 16 lanes per row), so that a pair of B^T values
-    // (rows j0, j0 + 1 of one state index) is one 4-byte LDS store.
+    // (rows j0, j0 + 1 of one state index) is one 4-byte LDS store. A chunk's
+    // planes are staged while the previous chunk's products run: C once G1
+    // and G3 are done with it, B^T once G4 is, and B once G2 has read M.
+    // C is zeroed past tlen and d_state, which is all G1 and G3 need; B rows
+    // past tlen only meet dt = 0 columns in G2 and G4.
+    auto stage_c = [&](const RunsWX6& rn, int tl, int j0, int u, int cpos) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int j = j0 + k;
+            const unsigned keep = ~(unsigned)(((tl - 1 - j) | (N - 1 - 8 * u)) >> 31);
+            u32x2 cq[3][2];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                unsigned c0, c1, c2;
+                split3_pair(as_f32(rn.c[k][e >> 1][2 * (e & 1)] & keep), as_f32(rn.c[k][e >> 1][2 * (e & 1) + 1] & keep),
+                            c0, c1, c2);
+                cq[0][e >> 1][e & 1] = c0;
+                cq[1][e >> 1][e & 1] = c1;
+                cq[2][e >> 1][e & 1] = c2;
+            }
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int pos = cpos + 8 * hh;
+                    *reinterpret_cast<u32x2*>(&sC[x6_off<HELIX_CS, NCH>(pl, j, pos >> 3) + (pos & 7)]) = cq[pl][hh];
+                }
+        }
+    };
+    // B's split planes, bw[row k][plane][pair e] (state indices 8u + 2e, +1).
+    auto split_b = [&](const RunsWX6& rn, unsigned (&bw)[2][3][4]) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                split3_pair(as_f32(rn.b[k][e >> 1][2 * (e & 1)]), as_f32(rn.b[k][e >> 1][2 * (e & 1) + 1]),
+                            bw[k][0][e], bw[k][1][e], bw[k][2][e]);
+    };
+    // B^T[n][j0 .. j0 + 1], n = 8u + e: the halves of rows j0 and j0 + 1.
+    auto write_bt = [&](const unsigned (&bw)[2][3][4], int j0, int u) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
+                const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+                *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
+            }
+    };
+    auto write_b = [&](const unsigned (&bw)[2][3][4], int j0, int cpos) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int pos = cpos + 8 * hh;
+                    *reinterpret_cast<u32x2*>(&sB[x6_off<HELIX_CS, NCH>(pl, j0 + k, pos >> 3) + (pos & 7)]) =
+                        u32x2{bw[k][pl][2 * hh], bw[k][pl][2 * hh + 1]};
+                }
+    };
+    auto tlen_of = [&](int c) { return min(HELIX_CS, p.n_tok - (p.chunk_base + c) * HELIX_CS); };
+
     RunsWX6 runs;
-    load_runs_x6(runs, p, B_g, C_g, c_begin, N, 8 * wave + 2 * (lane >> 4), lane & 15);
+    unsigned bw[2][3][4];
     StageWX6 st;
-    load_stage_x6(st, p, rec_h, x_h, c_begin, lane, lane >> 4, 16 * w4 + (lane & 15), pw);
+    {
+        const int u = lane & 15, rr = lane >> 4, j0 = 8 * wave + 2 * rr;
+        load_runs_x6(runs, p, B_g, C_g, c_begin, N, j0, u);
+        load_stage_x6(st, p, rec_h, x_h, c_begin, lane, rr, 16 * w4 + u, pw);
+        stage_c(runs, tlen_of(c_begin), j0, u, wx6_perm32(8 * u));
+        split_b(runs, bw);
+        write_bt(bw, j0, u);
+        load_runs_x6(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u);
+    }
 
     // The segment's start state S_seg from Pass B (its Pass A segment is the
     // one the walk segment starts at). R[n][pp], n = 16 nb + 4 q + r, from the
@@ -212,13 +285,13 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 
     __bf16* const sMh = sB + hw * PL_M;
 
-    // Four barriers per chunk: (1) staging done; (2) every wave's G1 has read
-    // B; (3) M written into B's region; (4) G2 has read M (the next chunk's
-    // staging overwrites it).
+    // Four barriers per chunk: (1) the chunk's planes and records are staged;
+    // (2) G1 and G3 are done with B and C; (3) M is written (in B's region)
+    // and G4 is done with B^T; (4) G2 is done with M.
     for (int c = c_begin; c < c_end; ++c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
-        const int tlen = min(HELIX_CS, p.n_tok - t0);
-        // On the last chunk the same chunk is loaded again: no branch.
+        const int tlen = tlen_of(c);
+        // On the last chunk the next chunk is this one again: no branch.
         const int cn = min(c + 1, c_end - 1);
         // Lane-derived indices, formed anew in every chunk: hoisted out of the
         // loop, the LDS addresses made from them would not fit the registers.
@@ -229,54 +302,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         const int cpos = wx6_perm32(8 * u);    // K position of 8u; 8u + 4 sits 8 further
         const int pp = 16 * w4 + c16;          // this lane's P column in the slab
 
-        // ---- C, B and B^T planes -------------------------------------------
-        // C is zeroed past tlen and d_state, which is all G1 and G3 need; B
-        // rows past tlen only meet dt = 0 columns in G2 and G4.
-        {
-            unsigned bw[2][3][4];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int j = j0 + k;
-                const unsigned keep = ~(unsigned)(((tlen - 1 - j) | (N - 1 - 8 * u)) >> 31);
-                float vb[8], vc[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    vb[e] = as_f32(runs.b[k][e >> 2][e & 3]);
-                    vc[e] = as_f32(runs.c[k][e >> 2][e & 3] & keep);
-                }
-                u32x2 cq[3][2], bq[3][2];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    unsigned c0, c1, c2;
-                    split3_pair(vc[2 * e], vc[2 * e + 1], c0, c1, c2);
-                    split3_pair(vb[2 * e], vb[2 * e + 1], bw[k][0][e], bw[k][1][e], bw[k][2][e]);
-                    cq[0][e >> 1][e & 1] = c0;
-                    cq[1][e >> 1][e & 1] = c1;
-                    cq[2][e >> 1][e & 1] = c2;
-                }
-#pragma unroll
-                for (int pl = 0; pl < 3; ++pl) {
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        bq[pl][hh] = u32x2{bw[k][pl][2 * hh], bw[k][pl][2 * hh + 1]};
-                        const int pos = cpos + 8 * hh;
-                        const int off = x6_off<HELIX_CS, NCH>(pl, j, pos >> 3) + (pos & 7);
-                        *reinterpret_cast<u32x2*>(&sC[off]) = cq[pl][hh];
-                        *reinterpret_cast<u32x2*>(&sB[off]) = bq[pl][hh];
-                    }
-                }
-            }
-            // B^T[n][j0 .. j0 + 1], n = 8u + e: the halves of rows j0 and j0 + 1.
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
-                    const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-                    *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
-                }
-        }
-        load_runs_x6(runs, p, B_g, C_g, cn, N, j0, u);
+        write_b(bw, j0, cpos);
 
         // ---- decay records of the two heads --------------------------------
         if (w4 == 0) {
@@ -305,6 +331,10 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
                 for (int k = 0; k < 4; ++k) xb[s][4 * h4 + k] = d4[k] * st.x[8 * s + 4 * h4 + k];
             }
+        // The scheduling fences keep each prefetch's loads after the last use
+        // of the registers they fill, and each staging step after the barrier
+        // that frees its LDS: hoisted, they wait on loads still in flight.
+        __builtin_amdgcn_sched_barrier(0);
         load_stage_x6(st, p, rec_h, x_h, cn, lane, q, pp, pw);
 
         // ---- G1: D[j][t] = (B C^T) of blocks idx = wave, wave + 8 -----------
@@ -327,25 +357,35 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         }
 
         // ---- G3: y = exp(Lcum_t) . (C R), R the state before this chunk -----
+        // Products (s, tb) in order; the C planes of a product are read PF
+        // products ahead, and R's split for the next K step during this one.
         f32x4 acc[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        {
+            auto split_r = [&](int s, bf16x8 (&rp)[3]) {
+                float rv[8];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            float rv[8];
+                for (int e = 0; e < 4; ++e) {
+                    rv[e] = R[2 * s][e];
+                    rv[4 + e] = R[2 * s + 1][e];
+                }
+                wx6_split8(rv, rp);
+            };
+            constexpr int NI = 4 * KS;
+            bf16x8 cv[PF + 1][3], rp[2][3];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                rv[e] = R[2 * s][e];
-                rv[4 + e] = R[2 * s + 1][e];
-            }
-            bf16x8 rp[3];
-            wx6_split8(rv, rp);
+            for (int k = 0; k < PF; ++k) x6_read<HELIX_CS, NCH>(sC, 16 * (k % 4) + c16, 4 * (k / 4) + q, cv[k]);
+            split_r(0, rp[0]);
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                bf16x8 cv[3];
-                x6_read<HELIX_CS, NCH>(sC, 16 * tb + c16, 4 * s + q, cv);
-                acc[tb] = wx6_mfma(cv, rp, acc[tb]);
-                if (tb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+            for (int it = 0; it < NI; ++it) {
+                const int s = it / 4, tb = it % 4;
+                const int nx = it + PF;
+                if (nx < NI) x6_read<HELIX_CS, NCH>(sC, 16 * (nx % 4) + c16, 4 * (nx / 4) + q, cv[nx % (PF + 1)]);
+                if (tb == 1 && s + 1 < KS) split_r(s + 1, rp[(s + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                acc[tb] = wx6_mfma(cv[it % (PF + 1)], rp[s & 1], acc[tb]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
 #pragma unroll
@@ -354,7 +394,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[tb][r] *= e4[r];
         }
-        __syncthreads();   // (2) B's rows are free
+        __syncthreads();   // (2)
 
         // ---- M[t][j] = (C B^T)[t][j] exp(Lcum_t - Lcum_j), j <= t, per head --
 #pragma unroll
@@ -388,30 +428,47 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
             }
         }
 
+        __builtin_amdgcn_sched_barrier(0);
+        stage_c(runs, tlen_of(cn), j0, u, cpos);
+
         // ---- G4: R <- exp(L_end) R + B^T . (decay dt x) (after G3 used R) ---
+        // Products (s, nb) in order, B^T's planes read PF products ahead.
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) R[nb] *= a_c;
+        {
+            auto split_x = [&](int s, bf16x8 (&xp)[3]) {
+                float xs[8];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            float xs[8];
+                for (int h4 = 0; h4 < 2; ++h4) {
+                    const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sSd[hw][32 * s + 8 * q + 4 * h4]);
 #pragma unroll
-            for (int h4 = 0; h4 < 2; ++h4) {
-                const f32x4 s4 = *reinterpret_cast<const f32x4*>(&sSd[hw][32 * s + 8 * q + 4 * h4]);
+                    for (int k = 0; k < 4; ++k) xs[4 * h4 + k] = s4[k] * xb[s][4 * h4 + k];
+                }
+                wx6_split8(xs, xp);
+            };
+            constexpr int NI = 2 * NB;
+            bf16x8 bt[PF + 1][3], xp[2][3];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) xs[4 * h4 + k] = s4[k] * xb[s][4 * h4 + k];
-            }
-            bf16x8 xp[3];
-            wx6_split8(xs, xp);
+            for (int k = 0; k < PF; ++k) x6_read<NP, 8>(sBt, 16 * (k % NB) + c16, 4 * (k / NB) + q, bt[k]);
+            split_x(0, xp[0]);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                bf16x8 bt[3];
-                x6_read<NP, 8>(sBt, 16 * nb + c16, 4 * s + q, bt);
-                R[nb] = wx6_mfma(bt, xp, R[nb]);
-                // Operand reads run at most two tiles ahead of the MFMAs.
-                if (nb % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+            for (int it = 0; it < NI; ++it) {
+                const int s = it / NB, nb = it % NB;
+                const int nx = it + PF;
+                if (nx < NI) x6_read<NP, 8>(sBt, 16 * (nx % NB) + c16, 4 * (nx / NB) + q, bt[nx % (PF + 1)]);
+                if (nb == 1 && s == 0) split_x(1, xp[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                R[nb] = wx6_mfma(bt[it % (PF + 1)], xp[s], R[nb]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __syncthreads();   // (3) M complete
+        __syncthreads();   // (3)
+
+        __builtin_amdgcn_sched_barrier(0);
+        split_b(runs, bw);
+        write_bt(bw, j0, u);
+        __builtin_amdgcn_sched_barrier(0);
+        load_runs_x6(runs, p, B_g, C_g, min(c + 2, c_end - 1), N, j0, u);
 
         // ---- G2: y += M . dtX (t block tb needs j < 16 (tb + 1)) -----------
         // K step s covers j blocks 2s and 2s + 1; for tb = 0 and 2 the second
