@@ -47,16 +47,25 @@ HELIX_DEV f32x4 zero4() {
 
 // One chunk's global inputs for this thread, loaded for chunk c+1 while chunk
 // c runs: dt of token `lane`, x of tokens tid / 16 + 16 i at channel tid % 16
-// of the block, and the C and B rows wave + 4 i at columns lane + 64 m. Every
+// of the block, and the wave's C and B rows wave + 4 r (r = 0..15). Every
 // address is clamped in bounds; the masks are applied when the registers are
-// staged into LDS.
+// staged into LDS. With fp32 storage a lane loads four consecutive state
+// indices per row at a time (16-byte loads, a quarter of the instructions):
+// load i covers rows r = i RPI + lane / LPR, indices 4 (lane % LPR) .. +3;
+// with 16-bit storage, one index per row: columns lane + 64 m.
 template <int NP, typename IO>
 struct StageS {
     typedef typename IoWord<IO>::type W;    // x, C, B in storage form
+    static constexpr bool WIDE = sizeof(IO) == 4;
+    static constexpr int LPR = NP / 4;      // lanes per row (WIDE)
+    static constexpr int RPI = 64 / LPR;    // rows per load (WIDE)
+    static constexpr int NW = WIDE ? 16 / RPI : 1;
+    static constexpr int NN = WIDE ? 1 : 16;
     float dtraw;
     W x[4];
-    W c[16][NP / 64];
-    W b[16][NP / 64];
+    u32x4 cw[NW], bw[NW];
+    W c[NN][NP / 64];
+    W b[NN][NP / 64];
 };
 
 template <int NP, typename IO>
@@ -76,7 +85,24 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScan
         const int jr = min((tid >> 4) + 16 * i, tlen - 1);
         st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
     }
-    load_cb_rows<NP, IO>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
+    if constexpr (StageS<NP, IO>::WIDE) {
+        constexpr int LPR = StageS<NP, IO>::LPR, RPI = StageS<NP, IO>::RPI;
+        const int N = p.d_state;
+        const int sc0 = (int)p.s_c[0], sb0 = (int)p.s_b[0];
+        const helix_rsrc rc = make_rsrc(b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0],
+                                        ((tlen - 1) * sc0 + N) * 4u);
+        const helix_rsrc rb = make_rsrc(b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0],
+                                        ((tlen - 1) * sb0 + N) * 4u);
+        const int n0 = min(4 * (lane % LPR), N - 4);   // d_state % 8 == 0: four indices all in or all out
+#pragma unroll
+        for (int i = 0; i < StageS<NP, IO>::NW; ++i) {
+            const int jr = min(wave + 4 * (i * RPI + lane / LPR), tlen - 1);
+            st.cw[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4, 0, 0);
+            st.bw[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4, 0, 0);
+        }
+    } else {
+        load_cb_rows<NP, IO>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
+    }
 }
 
 // G1 tile idx (0..9) of the causal 4 x 4 grid of 16 x 16 tiles, row-major
@@ -196,14 +222,31 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             const int j = (tid >> 4) + 16 * i;
             sX[j * 16 + (tid & 15)] = keep_if_lt(__shfl(dtv, j, 64) * io_widen<IO>(st.x[i]), tid & 15, pw);
         }
+        if constexpr (StageS<NP, IO>::WIDE) {
+            constexpr int LPR = StageS<NP, IO>::LPR, RPI = StageS<NP, IO>::RPI;
+            const int n = 4 * (lane % LPR);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int j = wave + 4 * i;
+            for (int i = 0; i < StageS<NP, IO>::NW; ++i) {
+                const int j = wave + 4 * (i * RPI + lane / LPR);
+                f32x4 cv, bv;
 #pragma unroll
-            for (int m = 0; m < NP / 64; ++m) {
-                const int n = lane + 64 * m;
-                sC[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.c[i][m]), j, tlen, n, N);
-                sB[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.b[i][m]), j, tlen, n, N);
+                for (int e = 0; e < 4; ++e) {
+                    cv[e] = keep_if_lt2(as_f32(st.cw[i][e]), j, tlen, n, N);
+                    bv[e] = keep_if_lt2(as_f32(st.bw[i][e]), j, tlen, n, N);
+                }
+                *reinterpret_cast<f32x4*>(&sC[j * RSC + n]) = cv;
+                *reinterpret_cast<f32x4*>(&sB[j * RSC + n]) = bv;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = wave + 4 * i;
+#pragma unroll
+                for (int m = 0; m < NP / 64; ++m) {
+                    const int n = lane + 64 * m;
+                    sC[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.c[i][m]), j, tlen, n, N);
+                    sB[j * RSC + n] = keep_if_lt2(io_widen<IO>(st.b[i][m]), j, tlen, n, N);
+                }
             }
         }
         __syncthreads();
