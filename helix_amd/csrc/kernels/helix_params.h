@@ -69,6 +69,10 @@
  * head per workgroup, two workgroups per CU, measured slower at config 2:
  * the B and C staging is then done for every head). */
 #define HELIX_WALK16_HPW(np) HELIX_WALK_HPW(np)
+/* Waves per workgroup of the scalar-A single-pass kernels: eight up to
+ * d_state 128; four at d_state 256, whose registers do not fit two waves per
+ * SIMD (the diagonal-A kernels run four). */
+#define HELIX_1PASS_WAVES(np) ((np) <= 128 ? 8 : 4)
 /* Items ((head, P slab) pairs of one B/C group) per workgroup of the
  * head-block Pass A (pass_a_hb.hip), two waves each, d_state <= 128. */
 #define HELIX_HB 4

@@ -71,12 +71,12 @@ __device__ __forceinline__ void load_stage_c(StageC<NP, SL, REC>& st, const Heli
 }
 
 // Rows of C and B of one (seq, chunk, group) for this thread: row
-// wave + 4 i, columns lane + 64 m, clamped in bounds (masked when staged).
-// IO is the caller's storage type of B and C; the values stay in storage
-// form (io_widen at the use).
-template <int NP, typename IO = float>
-__device__ __forceinline__ void load_cb_rows(typename IoWord<IO>::type (&vc)[16][NP / 64],
-                                             typename IoWord<IO>::type (&vb)[16][NP / 64],
+// wave + NWV i (NWV waves), columns lane + 64 m, clamped in bounds (masked
+// when staged). IO is the caller's storage type of B and C; the values stay
+// in storage form (io_widen at the use).
+template <int NP, typename IO = float, int NWV = 4>
+__device__ __forceinline__ void load_cb_rows(typename IoWord<IO>::type (&vc)[HELIX_CS / NWV][NP / 64],
+                                             typename IoWord<IO>::type (&vb)[HELIX_CS / NWV][NP / 64],
                                              const HelixScanParams& p, const HelixScanBuffers& b,
                                              int seq, int g, int t0, int tlen, int lane, int wave) {
     const int N = p.d_state;
@@ -88,8 +88,8 @@ __device__ __forceinline__ void load_cb_rows(typename IoWord<IO>::type (&vc)[16]
     const helix_rsrc rb = make_rsrc(B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0],
                                     ((tlen - 1) * sb0 + N) * (unsigned)sizeof(IO));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int jr = min(wave + 4 * i, tlen - 1);
+    for (int i = 0; i < HELIX_CS / NWV; ++i) {
+        const int jr = min(wave + NWV * i, tlen - 1);
 #pragma unroll
         for (int m = 0; m < NP / 64; ++m) {
             const int nc = min(lane + 64 * m, N - 1);

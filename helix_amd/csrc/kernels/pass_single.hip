@@ -46,30 +46,32 @@ HELIX_DEV f32x4 zero4() {
 }
 
 // One chunk's global inputs for this thread, loaded for chunk c+1 while chunk
-// c runs: dt of token `lane`, x of tokens tid / 16 + 16 i at channel tid % 16
-// of the block, and the wave's C and B rows wave + 4 r (r = 0..15). Every
+// c runs: dt of token `lane`, x of tokens tid / 16 + 4 NWV i at channel tid % 16
+// of the block, and the wave's C and B rows wave + NWV r (NWV waves). Every
 // address is clamped in bounds; the masks are applied when the registers are
 // staged into LDS. With fp32 storage a lane loads four consecutive state
 // indices per row at a time (16-byte loads, a quarter of the instructions):
 // load i covers rows r = i RPI + lane / LPR, indices 4 (lane % LPR) .. +3;
 // with 16-bit storage, one index per row: columns lane + 64 m.
-template <int NP, typename IO>
+template <int NP, typename IO, int NWV>
 struct StageS {
     typedef typename IoWord<IO>::type W;    // x, C, B in storage form
     static constexpr bool WIDE = sizeof(IO) == 4;
+    static constexpr int RPW = HELIX_CS / NWV;   // rows per wave
     static constexpr int LPR = NP / 4;      // lanes per row (WIDE)
     static constexpr int RPI = 64 / LPR;    // rows per load (WIDE)
-    static constexpr int NW = WIDE ? 16 / RPI : 1;
-    static constexpr int NN = WIDE ? 1 : 16;
+    static constexpr int NW = WIDE ? RPW / RPI : 1;
+    static constexpr int NN = WIDE ? 1 : RPW;
+    static constexpr int NX = 16 / NWV;     // x values per thread
     float dtraw;
-    W x[4];
+    W x[NX];
     u32x4 cw[NW], bw[NW];
     W c[NN][NP / 64];
     W b[NN][NP / 64];
 };
 
-template <int NP, typename IO>
-__device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScanParams& p,
+template <int NP, typename IO, int NWV>
+__device__ __forceinline__ void load_stage_s(StageS<NP, IO, NWV>& st, const HelixScanParams& p,
                                              const HelixScanBuffers& b, const float* __restrict__ dt_h,
                                              const IO* __restrict__ x_h, int seq, int g, int t0,
                                              int tlen, int pw, int lane, int wave) {
@@ -81,12 +83,12 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScan
     const int tid = 64 * wave + lane;
     const int xc = min(tid & 15, pw - 1) * sx2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int jr = min((tid >> 4) + 16 * i, tlen - 1);
+    for (int i = 0; i < StageS<NP, IO, NWV>::NX; ++i) {
+        const int jr = min((tid >> 4) + 4 * NWV * i, tlen - 1);
         st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
     }
-    if constexpr (StageS<NP, IO>::WIDE) {
-        constexpr int LPR = StageS<NP, IO>::LPR, RPI = StageS<NP, IO>::RPI;
+    if constexpr (StageS<NP, IO, NWV>::WIDE) {
+        constexpr int LPR = StageS<NP, IO, NWV>::LPR, RPI = StageS<NP, IO, NWV>::RPI;
         const int N = p.d_state;
         const int sc0 = (int)p.s_c[0], sb0 = (int)p.s_b[0];
         const helix_rsrc rc = make_rsrc(b.C + seq * p.seq_c + g * p.s_c[1] + (long long)t0 * p.s_c[0],
@@ -95,13 +97,13 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO>& st, const HelixScan
                                         ((tlen - 1) * sb0 + N) * 4u);
         const int n0 = min(4 * (lane % LPR), N - 4);   // d_state % 8 == 0: four indices all in or all out
 #pragma unroll
-        for (int i = 0; i < StageS<NP, IO>::NW; ++i) {
-            const int jr = min(wave + 4 * (i * RPI + lane / LPR), tlen - 1);
+        for (int i = 0; i < StageS<NP, IO, NWV>::NW; ++i) {
+            const int jr = min(wave + NWV * (i * RPI + lane / LPR), tlen - 1);
             st.cw[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4, 0, 0);
             st.bw[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4, 0, 0);
         }
     } else {
-        load_cb_rows<NP, IO>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
+        load_cb_rows<NP, IO, NWV>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
     }
 }
 
@@ -121,10 +123,18 @@ HELIX_DEV int tri_jb(int idx) {
 // exceed 1: C rows by exp(A_n cs_t) (G3), B rows by exp(A_n (cs_end - cs_j))
 // (G4), and the carried state by exp(A_n cs_end) per state index.
 // IO: the caller's storage type of x, B, C and y (dt, A and the states are fp32).
-template <int NP, bool DIAG, typename IO = float>
+//
+// NWV = 8 waves (d_state <= 128, scalar A): waves 0..3 produce y (G3 and G2 of
+// t block `wave`), waves 4..7 carry the state (G4 on tiles NTW sw .. +NTW-1,
+// sw = wave - 4), and G1's ten blocks go to the state waves (two each) and to
+// waves 0 and 1 (one each), which balances each SIMD's two waves (w, w + 4).
+// Two waves per SIMD hide each other's staging, preamble and load latencies.
+// NWV = 4 (diagonal A, d_state 256): every wave does all four parts.
+template <int NP, bool DIAG, typename IO = float, int NWV = 4>
 __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(NWV == 4 || (NWV == 8 && !DIAG), "eight waves on the scalar-A path only");
     constexpr int NT  = NP / 16;           // 16-row state tiles
-    constexpr int NTW = NT / 4;            // state tiles wave w advances: NTW w .. NTW w + NTW - 1
+    constexpr int NTW = NT / 4;            // state tiles state wave sw advances: NTW sw .. NTW sw + NTW - 1
     constexpr int RSC = NP + 4;            // C and B rows
     constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
     constexpr int RSR = NP + 4;            // state rows, one per channel of the block
@@ -143,6 +153,19 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     const int lane = threadIdx.x & 63, wave = wave_uniform();
     const int l16 = lane & 15, g4 = lane >> 4;
     const int tid = (int)threadIdx.x;
+    const bool ywave = wave < 4;           // produces y (G3, G2)
+    const bool swave = wave >= NWV - 4;    // carries state tiles (G4)
+    const int sw = wave - (NWV - 4);       // its state-wave index
+    // G1 block q of this wave (wave-uniform), or -1.
+    auto g1_idx = [&](int q) -> int {
+        if constexpr (NWV == 4) {
+            const int idx = wave + 4 * q;
+            return idx < 10 ? idx : -1;
+        } else {
+            if (swave) return q < 2 ? sw + 4 * q : -1;
+            return (q == 0 && wave < 2) ? 8 + wave : -1;
+        }
+    };
 
     // 1-D grid over (seq, head, P slab, 16-channel block), block fastest in
     // the logical order, so a head's blocks and a group's heads (which read
@@ -158,11 +181,11 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     const int p0 = slab * HELIX_HD + 16 * pb;          // the block's first channel
     const int pw = min(16, p.head_dim - p0);           // its channels
     if (pw <= 0) return;   // a block past a short last slab: uniform, before any barrier
-    const int tb = wave;   // the t block of y this wave produces
+    const int tb = wave & 3;   // the t block of y this wave produces (y waves)
 
     const float A_h = DIAG ? 0.0f : b.A[(long long)h * p.s_a];
     if constexpr (DIAG) {
-        for (int n = tid; n < NP; n += HELIX_WG)
+        for (int n = tid; n < NP; n += 64 * NWV)
             sA2[n] = n < N ? (double)b.A[(long long)h * p.s_a + n] * 1.4426950408889634074 : 0.0;
     }
     const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
@@ -170,35 +193,38 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                                  (long long)p0 * p.s_x[2];
 
     // State entering the sequence, s0[ids[seq]] in the caller's [P][N] rows
-    // (s_s[1] == d_state): register r of tile i holds n = 16 (NTW wave + i) +
+    // (s_s[1] == d_state): register r of tile i holds n = 16 (NTW sw + i) +
     // 4 g4 + r at channel p0 + l16. Channels past the block read 0 through the
     // range check; n past d_state is masked (it would read the next row).
+    // Waves that carry no state load an empty range.
     const int src = p.has_ids ? b.ids[seq] : seq;
     f32x4 R[NTW];
     {
         const helix_rsrc rs = make_rsrc(b.s0 + src * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
-                                        (unsigned)(pw * N) * 4u);
+                                        swave ? (unsigned)(pw * N) * 4u : 0u);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int n = 16 * (NTW * wave + i) + 4 * g4 + r;
+                const int n = 16 * (NTW * max(sw, 0) + i) + 4 * g4 + r;
                 R[i][r] = keep_if_lt(buf_f32(rs, (l16 * N + n) * 4, 0), n, N);
             }
     }
     // Every wave's G3 reads the whole state: it is shared through sR, written
     // by the wave that advances each tile.
     auto publish_state = [&]() {
+        if (swave) {
 #pragma unroll
-        for (int i = 0; i < NTW; ++i)
-            *reinterpret_cast<f32x4*>(&sR[l16 * RSR + 16 * (NTW * wave + i) + 4 * g4]) = R[i];
+            for (int i = 0; i < NTW; ++i)
+                *reinterpret_cast<f32x4*>(&sR[l16 * RSR + 16 * (NTW * sw + i) + 4 * g4]) = R[i];
+        }
     };
     publish_state();
 
     const int n_ch = (p.n_tok + HELIX_CS - 1) / HELIX_CS;
     const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
-    StageS<NP, IO> st;
-    load_stage_s<NP, IO>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
+    StageS<NP, IO, NWV> st;
+    load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
 
     for (int c = 0; c < n_ch; ++c) {
         const int t0   = c * HELIX_CS;
@@ -218,16 +244,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = (tid >> 4) + 16 * i;
+        for (int i = 0; i < StageS<NP, IO, NWV>::NX; ++i) {
+            const int j = (tid >> 4) + 4 * NWV * i;
             sX[j * 16 + (tid & 15)] = keep_if_lt(__shfl(dtv, j, 64) * io_widen<IO>(st.x[i]), tid & 15, pw);
         }
-        if constexpr (StageS<NP, IO>::WIDE) {
-            constexpr int LPR = StageS<NP, IO>::LPR, RPI = StageS<NP, IO>::RPI;
+        if constexpr (StageS<NP, IO, NWV>::WIDE) {
+            constexpr int LPR = StageS<NP, IO, NWV>::LPR, RPI = StageS<NP, IO, NWV>::RPI;
             const int n = 4 * (lane % LPR);
 #pragma unroll
-            for (int i = 0; i < StageS<NP, IO>::NW; ++i) {
-                const int j = wave + 4 * (i * RPI + lane / LPR);
+            for (int i = 0; i < StageS<NP, IO, NWV>::NW; ++i) {
+                const int j = wave + NWV * (i * RPI + lane / LPR);
                 f32x4 cv, bv;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -239,8 +265,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int j = wave + 4 * i;
+            for (int i = 0; i < StageS<NP, IO, NWV>::RPW; ++i) {
+                const int j = wave + NWV * i;
 #pragma unroll
                 for (int m = 0; m < NP / 64; ++m) {
                     const int n = lane + 64 * m;
@@ -253,7 +279,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
         // The next chunk's inputs travel while this one runs on the MFMA pipe.
         if (c + 1 < n_ch)
-            load_stage_s<NP, IO>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
+            load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
                                  min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
 
         // B operands of G2 (dtX) and G4 (dtX scaled by exp(L_end - Lcum_j); with
@@ -316,8 +342,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
             mt[q] = zero4();
-            const int idx = wave + 4 * q;
-            if (!DIAG && idx < 10) {
+            const int idx = g1_idx(q);
+            if (!DIAG && idx >= 0) {
                 const int gtb = tri_tb(idx), jb = tri_jb(idx);
                 f32x4 acc = zero4();
 #pragma unroll 4
@@ -341,6 +367,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
         // ---- G3: y = exp(Lcum_t) . (C S) for this wave's t block; S from sR --
         f32x4 ya = zero4();
+        if (ywave) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * nt + 4 * g4]);
@@ -352,14 +379,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
             for (int r = 0; r < 4; ++r) ya[r] *= sE[16 * tb + 4 * g4 + r];
         }
+        }
 
         // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x), own tiles --
+        if (swave) {
         if constexpr (DIAG) {
 #pragma unroll
             for (int i = 0; i < NTW; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    R[i][r] *= __builtin_amdgcn_exp2f((float)(sA2[16 * (NTW * wave + i) + 4 * g4 + r] * lend));
+                    R[i][r] *= __builtin_amdgcn_exp2f((float)(sA2[16 * (NTW * sw + i) + 4 * g4 + r] * lend));
         } else {
             const float a_c = expf((float)lend);
 #pragma unroll
@@ -370,7 +399,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             const int j = 4 * s + g4;
 #pragma unroll
             for (int i = 0; i < NTW; ++i)
-                R[i] = mfma16(sB[j * RSC + 16 * (NTW * wave + i) + l16], xs[s], R[i]);
+                R[i] = mfma16(sB[j * RSC + 16 * (NTW * sw + i) + l16], xs[s], R[i]);
+        }
         }
         // Every wave is done with the B rows and with sR: M takes over B's
         // rows, and the advanced state replaces the old one.
@@ -378,8 +408,8 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         if constexpr (!DIAG) {
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
-                const int idx = wave + 4 * q;
-                if (idx < 10) {
+                const int idx = g1_idx(q);
+                if (idx >= 0) {
                     const int gtb = tri_tb(idx), jb = tri_jb(idx);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) sM[(16 * gtb + 4 * g4 + r) * RSM + 16 * jb + l16] = mt[q][r];
@@ -390,6 +420,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         __syncthreads();
 
         // ---- G2: y += M dtX over the causal K range of this t block --------
+        if (ywave) {
         for (int s = 0; s < 4 * (tb + 1); ++s)
             ya = mfma16(sM[(16 * tb + l16) * RSM + 4 * s + g4], xb[s], ya);
 
@@ -406,36 +437,39 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 io_store<IO, HELIX_NT>(ry, ya[r], store_off_if_lt((t * sy0 + l16 * sy2) * ES, t, tlen, l16, pw), 0);
             }
         }
+        }
         __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX
     }
 
-    // Final state to s1[seq], same register layout as the s0 read.
-    const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * N, (unsigned)(pw * N) * 4u);
+    // Final state to s1[seq], same register layout as the s0 read (the state
+    // waves; the others store to an empty range).
+    const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
+                                    swave ? (unsigned)(pw * N) * 4u : 0u);
 #pragma unroll
     for (int i = 0; i < NTW; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int n = 16 * (NTW * wave + i) + 4 * g4 + r;
+            const int n = 16 * (NTW * max(sw, 0) + i) + 4 * g4 + r;
             __builtin_amdgcn_raw_buffer_store_b32(as_u32(R[i][r]), ro,
                                                   store_off_if_lt((l16 * N + n) * 4, n, N, l16, pw), 0, 0);
         }
 }
 
 #define HELIX_SCAN_1PASS(NP)                                                                    \
-    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_f32_n##NP(           \
+    extern "C" __global__ __launch_bounds__(64 * HELIX_1PASS_WAVES(NP)) void helix_scan_1pass_f32_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        scan_1pass_impl<NP, false>(p, b);                                                       \
+        scan_1pass_impl<NP, false, float, HELIX_1PASS_WAVES(NP)>(p, b);                         \
     }
 
 // 16-bit storage of x, B, C and y (io_dtype BF16 / F16), fp32 compute.
 #define HELIX_SCAN_1PASS_IO(NP)                                                                 \
-    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_bf16io_n##NP(        \
+    extern "C" __global__ __launch_bounds__(64 * HELIX_1PASS_WAVES(NP)) void helix_scan_1pass_bf16io_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        scan_1pass_impl<NP, false, __bf16>(p, b);                                               \
+        scan_1pass_impl<NP, false, __bf16, HELIX_1PASS_WAVES(NP)>(p, b);                        \
     }                                                                                           \
-    extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_scan_1pass_f16io_n##NP(         \
+    extern "C" __global__ __launch_bounds__(64 * HELIX_1PASS_WAVES(NP)) void helix_scan_1pass_f16io_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                \
-        scan_1pass_impl<NP, false, _Float16>(p, b);                                             \
+        scan_1pass_impl<NP, false, _Float16, HELIX_1PASS_WAVES(NP)>(p, b);                      \
     }
 
 #define HELIX_SCAN_1PASS_DIAG(NP)                                                               \

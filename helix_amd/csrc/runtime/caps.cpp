@@ -98,6 +98,7 @@ struct TraitTable {
                 t.mfma_a = t.mfma_c = "v_mfma_f32_16x16x4_f32";
                 t.np = kNps[k];
                 t.k_single = kernel(std::string("helix_scan_1pass_") + (io == 0 ? "f32_" : kIoTag[io]) + "n" + np);
+                t.single_threads = 64 * HELIX_1PASS_WAVES(kNps[k]);
             }
             if (k < 2) {
                 HelixMatmulTraits& t = diag[k];
@@ -107,6 +108,7 @@ struct TraitTable {
                 t.mfma_a = t.mfma_c = "v_mfma_f32_16x16x4_f32";
                 t.np = kNps[k];
                 t.k_single = kernel("helix_scan_1pass_diag_f32_n" + np);
+                t.single_threads = HELIX_WG;
             }
             {
                 HelixMatmulTraits& t = f32[k];

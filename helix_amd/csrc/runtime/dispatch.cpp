@@ -119,8 +119,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             return HELIX_ERR_NO_DEVICE;
         }
         void* args[] = {&params, &bufs};
-        const hipError_t e = hipModuleLaunchKernel(f1, (unsigned)n_wg, 1, 1, HELIX_WG, 1, 1, 0, stream, args,
-                                                   nullptr);
+        const hipError_t e = hipModuleLaunchKernel(f1, (unsigned)n_wg, 1, 1, (unsigned)tr.single_threads, 1, 1, 0,
+                                                   stream, args, nullptr);
         if (prev >= 0 && prev != ctx->device) (void)hipSetDevice(prev);
         if (e != hipSuccess) {
             (void)hipGetLastError();

@@ -65,6 +65,7 @@ struct HelixMatmulTraits {
     // caps.mm:18-25). Set only in the single-pass trait set, where the three
     // pass names are null.
     const char*   k_single;
+    int           single_threads;  // its workgroup size (64 x waves)
     // Heads per workgroup of a walking Pass C; 0 means HELIX_WALK_HPW(np).
     int           walk_hpw;
     // Pass A writes bf16 copies of B and C that the walking Pass C reads.
