@@ -40,6 +40,17 @@ HELIX_DEV f32x4 mfma16(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Six 16 x 16 x 32 products of split operands a[3] x b[3], smallest terms first.
+HELIX_DEV f32x4 mfma16_x6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+    return acc;
+}
+
 HELIX_DEV f32x4 zero4() {
     f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     return z;
@@ -139,10 +150,20 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
     constexpr int RSR = NP + 4;            // state rows, one per channel of the block
     static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
-    __shared__ __attribute__((aligned(16))) float sC[HELIX_CS * RSC];
+    // X6 (fp32 storage, scalar A, d_state <= 128): G1 and G3 on bf16x6
+    // 16x16x32 products, from C and B staged as three bf16 planes each and the
+    // state shared as planes; G4 and G2 stay on fp32 MFMA (B's fp32 rows).
+    constexpr bool X6 = !DIAG && NP <= 128 && sizeof(IO) == 4;
+    constexpr int NCH = NP / 8;            // 16-byte chunks per plane row (X6)
+    constexpr int PLC = X6 ? 3 * HELIX_CS * NP : 8;   // C or B planes, bf16 elements
+    constexpr int PLR = X6 ? 3 * 16 * NP : 8;         // state planes
+    __shared__ __attribute__((aligned(16))) float sC[X6 ? 4 : HELIX_CS * RSC];
     __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSC];
     __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * 16];   // dtX[token][channel]
-    __shared__ __attribute__((aligned(16))) float sR[16 * RSR];        // S[channel][state index]
+    __shared__ __attribute__((aligned(16))) float sR[X6 ? 4 : 16 * RSR];   // S[channel][state index]
+    __shared__ __attribute__((aligned(16))) __bf16 sCp[PLC];          // C[t][n] planes (X6)
+    __shared__ __attribute__((aligned(16))) __bf16 sBp[PLC];          // B[j][n] planes (X6)
+    __shared__ __attribute__((aligned(16))) __bf16 sRp[PLR];          // S[p][n] planes (X6)
     __shared__ double sL[HELIX_CS];        // Lcum_t (scalar A) or cs_t (DIAG), fp64
     __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
     __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
@@ -215,8 +236,20 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     auto publish_state = [&]() {
         if (swave) {
 #pragma unroll
-            for (int i = 0; i < NTW; ++i)
-                *reinterpret_cast<f32x4*>(&sR[l16 * RSR + 16 * (NTW * sw + i) + 4 * g4]) = R[i];
+            for (int i = 0; i < NTW; ++i) {
+                const int n = 16 * (NTW * sw + i) + 4 * g4;
+                if constexpr (X6) {
+                    unsigned w[2][3];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) split3_pair(R[i][2 * e], R[i][2 * e + 1], w[e][0], w[e][1], w[e][2]);
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        *reinterpret_cast<u32x2*>(&sRp[x6_off<16, NCH>(pl, l16, n >> 3) + (n & 7)]) =
+                            u32x2{w[0][pl], w[1][pl]};
+                } else {
+                    *reinterpret_cast<f32x4*>(&sR[l16 * RSR + n]) = R[i];
+                }
+            }
         }
     };
     publish_state();
@@ -260,8 +293,23 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                     cv[e] = keep_if_lt2(as_f32(st.cw[i][e]), j, tlen, n, N);
                     bv[e] = keep_if_lt2(as_f32(st.bw[i][e]), j, tlen, n, N);
                 }
-                *reinterpret_cast<f32x4*>(&sC[j * RSC + n]) = cv;
                 *reinterpret_cast<f32x4*>(&sB[j * RSC + n]) = bv;
+                if constexpr (X6) {
+                    unsigned wc[2][3], wb[2][3];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        split3_pair(cv[2 * e], cv[2 * e + 1], wc[e][0], wc[e][1], wc[e][2]);
+                        split3_pair(bv[2 * e], bv[2 * e + 1], wb[e][0], wb[e][1], wb[e][2]);
+                    }
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl) {
+                        const int off = x6_off<HELIX_CS, NCH>(pl, j, n >> 3) + (n & 7);
+                        *reinterpret_cast<u32x2*>(&sCp[off]) = u32x2{wc[0][pl], wc[1][pl]};
+                        *reinterpret_cast<u32x2*>(&sBp[off]) = u32x2{wb[0][pl], wb[1][pl]};
+                    }
+                } else {
+                    *reinterpret_cast<f32x4*>(&sC[j * RSC + n]) = cv;
+                }
             }
         } else {
 #pragma unroll
@@ -346,12 +394,22 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             if (!DIAG && idx >= 0) {
                 const int gtb = tri_tb(idx), jb = tri_jb(idx);
                 f32x4 acc = zero4();
+                if constexpr (X6) {
+#pragma unroll
+                    for (int s = 0; s < NP / 32; ++s) {
+                        bf16x8 av[3], bv[3];
+                        x6_read<HELIX_CS, NCH>(sCp, 16 * gtb + l16, 4 * s + g4, av);
+                        x6_read<HELIX_CS, NCH>(sBp, 16 * jb + l16, 4 * s + g4, bv);
+                        acc = mfma16_x6(av, bv, acc);
+                    }
+                } else {
 #pragma unroll 4
                 for (int kb = 0; kb < NP / 16; ++kb) {
                     const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * gtb + l16) * RSC + 16 * kb + 4 * g4]);
                     const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sB[(16 * jb + l16) * RSC + 16 * kb + 4 * g4]);
 #pragma unroll
                     for (int s = 0; s < 4; ++s) acc = mfma16(a4[s], b4[s], acc);
+                }
                 }
                 const int j = 16 * jb + l16;
                 const double lj = sL[j];
@@ -368,12 +426,22 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         // ---- G3: y = exp(Lcum_t) . (C S) for this wave's t block; S from sR --
         f32x4 ya = zero4();
         if (ywave) {
+        if constexpr (X6) {
+#pragma unroll
+            for (int s = 0; s < NP / 32; ++s) {
+                bf16x8 av[3], rv[3];
+                x6_read<HELIX_CS, NCH>(sCp, 16 * tb + l16, 4 * s + g4, av);
+                x6_read<16, NCH>(sRp, l16, 4 * s + g4, rv);
+                ya = mfma16_x6(av, rv, ya);
+            }
+        } else {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sC[(16 * tb + l16) * RSC + 16 * nt + 4 * g4]);
             const f32x4 r4 = *reinterpret_cast<const f32x4*>(&sR[l16 * RSR + 16 * nt + 4 * g4]);
 #pragma unroll
             for (int s = 0; s < 4; ++s) ya = mfma16(a4[s], r4[s], ya);
+        }
         }
         if constexpr (!DIAG) {
 #pragma unroll
