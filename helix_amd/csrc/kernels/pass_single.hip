@@ -137,8 +137,9 @@ HELIX_DEV int tri_jb(int idx) {
 //
 // NWV = 8 waves (d_state <= 128, scalar A): waves 0..3 produce y (G3 and G2 of
 // t block `wave`), waves 4..7 carry the state (G4 on tiles NTW sw .. +NTW-1,
-// sw = wave - 4), and G1's ten blocks go to the state waves (two each) and to
-// waves 0 and 1 (one each), which balances each SIMD's two waves (w, w + 4).
+// sw = wave - 4), and G1's ten blocks go one to each state wave and the other
+// six to the y waves (two to waves 0 and 1), whose G3 and G2 are the lighter
+// part (per-phase cycle counts).
 // Two waves per SIMD hide each other's staging, preamble and load latencies.
 // NWV = 4 (diagonal A, d_state 256): every wave does all four parts.
 template <int NP, bool DIAG, typename IO = float, int NWV = 4>
@@ -183,8 +184,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             const int idx = wave + 4 * q;
             return idx < 10 ? idx : -1;
         } else {
-            if (swave) return q < 2 ? sw + 4 * q : -1;
-            return (q == 0 && wave < 2) ? 8 + wave : -1;
+            if (swave) return q == 0 ? sw : -1;                  // blocks 0..3
+            if (q == 0) return 4 + wave;                         // blocks 4..7
+            return (q == 1 && wave < 2) ? 8 + wave : -1;         // blocks 8, 9
         }
     };
 
