@@ -398,6 +398,35 @@ HELIX_DEV void x6_write8(__bf16* planes, int r, int c, const float* v) {
     *reinterpret_cast<u32x4*>(&planes[x6_off<ROWS, NCH>(2, r, c)]) = q2;
 }
 
+// Eight fp32 values as the three split planes of one MFMA operand.
+HELIX_DEV void x6_split8(const float (&v)[8], bf16x8 (&o)[3]) {
+    u32x4 q0, q1, q2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        unsigned w0, w1, w2;
+        split3_pair(v[2 * e], v[2 * e + 1], w0, w1, w2);
+        q0[e] = w0;
+        q1[e] = w1;
+        q2[e] = w2;
+    }
+    o[0] = __builtin_bit_cast(bf16x8, q0);
+    o[1] = __builtin_bit_cast(bf16x8, q1);
+    o[2] = __builtin_bit_cast(bf16x8, q2);
+}
+
+// LDS transpose read of 16-bit elements (ds_read_b64_tr_b16): every lane
+// names 8 bytes (four elements); lane l of each 16-lane group receives, as
+// element r (r = 0..3), element l % 4 of the 8 bytes named by lane
+// 4 r + l / 4 of its group. With lane 4 r + q naming row k_r, columns
+// c0 + 4 q .. c0 + 4 q + 3 of a row-major array, lane l gets column c0 + l of
+// rows k_0 .. k_3: a K-major operand read from rows that run along the other
+// index.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+HELIX_DEV u32x2 lds_read_tr16(const __bf16* p) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)p);
+    return __builtin_bit_cast(u32x2, v);
+}
+
 // Split eight fp32 values v[0..7] into NS bf16 planes (NS = 3: split3_pair,
 // NS = 2: split2_pair) and store them as chunk c of row r.
 template <int ROWS, int NS>

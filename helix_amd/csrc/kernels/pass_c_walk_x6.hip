@@ -47,22 +47,6 @@ HELIX_DEV f32x4 wx6_mfma(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x4 acc) 
     return acc;
 }
 
-// Eight fp32 values as the three split planes of one MFMA operand.
-HELIX_DEV void wx6_split8(const float (&v)[8], bf16x8 (&o)[3]) {
-    u32x4 q0, q1, q2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        unsigned w0, w1, w2;
-        split3_pair(v[2 * e], v[2 * e + 1], w0, w1, w2);
-        q0[e] = w0;
-        q1[e] = w1;
-        q2[e] = w2;
-    }
-    o[0] = __builtin_bit_cast(bf16x8, q0);
-    o[1] = __builtin_bit_cast(bf16x8, q1);
-    o[2] = __builtin_bit_cast(bf16x8, q2);
-}
-
 // v, opaque to the optimizer (it stays in a VGPR and is not known to be
 // loop-invariant).
 HELIX_DEV int vgpr_opaque(int v) {
@@ -370,7 +354,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                     rv[e] = R[2 * s][e];
                     rv[4 + e] = R[2 * s + 1][e];
                 }
-                wx6_split8(rv, rp);
+                x6_split8(rv, rp);
             };
             constexpr int NI = 4 * KS;
             bf16x8 cv[PF + 1][3], rp[2][3];
@@ -444,7 +428,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
                     for (int k = 0; k < 4; ++k) xs[4 * h4 + k] = s4[k] * xb[s][4 * h4 + k];
                 }
-                wx6_split8(xs, xp);
+                x6_split8(xs, xp);
             };
             constexpr int NI = 2 * NB;
             bf16x8 bt[PF + 1][3], xp[2][3];
@@ -476,7 +460,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             bf16x8 xp[3];
-            wx6_split8(xb[s], xp);
+            x6_split8(xb[s], xp);
 #pragma unroll
             for (int tb = 2 * s; tb < 4; ++tb) {
                 bf16x8 mv[3];

@@ -151,15 +151,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
     constexpr int RSR = NP + 4;            // state rows, one per channel of the block
     static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
-    // X6 (fp32 storage, scalar A, d_state <= 128): G1 and G3 on bf16x6
-    // 16x16x32 products, from C and B staged as three bf16 planes each and the
-    // state shared as planes; G4 and G2 stay on fp32 MFMA (B's fp32 rows).
+    // X6 (fp32 storage, scalar A, d_state <= 128): G1, G3 and G4 on bf16x6
+    // 16x16x32 products, from C and B staged as three bf16 planes each (G4
+    // reads B's planes transposed) and the state shared as planes; G2 stays
+    // on fp32 MFMA, and sB holds M only.
     constexpr bool X6 = !DIAG && NP <= 128 && sizeof(IO) == 4;
     constexpr int NCH = NP / 8;            // 16-byte chunks per plane row (X6)
     constexpr int PLC = X6 ? 3 * HELIX_CS * NP : 8;   // C or B planes, bf16 elements
     constexpr int PLR = X6 ? 3 * 16 * NP : 8;         // state planes
     __shared__ __attribute__((aligned(16))) float sC[X6 ? 4 : HELIX_CS * RSC];
-    __shared__ __attribute__((aligned(16))) float sB[HELIX_CS * RSC];
+    __shared__ __attribute__((aligned(16))) float sB[X6 ? HELIX_CS * RSM : HELIX_CS * RSC];   // B rows, then M
     __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * 16];   // dtX[token][channel]
     __shared__ __attribute__((aligned(16))) float sR[X6 ? 4 : 16 * RSR];   // S[channel][state index]
     __shared__ __attribute__((aligned(16))) __bf16 sCp[PLC];          // C[t][n] planes (X6)
@@ -295,7 +296,6 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                     cv[e] = keep_if_lt2(as_f32(st.cw[i][e]), j, tlen, n, N);
                     bv[e] = keep_if_lt2(as_f32(st.bw[i][e]), j, tlen, n, N);
                 }
-                *reinterpret_cast<f32x4*>(&sB[j * RSC + n]) = bv;
                 if constexpr (X6) {
                     unsigned wc[2][3], wb[2][3];
 #pragma unroll
@@ -310,6 +310,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                         *reinterpret_cast<u32x2*>(&sBp[off]) = u32x2{wb[0][pl], wb[1][pl]};
                     }
                 } else {
+                    *reinterpret_cast<f32x4*>(&sB[j * RSC + n]) = bv;
                     *reinterpret_cast<f32x4*>(&sC[j * RSC + n]) = cv;
                 }
             }
@@ -464,12 +465,41 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
             for (int i = 0; i < NTW; ++i) R[i] *= a_c;
         }
+        if constexpr (X6) {
+            // K slot 4 h + r of lane group g4 in step S is token
+            // j = 32 S + 16 h + 4 r + g4, the token of xs[8 S + 4 h + r], so
+            // the x operand is xs split in registers; the B^T operand comes
+            // from B's planes by transpose reads (lane 4 r + q names row j,
+            // state indices n0 + 4 q .. + 3).
+            const int rr = l16 >> 2, qq = l16 & 3;
+#pragma unroll
+            for (int S = 0; S < HELIX_CS / 32; ++S) {
+                float xv8[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv8[i] = xs[8 * S + i];
+                bf16x8 xp[3];
+                x6_split8(xv8, xp);
+#pragma unroll
+                for (int i = 0; i < NTW; ++i) {
+                    const int n = 16 * (NTW * sw + i) + 4 * qq;
+                    bf16x8 bt[3];
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl) {
+                        const u32x2 lo = lds_read_tr16(&sBp[x6_off<HELIX_CS, NCH>(pl, 32 * S + 4 * rr + g4, n >> 3) + (n & 7)]);
+                        const u32x2 hi = lds_read_tr16(&sBp[x6_off<HELIX_CS, NCH>(pl, 32 * S + 16 + 4 * rr + g4, n >> 3) + (n & 7)]);
+                        bt[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                    }
+                    R[i] = mfma16_x6(bt, xp, R[i]);
+                }
+            }
+        } else {
 #pragma unroll 4
         for (int s = 0; s < 16; ++s) {
             const int j = 4 * s + g4;
 #pragma unroll
             for (int i = 0; i < NTW; ++i)
                 R[i] = mfma16(sB[j * RSC + 16 * (NTW * sw + i) + l16], xs[s], R[i]);
+        }
         }
         }
         // Every wave is done with the B rows and with sR: M takes over B's
