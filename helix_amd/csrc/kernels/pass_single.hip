@@ -151,21 +151,22 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     constexpr int RSM = HELIX_CS + 4;      // M rows: in B's region after G4 (scalar A), own rows (DIAG)
     constexpr int RSR = NP + 4;            // state rows, one per channel of the block
     static_assert(HELIX_CS * RSM <= HELIX_CS * RSC, "M fits in the B rows");
-    // X6 (fp32 storage, scalar A, d_state <= 128): G1, G3 and G4 on bf16x6
-    // 16x16x32 products, from C and B staged as three bf16 planes each (G4
-    // reads B's planes transposed) and the state shared as planes; G2 stays
-    // on fp32 MFMA, and sB holds M only.
+    // X6 (fp32 storage, scalar A, d_state <= 128): all four products on
+    // bf16x6 16x16x32 MFMA, from C and B staged as three bf16 planes each
+    // (G4 reads B's planes transposed), the state shared as planes, and M
+    // stored as planes of M^T (G2 reads them transposed); no fp32 rows.
     constexpr bool X6 = !DIAG && NP <= 128 && sizeof(IO) == 4;
     constexpr int NCH = NP / 8;            // 16-byte chunks per plane row (X6)
     constexpr int PLC = X6 ? 3 * HELIX_CS * NP : 8;   // C or B planes, bf16 elements
     constexpr int PLR = X6 ? 3 * 16 * NP : 8;         // state planes
     __shared__ __attribute__((aligned(16))) float sC[X6 ? 4 : HELIX_CS * RSC];
-    __shared__ __attribute__((aligned(16))) float sB[X6 ? HELIX_CS * RSM : HELIX_CS * RSC];   // B rows, then M
+    __shared__ __attribute__((aligned(16))) float sB[X6 ? 4 : HELIX_CS * RSC];   // B rows, then M
     __shared__ __attribute__((aligned(16))) float sX[HELIX_CS * 16];   // dtX[token][channel]
     __shared__ __attribute__((aligned(16))) float sR[X6 ? 4 : 16 * RSR];   // S[channel][state index]
     __shared__ __attribute__((aligned(16))) __bf16 sCp[PLC];          // C[t][n] planes (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sBp[PLC];          // B[j][n] planes (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sRp[PLR];          // S[p][n] planes (X6)
+    __shared__ __attribute__((aligned(16))) __bf16 sMt[X6 ? 3 * HELIX_CS * HELIX_CS : 8];   // M[t][j] as M^T[j][t] planes (X6)
     __shared__ double sL[HELIX_CS];        // Lcum_t (scalar A) or cs_t (DIAG), fp64
     __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
     __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
@@ -257,6 +258,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     };
     publish_state();
 
+    if constexpr (X6) {
+        // M^T blocks above the diagonal that G2's 32-token steps cover, rows
+        // j 16..31 at t 0..15 and rows 48..63 at t 32..47: zero for good (no
+        // chunk writes them). 2 blocks x 16 rows x 2 chunks x 3 planes.
+        for (int e = tid; e < 192; e += 64 * NWV) {
+            const int pl = e % 3, c = (e / 3) & 1, row = (e / 6) & 15, blk = e / 96;
+            *reinterpret_cast<u32x4*>(&sMt[x6_off<HELIX_CS, 8>(pl, 16 + 32 * blk + row, 4 * blk + c)]) =
+                u32x4{0u, 0u, 0u, 0u};
+        }
+    }
     const int n_ch = (p.n_tok + HELIX_CS - 1) / HELIX_CS;
     const int sy0 = (int)p.s_y[0], sy2 = (int)p.s_y[2];
     StageS<NP, IO, NWV> st;
@@ -423,6 +434,18 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                     // bitwise mask clears the product whatever it is.
                     mt[q][r] = keep_if_le(acc[r] * exp_diff(sL[t], lj), j, t);
                 }
+                if constexpr (X6) {
+                    // Planes of M^T: row j, t = 16 gtb + 4 g4 .. + 3 (8 bytes a
+                    // plane). The previous chunk's G2 is behind the last barrier.
+                    unsigned w[2][3];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) split3_pair(mt[q][2 * e], mt[q][2 * e + 1], w[e][0], w[e][1], w[e][2]);
+                    const int t = 16 * gtb + 4 * g4;
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        *reinterpret_cast<u32x2*>(&sMt[x6_off<HELIX_CS, 8>(pl, j, t >> 3) + (t & 7)]) =
+                            u32x2{w[0][pl], w[1][pl]};
+                }
             }
         }
 
@@ -505,7 +528,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         // Every wave is done with the B rows and with sR: M takes over B's
         // rows, and the advanced state replaces the old one.
         __syncthreads();
-        if constexpr (!DIAG) {
+        if constexpr (!DIAG && !X6) {
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
                 const int idx = g1_idx(q);
@@ -521,8 +544,34 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
         // ---- G2: y += M dtX over the causal K range of this t block --------
         if (ywave) {
+        if constexpr (X6) {
+            // K slot 4 h + r of lane group g4 in step S is token
+            // j = 32 S + 16 h + 4 r + g4 (xb[8 S + 4 h + r]); lane 4 r + q
+            // names row j of M^T, t = 16 tb + 4 q .. + 3. Steps past the t
+            // block's causal range are skipped; the blocks above the diagonal
+            // inside a step, (0,1) and (2,3), hold zeros.
+            const int rr = l16 >> 2, qq = l16 & 3;
+            const int t = 16 * tb + 4 * qq;
+#pragma unroll
+            for (int S = 0; S < HELIX_CS / 32; ++S) {
+                if (S > (tb >> 1)) break;
+                float xv8[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xv8[i] = xb[8 * S + i];
+                bf16x8 xp[3], mv[3];
+                x6_split8(xv8, xp);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) {
+                    const u32x2 lo = lds_read_tr16(&sMt[x6_off<HELIX_CS, 8>(pl, 32 * S + 4 * rr + g4, t >> 3) + (t & 7)]);
+                    const u32x2 hi = lds_read_tr16(&sMt[x6_off<HELIX_CS, 8>(pl, 32 * S + 16 + 4 * rr + g4, t >> 3) + (t & 7)]);
+                    mv[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                }
+                ya = mfma16_x6(mv, xp, ya);
+            }
+        } else {
         for (int s = 0; s < 4 * (tb + 1); ++s)
             ya = mfma16(sM[(16 * tb + l16) * RSM + 4 * s + g4], xb[s], ya);
+        }
 
         // ---- y rows t < tlen, channels < pw ---------------------------------
         {
