@@ -60,7 +60,8 @@ HELIX_DEV f32x4 zero4() {
 // c runs: dt of token `lane`, x of tokens tid / 16 + 4 NWV i at channel tid % 16
 // of the block, and the wave's C and B rows wave + NWV r (NWV waves). Every
 // address is clamped in bounds; the masks are applied when the registers are
-// staged into LDS. With fp32 storage a lane loads four consecutive state
+// staged into LDS (fp32 storage: C and B rows read 0 there instead, through
+// the range check). With fp32 storage a lane loads four consecutive state
 // indices per row at a time (16-byte loads, a quarter of the instructions):
 // load i covers rows r = i RPI + lane / LPR, indices 4 (lane % LPR) .. +3;
 // with 16-bit storage, one index per row: columns lane + 64 m.
@@ -96,7 +97,7 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO, NWV>& st, const Heli
 #pragma unroll
     for (int i = 0; i < StageS<NP, IO, NWV>::NX; ++i) {
         const int jr = min((tid >> 4) + 4 * NWV * i, tlen - 1);
-        st.x[i] = io_load_word<IO>(rx, xc, jr * sx0);
+        st.x[i] = io_load_word<IO>(rx, xc + jr * sx0, 0);   // lane-varying row: all in the VGPR offset
     }
     if constexpr (StageS<NP, IO, NWV>::WIDE) {
         constexpr int LPR = StageS<NP, IO, NWV>::LPR, RPI = StageS<NP, IO, NWV>::RPI;
@@ -106,12 +107,14 @@ __device__ __forceinline__ void load_stage_s(StageS<NP, IO, NWV>& st, const Heli
                                         ((tlen - 1) * sc0 + N) * 4u);
         const helix_rsrc rb = make_rsrc(b.B + seq * p.seq_b + g * p.s_b[1] + (long long)t0 * p.s_b[0],
                                         ((tlen - 1) * sb0 + N) * 4u);
-        const int n0 = min(4 * (lane % LPR), N - 4);   // d_state % 8 == 0: four indices all in or all out
+        // Rows past tlen and indices past d_state (d_state % 8 == 0: four
+        // indices all in or all out) take an offset past the range: they read 0.
+        const int n0 = 4 * (lane % LPR);
 #pragma unroll
         for (int i = 0; i < StageS<NP, IO, NWV>::NW; ++i) {
-            const int jr = min(wave + NWV * (i * RPI + lane / LPR), tlen - 1);
-            st.cw[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4, 0, 0);
-            st.bw[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4, 0, 0);
+            const int j = wave + NWV * (i * RPI + lane / LPR);
+            st.cw[i] = __builtin_amdgcn_raw_buffer_load_b128(rc, store_off_if_lt((n0 + j * sc0) * 4, j, tlen, n0, N), 0, 0);
+            st.bw[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, store_off_if_lt((n0 + j * sb0) * 4, j, tlen, n0, N), 0, 0);
         }
     } else {
         load_cb_rows<NP, IO, NWV>(st.c, st.b, p, b, seq, g, t0, tlen, lane, wave);
@@ -301,11 +304,11 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
             for (int i = 0; i < StageS<NP, IO, NWV>::NW; ++i) {
                 const int j = wave + NWV * (i * RPI + lane / LPR);
-                f32x4 cv, bv;
+                f32x4 cv, bv;   // zero past tlen and d_state (range check)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    cv[e] = keep_if_lt2(as_f32(st.cw[i][e]), j, tlen, n, N);
-                    bv[e] = keep_if_lt2(as_f32(st.bw[i][e]), j, tlen, n, N);
+                    cv[e] = as_f32(st.cw[i][e]);
+                    bv[e] = as_f32(st.bw[i][e]);
                 }
                 if constexpr (X6) {
                     unsigned wc[2][3], wb[2][3];
@@ -340,7 +343,10 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         __syncthreads();
 
         // The next chunk's inputs travel while this one runs on the MFMA pipe.
-        if (c + 1 < n_ch)
+        // With eight waves the state waves issue theirs after G1, so the two
+        // halves do not queue for the texture units at the same time.
+        const bool early_pf = NWV == 4 || ywave;
+        if (c + 1 < n_ch && early_pf)
             load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
                                  min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
 
@@ -448,6 +454,10 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 }
             }
         }
+
+        if (c + 1 < n_ch && !early_pf)
+            load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
+                                 min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
 
         // ---- G3: y = exp(Lcum_t) . (C S) for this wave's t block; S from sR --
         f32x4 ya = zero4();
