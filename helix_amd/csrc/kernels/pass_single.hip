@@ -170,9 +170,16 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     __shared__ __attribute__((aligned(16))) __bf16 sBp[PLC];          // B[j][n] planes (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sRp[PLR];          // S[p][n] planes (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sMt[X6 ? 3 * HELIX_CS * HELIX_CS : 8];   // M[t][j] as M^T[j][t] planes (X6)
-    __shared__ double sL[HELIX_CS];        // Lcum_t (scalar A) or cs_t (DIAG), fp64
-    __shared__ float sCs[HELIX_CS];        // exp(L_end - Lcum_j)
-    __shared__ float sE[HELIX_CS];         // exp(Lcum_t)
+    // PRE (eight waves): the chunk preamble (dt, Lcum and its exponentials)
+    // is formed once, by wave PW during the previous chunk, into the other
+    // half of two-chunk buffers, instead of by every wave at the chunk's start.
+    constexpr bool PRE = NWV == 8;
+    constexpr int PW = 3;                  // a y wave with one G1 block
+    constexpr int NB = PRE ? 2 : 1;
+    __shared__ double sLb[NB * HELIX_CS];  // Lcum_t (scalar A) or cs_t (DIAG), fp64
+    __shared__ float sCsb[NB * HELIX_CS];  // exp(L_end - Lcum_j)
+    __shared__ float sEb[NB * HELIX_CS];   // exp(Lcum_t)
+    __shared__ float sDtb[PRE ? 2 * HELIX_CS : 4];   // dt_t (PRE)
     __shared__ double sA2[DIAG ? NP : 2];        // A_n log2(e) in fp64, 0 past d_state
     __shared__ __attribute__((aligned(16))) float sMd[DIAG ? HELIX_CS * RSM : 4];
     float* const sM = DIAG ? sMd : sB;
@@ -276,6 +283,25 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     StageS<NP, IO, NWV> st;
     load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, 0, min(HELIX_CS, p.n_tok), pw, lane, wave);
 
+    // Chunk cc's preamble from its raw dt (one wave, lane = token), into
+    // buffer half cc & 1. dt = 0 past the chunk's length, so Lcum stays at
+    // Lcum[tlen-1] there and dtX rows past tlen are zero.
+    auto preamble = [&](int cc, float dtraw) {
+        const int tl = min(HELIX_CS, p.n_tok - cc * HELIX_CS);
+        const float d = keep_if_lt(helix_dt(p, dtraw), lane, tl);
+        const double lc = wave_incl_sum((double)A_h * (double)d);
+        const double le = bcast(lc, 63);
+        const int o = (cc & 1) * HELIX_CS;
+        sDtb[o + lane] = d;
+        sLb[o + lane]  = lc;
+        sCsb[o + lane] = exp_diff(le, lc);
+        sEb[o + lane]  = expf((float)lc);
+    };
+    if constexpr (PRE) {
+        if (wave == PW) preamble(0, st.dtraw);
+        __syncthreads();
+    }
+
     for (int c = 0; c < n_ch; ++c) {
         const int t0   = c * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
@@ -283,20 +309,31 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         // ---- chunk preamble and staging ------------------------------------
         // dt = 0 past tlen, so Lcum stays at Lcum[tlen-1] there and dtX rows
         // past tlen are zero.
-        const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
-        const double lcum = wave_incl_sum(DIAG ? (double)dtv : (double)A_h * (double)dtv);
-        const double lend = bcast(lcum, 63);
-        if (wave == 0) {
-            sL[lane] = lcum;
-            if constexpr (!DIAG) {
-                sCs[lane] = exp_diff(lend, lcum);
-                sE[lane]  = expf((float)lcum);
+        const int cbo = PRE ? (c & 1) * HELIX_CS : 0;
+        double* const sL = sLb + cbo;
+        float* const sCs = sCsb + cbo;
+        float* const sE  = sEb + cbo;
+        float dtv = 0.0f;
+        double lend;
+        if constexpr (PRE) {
+            lend = sL[HELIX_CS - 1];
+        } else {
+            dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+            const double lcum = wave_incl_sum(DIAG ? (double)dtv : (double)A_h * (double)dtv);
+            lend = bcast(lcum, 63);
+            if (wave == 0) {
+                sL[lane] = lcum;
+                if constexpr (!DIAG) {
+                    sCs[lane] = exp_diff(lend, lcum);
+                    sE[lane]  = expf((float)lcum);
+                }
             }
         }
 #pragma unroll
         for (int i = 0; i < StageS<NP, IO, NWV>::NX; ++i) {
             const int j = (tid >> 4) + 4 * NWV * i;
-            sX[j * 16 + (tid & 15)] = keep_if_lt(__shfl(dtv, j, 64) * io_widen<IO>(st.x[i]), tid & 15, pw);
+            const float dj = PRE ? sDtb[cbo + j] : __shfl(dtv, j, 64);
+            sX[j * 16 + (tid & 15)] = keep_if_lt(dj * io_widen<IO>(st.x[i]), tid & 15, pw);
         }
         if constexpr (StageS<NP, IO, NWV>::WIDE) {
             constexpr int LPR = StageS<NP, IO, NWV>::LPR, RPI = StageS<NP, IO, NWV>::RPI;
@@ -483,6 +520,11 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 #pragma unroll
             for (int r = 0; r < 4; ++r) ya[r] *= sE[16 * tb + 4 * g4 + r];
         }
+        }
+        // The next chunk's preamble (its dt arrived with this chunk's prefetch;
+        // its buffer half was last read before the previous chunk's end).
+        if constexpr (PRE) {
+            if (wave == PW && c + 1 < n_ch) preamble(c + 1, st.dtraw);
         }
 
         // ---- G4: S <- exp(L_end) S + B^T (exp(L_end - Lcum) dt x), own tiles --
