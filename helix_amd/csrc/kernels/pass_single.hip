@@ -168,7 +168,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     __shared__ __attribute__((aligned(16))) float sR[X6 ? 4 : 16 * RSR];   // S[channel][state index]
     __shared__ __attribute__((aligned(16))) __bf16 sCp[PLC];          // C[t][n] planes (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sBp[PLC];          // B[j][n] planes (X6)
-    __shared__ __attribute__((aligned(16))) __bf16 sRp[PLR];          // S[p][n] planes (X6)
+    __shared__ __attribute__((aligned(16))) __bf16 sRp[2 * PLR];      // S[p][n] planes, two chunks (X6)
     __shared__ __attribute__((aligned(16))) __bf16 sMt[X6 ? 3 * HELIX_CS * HELIX_CS : 8];   // M[t][j] as M^T[j][t] planes (X6)
     // PRE (eight waves): the chunk preamble (dt, Lcum and its exponentials)
     // is formed once, by wave PW during the previous chunk, into the other
@@ -246,8 +246,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
     }
     // Every wave's G3 reads the whole state: it is shared through sR, written
-    // by the wave that advances each tile.
-    auto publish_state = [&]() {
+    // by the wave that advances each tile. X6: planes in half `half` of sRp,
+    // the one chunk `half` (mod 2) reads.
+    auto publish_state = [&](int half) {
         if (swave) {
 #pragma unroll
             for (int i = 0; i < NTW; ++i) {
@@ -258,7 +259,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                     for (int e = 0; e < 2; ++e) split3_pair(R[i][2 * e], R[i][2 * e + 1], w[e][0], w[e][1], w[e][2]);
 #pragma unroll
                     for (int pl = 0; pl < 3; ++pl)
-                        *reinterpret_cast<u32x2*>(&sRp[x6_off<16, NCH>(pl, l16, n >> 3) + (n & 7)]) =
+                        *reinterpret_cast<u32x2*>(&sRp[half * PLR + x6_off<16, NCH>(pl, l16, n >> 3) + (n & 7)]) =
                             u32x2{w[0][pl], w[1][pl]};
                 } else {
                     *reinterpret_cast<f32x4*>(&sR[l16 * RSR + n]) = R[i];
@@ -266,7 +267,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
     };
-    publish_state();
+    publish_state(0);
 
     if constexpr (X6) {
         // M^T blocks above the diagonal that G2's 32-token steps cover, rows
@@ -504,7 +505,7 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             for (int s = 0; s < NP / 32; ++s) {
                 bf16x8 av[3], rv[3];
                 x6_read<HELIX_CS, NCH>(sCp, 16 * tb + l16, 4 * s + g4, av);
-                x6_read<16, NCH>(sRp, l16, 4 * s + g4, rv);
+                x6_read<16, NCH>(sRp + (c & 1) * PLR, l16, 4 * s + g4, rv);
                 ya = mfma16_x6(av, rv, ya);
             }
         } else {
@@ -577,10 +578,15 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         }
         }
         }
-        // Every wave is done with the B rows and with sR: M takes over B's
-        // rows, and the advanced state replaces the old one.
+        // X6: the advanced state goes to the other half of sRp (the one chunk
+        // c + 1 reads; chunk c - 1's readers are behind the last barrier), and
+        // M^T is complete once every wave is past this barrier. Otherwise
+        // every wave is done with the B rows and with sR here: M takes over
+        // B's rows, and the advanced state replaces the old one.
+        if constexpr (X6) publish_state((c + 1) & 1);
         __syncthreads();
-        if constexpr (!DIAG && !X6) {
+        if constexpr (!X6) {
+        if constexpr (!DIAG) {
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
                 const int idx = g1_idx(q);
@@ -591,8 +597,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                 }
             }
         }
-        publish_state();
+        publish_state(0);
         __syncthreads();
+        }
 
         // ---- G2: y += M dtX over the causal K range of this t block --------
         if (ywave) {
@@ -639,7 +646,12 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
         }
-        __syncthreads();   // the next chunk's staging overwrites C, B/M and dtX
+        // The next chunk's staging overwrites C, B/M and dtX. X6 needs no
+        // barrier here: G2 reads only M^T (rewritten after the next chunk's
+        // first barrier) and registers, and every reader of C, B, dtX and
+        // the state planes is behind the barrier above; the state waves stage
+        // the next chunk while the y waves finish G2.
+        if constexpr (!X6) __syncthreads();
     }
 
     // Final state to s1[seq], same register layout as the s0 read (the state
