@@ -176,16 +176,20 @@ const TraitTable& table() {
     return t;
 }
 
-// Pass A writes bf16 copies of B and C for the walking Pass C (fp32 storage)
-// when the K = heads_per_group * n_pslab workgroups of a chunk cover its 64
-// rows with two quads of four state indices per thread (pass_a_x6.hip,
-// copy_map); the tuning's bccopy = 0 (HELIX_WALK_BCCOPY=0) switches them off.
+// Pass A writes bf16 copies of B and C for the walking Pass C (fp32 storage);
+// HELIX_WALK_BCCOPY=0 / 1 switches them off / on where the kernels can. At
+// d_state 256 the per-item Pass A copies when the K = heads_per_group *
+// n_pslab workgroups of a chunk cover its 64 rows with two quads of four state
+// indices per thread (pass_a_x6.hip, copy_map).
 bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d) {
     if (tu.bccopy == 0) return false;
-    // The head-block Pass A (d_state <= 128) copies at every shape: one wave
-    // per 8-token block of a chunk and group (pass_a_hb.hip).
-    if (d.d_state <= 128) return true;
     const long K = (long)(d.n_head / d.n_group) * ((d.head_dim + HELIX_HD - 1) / HELIX_HD);
+    // The head-block Pass A (d_state <= 128) can copy at every shape (one
+    // wave per 8-token block of a chunk and group, pass_a_hb.hip). The copies
+    // pay off when many walk workgroups read a chunk's rows (measured at
+    // configs 4a and 4b, 80 and 27 heads per group: 45 and 56 us faster);
+    // at 8 (config 2) the walk reading the fp32 rows itself is 3 us faster.
+    if (d.d_state <= 128) return tu.bccopy == 1 || K > 8;
     return (64 + K - 1) / K * (d.d_state / 4) <= 2 * 256;
 }
 
@@ -229,7 +233,8 @@ helix_tuning tuning_from_env() {
     if (env_switch("HELIX_PASSA_SPLIT") == 3) t.passa_split = 3;
     t.fuse_b = env_switch("HELIX_FUSE_B");
     if (t.fuse_b > 1) t.fuse_b = 1;
-    t.bccopy = env_switch("HELIX_WALK_BCCOPY") == 0 ? 0 : -1;
+    const int bc = env_switch("HELIX_WALK_BCCOPY");
+    t.bccopy = bc == 0 ? 0 : bc > 0 ? 1 : -1;
     t.seg_len = (int)env_long("HELIX_SEG_LEN", 0);
     t.hblk = (int)env_long("HELIX_HBLK", 0);
     if (env_switch("HELIX_F32_WALK") == 0) t.f32_walk = 0;

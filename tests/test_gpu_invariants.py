@@ -42,8 +42,10 @@ PATHS = [
     # through it), and in its own launch.
     ("bf16/fuseB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "1"}),
     ("bf16/passB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "0"}),
-    # The walk on the caller's fp32 B and C instead of Pass A's bf16 copies.
+    # The walk on the caller's fp32 B and C, and on Pass A's bf16 copies of
+    # them (by default only past eight items per group).
     ("bf16/nocopy", HELIX_BACKEND_MPP, True, {"HELIX_WALK_BCCOPY": "0"}),
+    ("bf16/copy", HELIX_BACKEND_MPP, True, {"HELIX_WALK_BCCOPY": "1"}),
     ("1pass", HELIX_BACKEND_AUTO, False, {}),
 ]
 PATH_IDS = [p[0] for p in PATHS]

@@ -79,8 +79,11 @@ MODES = [
     # segments).
     ("bf16/passB/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_FUSE_B": "0"}, True),
     ("bf16/fuseB/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_FUSE_B": "1"}, True),
-    # The walk on the caller's fp32 B and C instead of Pass A's bf16 copies.
+    # The walk on the caller's fp32 B and C, and on Pass A's bf16 copies of
+    # them (by default only past eight items per group).
     ("bf16/nocopy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_WALK_BCCOPY": "0"}, True),
+    ("bf16/copy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_WALK_BCCOPY": "1"}, True),
+    ("bf16/copy/sm", HELIX_BACKEND_MPP, 1, "short", {"HELIX_WALK_BCCOPY": "1"}, True),
     # Opt-in: Pass A on two split planes (three products), s1 at the wider bound.
     ("bf16/x3", HELIX_BACKEND_MPP, None, "short", {"HELIX_PASSA_SPLIT": "3"}, True),
     ("bf16/x3/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA_SPLIT": "3"}, True),

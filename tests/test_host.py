@@ -303,19 +303,20 @@ def test_backend_selection(host):
     x3 = tuned(HELIX_PASSA_SPLIT="3")
     assert x3.backend_desc(mp(shape)) == ("mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in) "
                                           "(d_state<=128)")
-    assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x3agg_bc_n128"
+    assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x3agg_n128"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
     assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
-    # Pass A writes bf16 copies of B and C that the walking Pass C reads.
-    # Pass B keeps its own launch: the walk's prologue scans only walk
-    # segments that are Pass A's segments too (HELIX_FUSE_B=1 with
+    # Eight heads per group: the walk reads the caller's fp32 B and C (no
+    # bf16 copies). Pass B keeps its own launch: the walk's prologue scans
+    # only walk segments that are Pass A's segments too (HELIX_FUSE_B=1 with
     # HELIX_SEG_LEN=16 runs it there).
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_hb_x6agg_bc_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_bc_n128")
+        b"helix_chunk_state_hb_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
+    assert k.bccopy_bytes == 0
     # Pass A (head blocks of four heads) runs 8-chunk segments, 16 per
     # sequence; the walk runs 16-chunk ones, each starting at every other
     # Pass A segment.
@@ -331,17 +332,20 @@ def test_backend_selection(host):
     assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
     assert km.launches == 3 * km.n_groups
     L, S, H, P, N, G = shape
-    assert k.bccopy_bytes == 2 * (S * L * G * N * 2)
+    # HELIX_WALK_BCCOPY=1: Pass A writes bf16 copies of B and C that the walk reads.
+    kc = tuned(HELIX_WALK_BCCOPY="1").plan_info(mp(shape))
+    assert (kc.kernel_a, kc.kernel_c) == (b"helix_chunk_state_hb_x6agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
+    assert kc.bccopy_bytes == 2 * (S * L * G * N * 2)
+    assert k4.bccopy_bytes > 0   # 80 heads per group: copies by default
     # Pass A writes one 16-byte decay record per (seq, chunk, head, token) for
     # the walk and for the fp32 path's bf16x6 Pass C.
     recs = S * (-(-L // 64)) * H * 64 * 16
     assert k.rec_bytes == recs
     assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == recs
     assert host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
-    assert k.total_bytes >= k.s_seg_bytes + k.bccopy_bytes
-    k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(shape))
-    assert (k0.kernel_a, k0.kernel_c) == (b"helix_chunk_state_hb_x6agg_n128", b"helix_scan_walk16_bf16_n128")
-    assert k0.bccopy_bytes == 0 and k0.total_bytes < k.total_bytes
+    assert kc.total_bytes >= kc.s_seg_bytes + kc.bccopy_bytes and kc.total_bytes > k.total_bytes
+    k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(CONFIG_SHAPES["cfg4a"]))
+    assert b"_bc_" not in k0.kernel_a and b"_bc_" not in k0.kernel_c and k0.bccopy_bytes == 0
     k = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6agg_r64_n128", b"helix_scan_walk_x6_n128")
     k = tuned(HELIX_F32_WALK="0").plan_info(mp(shape, HELIX_BACKEND_SGMMA))
@@ -375,13 +379,14 @@ def test_backend_selection(host):
 # ---------------------------------------------------------------------------
 
 def test_bc_copy_condition(host):
-    # Up to d_state 128 the head-block Pass A writes the copies at every shape
-    # (one wave per 8-token block of a chunk and group). At d_state 256 the
-    # per-item Pass A needs the K = heads_per_group * n_pslab workgroups of a
-    # chunk to cover its 64 rows with two quads of four state indices per
+    # Up to d_state 128 the head-block Pass A writes the copies when more than
+    # eight (head, P slab) items share a group's rows (K = heads_per_group *
+    # n_pslab > 8). At d_state 256 the per-item Pass A needs the K workgroups
+    # of a chunk to cover its 64 rows with two quads of four state indices per
     # thread: ceil(64 / K) * d_state / 4 <= 512.
-    for (H, P, N, G), copy in [((64, 64, 128, 8), True), ((4, 64, 128, 1), True), ((2, 64, 128, 1), True),
-                               ((1, 192, 128, 1), True), ((1, 64, 64, 1), True), ((1, 64, 128, 1), True),
+    for (H, P, N, G), copy in [((64, 64, 128, 8), False), ((72, 64, 128, 8), True), ((16, 64, 128, 1), True),
+                               ((4, 64, 128, 1), False), ((2, 64, 128, 1), False), ((3, 192, 128, 1), True),
+                               ((1, 192, 128, 1), False), ((9, 64, 64, 1), True), ((1, 64, 128, 1), False),
                                ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((2, 128, 256, 1), False),
                                ((4, 128, 256, 1), True)]:
         d = mp((4096, 1, H, P, N, G))
