@@ -174,13 +174,9 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     // its B reads.
     constexpr bool M_IN_B = HPW * HELIX_CS * RSJ <= HELIX_CS * RS;
     constexpr int MB = M_IN_B ? 0 : HPW * HELIX_CS * RSJ;
-    // With B's rows intact until G4 (M in rows of its own), G4 reads its B^T
-    // operand from them by LDS transpose reads; otherwise from a transposed
-    // copy staged with B.
-    constexpr bool BT_TR = !M_IN_B;
     __shared__ __attribute__((aligned(16))) __bf16 sC[HELIX_CS * RS];
     __shared__ __attribute__((aligned(16))) __bf16 sB[HELIX_CS * RS];
-    __shared__ __attribute__((aligned(16))) __bf16 sBt[BT_TR ? 8 : NP * RSJ];
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[NP * RSJ];
     __shared__ __attribute__((aligned(16))) __bf16 sXt[2][HPW][HELIX_HD * RSJ];   // by chunk parity
     __shared__ __attribute__((aligned(16))) __bf16 sXst[HPW][HELIX_HD * RSJ];
     __shared__ __attribute__((aligned(16))) __bf16 sMown[MB > 0 ? MB : 8];
@@ -395,12 +391,10 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                 *reinterpret_cast<bf16x4*>(&sB[swz_off<RS>(j, cpos + 8)]) = b_hi;
                 *reinterpret_cast<bf16x4*>(&sC[swz_off<RS>(j, cpos)]) = c_lo;
                 *reinterpret_cast<bf16x4*>(&sC[swz_off<RS>(j, cpos + 8)]) = c_hi;
-                if constexpr (!BT_TR) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sBt[bt_off(8 * u + e, j)] = b_lo[e];
-                        sBt[bt_off(8 * u + 4 + e, j)] = b_hi[e];
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    sBt[bt_off(8 * u + e, j)] = b_lo[e];
+                    sBt[bt_off(8 * u + 4 + e, j)] = b_hi[e];
                 }
             }
         }
@@ -510,27 +504,12 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             bf16x8 xs[2];
 #pragma unroll
             for (int s = 0; s < 2; ++s) xs[s] = *reinterpret_cast<const bf16x8*>(&sXst[hw][swz_off<RSJ>(pp, 32 * s + 8 * q)]);
-            // BT_TR: K slot 4 h + r of lane group q in step s is token
-            // j = 32 s + 8 q + 4 h + r (xs's order); lane 4 r + v of the group
-            // names row j of B, the four state indices 16 nb + 4 v .. + 3,
-            // which perm32 keeps together at 32 (nb / 2) + 8 v + 4 (nb % 2).
-            const int rr = c16 >> 2, vv = c16 & 3;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 f32x4 rn = R[nb] * a_c;
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    bf16x8 bt;
-                    if constexpr (BT_TR) {
-                        const int col = 32 * (nb >> 1) + 8 * vv + 4 * (nb & 1);
-                        const u32x2 lo = lds_read_tr16(&sB[swz_off<RS>(32 * s + 8 * q + rr, col)]);
-                        const u32x2 hi = lds_read_tr16(&sB[swz_off<RS>(32 * s + 8 * q + 4 + rr, col)]);
-                        bt = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-                    } else {
-                        bt = *reinterpret_cast<const bf16x8*>(&sBt[bt_off(16 * nb + c16, 32 * s + 8 * q)]);
-                    }
-                    rn = mfma16(bt, xs[s], rn);
-                }
+                for (int s = 0; s < 2; ++s)
+                    rn = mfma16(*reinterpret_cast<const bf16x8*>(&sBt[bt_off(16 * nb + c16, 32 * s + 8 * q)]), xs[s], rn);
                 R[nb] = rn;
             }
         }
