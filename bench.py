@@ -401,6 +401,8 @@ def main():
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
         variants.append(Variant("bf16-passA-x3-optin", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_PASSA_SPLIT": "3"}))
+        variants.append(Variant("bf16-copies", ctx, HELIX_BACKEND_MPP, tensors,
+                                env={"HELIX_WALK_BCCOPY": "1"}))
 
     def warm_up(v, ms):
         """W steps, then more until the wall clock has run `ms` (the
