@@ -49,8 +49,9 @@ namespace {
 //            helix_chunk_state{_hb}_x{6,3}agg_{bf16,f16}io_n*   16-bit storage
 //     Pass B helix_state_scan_f32 (or the walk's prologue, fuse_b)
 //     Pass C helix_scan_walk16_bf16{,_bc,_bf16io,_f16io}_n*
-//   single pass (multipass = false): helix_scan_1pass_{f32,bf16io,f16io}_n*,
-//   fp32 MFMA, no scratch; diagonal A: helix_scan_1pass_diag_f32_n{64,128}.
+//   single pass (multipass = false): helix_scan_1pass_{f32,bf16io,f16io}_n*, no
+//   scratch; fp32-accurate (bf16x6 products with fp32 storage up to d_state
+//   128, fp32 MFMA otherwise); diagonal A: helix_scan_1pass_diag_f32_n{64,128}.
 
 constexpr int kNps[3] = {64, 128, 256};
 
@@ -95,7 +96,10 @@ struct TraitTable {
                 t.backend = HELIX_BACKEND_SGMMA;
                 t.name = keep(std::string("mfma fp32, single pass") +
                               (io == 0 ? "" : io == 1 ? ", bf16 storage" : ", f16 storage") + upto);
-                t.mfma_a = t.mfma_c = "v_mfma_f32_16x16x4_f32";
+                // fp32 storage up to d_state 128: every product on six bf16
+                // split products (pass_single.hip, X6); otherwise fp32 MFMA.
+                t.mfma_a = t.mfma_c = io == 0 && kNps[k] <= 128 ? "v_mfma_f32_16x16x32_bf16 (bf16x6 split operands)"
+                                                                : "v_mfma_f32_16x16x4_f32";
                 t.np = kNps[k];
                 t.k_single = kernel(std::string("helix_scan_1pass_") + (io == 0 ? "f32_" : kIoTag[io]) + "n" + np);
                 t.single_threads = 64 * HELIX_1PASS_WAVES(kNps[k]);

@@ -91,7 +91,8 @@ typedef enum {
  *            state and s1 stay fp32-accurate
  *   AUTO  -> MPP whenever the shape is served by it, else SGMMA
  *   REF   -> reported when no usable context exists; never launched
- * multipass = false runs the fp32 single-pass kernel under AUTO and SGMMA. */
+ * multipass = false runs the fp32-accurate single-pass kernel under AUTO and
+ * SGMMA. */
 typedef enum {
     HELIX_BACKEND_AUTO  = 0,
     HELIX_BACKEND_SGMMA = 1,
