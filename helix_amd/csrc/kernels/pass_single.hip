@@ -493,7 +493,10 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             }
         }
 
-        if (c + 1 < n_ch && !early_pf)
+        // With bf16x6 products the state waves issue theirs inside G4, behind
+        // its first product, so a stall at the texture units does not hold
+        // back MFMAs that are already queued.
+        if (!X6 && c + 1 < n_ch && !early_pf)
             load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
                                  min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
 
@@ -566,6 +569,13 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                         bt[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
                     }
                     R[i] = mfma16_x6(bt, xp, R[i]);
+                    if (S == 0 && i == 0) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (c + 1 < n_ch)
+                            load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
+                                                      min(HELIX_CS, p.n_tok - t0 - HELIX_CS), pw, lane, wave);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
         } else {
