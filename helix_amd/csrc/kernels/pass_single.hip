@@ -381,8 +381,9 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         __syncthreads();
 
         // The next chunk's inputs travel while this one runs on the MFMA pipe.
-        // With eight waves the state waves issue theirs after G1, so the two
-        // halves do not queue for the texture units at the same time.
+        // With eight waves the state waves issue theirs later (after G1, or
+        // inside G4 with bf16x6 products), so the two halves do not queue for
+        // the texture units at the same time.
         const bool early_pf = NWV == 4 || ywave;
         if (c + 1 < n_ch && early_pf)
             load_stage_s<NP, IO, NWV>(st, p, b, dt_h, x_h, seq, g, t0 + HELIX_CS,
