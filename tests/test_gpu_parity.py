@@ -52,6 +52,10 @@ SHAPES = [
     (300, 1, 4, 128, 256, 1, "d_state=256 ragged tail"),
     (256, 1, 8, 128, 256, 2, "d_state=256 grouped"),
     (256, 1, 4, 192, 128, 1, "head_dim=192 three slabs"),
+    # Partial 16-channel blocks and padded state indices (head_dim and
+    # d_state need only be multiples of 8).
+    (200, 1, 3, 40, 96, 1, "head_dim=40 d_state=96"),
+    (150, 1, 2, 72, 40, 1, "head_dim=72 d_state=40"),
     (256, 1, 8, 128, 128, 8, "n_group=8 grouped"),
     (256, 4, 4, 64, 128, 1, "n_seq=4 batched"),
     (1024, 1, 2, 64, 128, 1, "L=1024 sixteen chunks"),
