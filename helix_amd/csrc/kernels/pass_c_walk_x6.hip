@@ -129,11 +129,10 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     constexpr int NCH = NP / 8;                // 16-byte chunks per C / B row
     constexpr int PL_CB = 3 * HELIX_CS * NP;   // C (or B) planes, elements
     constexpr int PL_M  = 3 * HELIX_CS * HELIX_CS;
-    static_assert(HPW * PL_M <= PL_CB, "the heads' M fit in B's region");
     constexpr int PF = 2;                      // products an operand read runs ahead
     __shared__ __attribute__((aligned(16))) __bf16 sC[PL_CB];
-    __shared__ __attribute__((aligned(16))) __bf16 sB[PL_CB];
-    __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];
+    __shared__ __attribute__((aligned(16))) __bf16 sB[PL_CB];          // x6_off_tr swizzle
+    __shared__ __attribute__((aligned(16))) __bf16 sM[HPW * PL_M];     // each head's M[t][j] planes
     __shared__ __attribute__((aligned(16))) float sDt[HPW][HELIX_CS];    // dt_j (0 past tlen)
     __shared__ __attribute__((aligned(16))) float sSd[HPW][HELIX_CS];    // exp(L_end - Lcum_j)
     __shared__ __attribute__((aligned(16))) float sE[HPW][HELIX_CS];     // exp(Lcum_t)
@@ -173,12 +172,10 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
 
     // Staging: lane (u, rr) holds state indices 8u .. 8u+7 of rows j0 and j0 + 1
-    // (the wave's eight rows, 16 lanes per row), so that a pair of B^T values
-    // (rows j0, j0 + 1 of one state index) is one 4-byte LDS store. A chunk's
-    // planes are staged while the previous chunk's products run: C once G1
-    // and G3 are done with it, B^T once G4 is, and B once G2 has read M.
-    // C is zeroed past tlen and d_state, which is all G1 and G3 need; B rows
-    // past tlen only meet dt = 0 columns in G2 and G4.
+    // (the wave's eight rows, 16 lanes per row). A chunk's planes are staged
+    // while the previous chunk's products run: C once G1 and G3 are done with
+    // it, B once G4 is. C is zeroed past tlen and d_state, which is all G1 and
+    // G3 need; B rows past tlen only meet dt = 0 columns in G4.
     auto stage_c = [&](const RunsWX6& rn, int tl, int j0, int u, int cpos) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -212,17 +209,6 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 split3_pair(as_f32(rn.b[k][e >> 1][2 * (e & 1)]), as_f32(rn.b[k][e >> 1][2 * (e & 1) + 1]),
                             bw[k][0][e], bw[k][1][e], bw[k][2][e]);
     };
-    // B^T[n][j0 .. j0 + 1], n = 8u + e: the halves of rows j0 and j0 + 1.
-    auto write_bt = [&](const unsigned (&bw)[2][3][4], int j0, int u) {
-#pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
-                const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-                *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
-            }
-    };
     auto write_b = [&](const unsigned (&bw)[2][3][4], int j0, int cpos) {
 #pragma unroll
         for (int k = 0; k < 2; ++k)
@@ -231,7 +217,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const int pos = cpos + 8 * hh;
-                    *reinterpret_cast<u32x2*>(&sB[x6_off<HELIX_CS, NCH>(pl, j0 + k, pos >> 3) + (pos & 7)]) =
+                    *reinterpret_cast<u32x2*>(&sB[x6_off_tr<HELIX_CS, NCH>(pl, j0 + k, pos >> 3) + (pos & 7)]) =
                         u32x2{bw[k][pl][2 * hh], bw[k][pl][2 * hh + 1]};
                 }
     };
@@ -246,7 +232,6 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         load_stage_x6(st, p, rec_h, x_h, c_begin, lane, rr, 16 * w4 + u, pw);
         stage_c(runs, tlen_of(c_begin), j0, u, wx6_perm32(8 * u));
         split_b(runs, bw);
-        write_bt(bw, j0, u);
         load_runs_x6(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u);
     }
 
@@ -267,11 +252,13 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
             R[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
     }
 
-    __bf16* const sMh = sB + hw * PL_M;
+    __bf16* const sMh = sM + hw * PL_M;
 
-    // Four barriers per chunk: (1) the chunk's planes and records are staged;
-    // (2) G1 and G3 are done with B and C; (3) M is written (in B's region)
-    // and G4 is done with B^T; (4) G2 is done with M.
+    // Three barriers per chunk: (1) the chunk's planes and records are staged;
+    // (2) M is written and G1 and G3 are done with C (the next chunk's C
+    // planes are staged behind it); (3) G4 is done with B (the next chunk's B
+    // planes are written at the top of the loop). G2 reads M after (2); the
+    // next chunk writes M only after its (1).
     for (int c = c_begin; c < c_end; ++c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = tlen_of(c);
@@ -333,9 +320,41 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
                     bf16x8 av[3], bv[3];
-                    x6_read<HELIX_CS, NCH>(sB, 16 * jb + c16, 4 * s + q, av);
+                    x6_read_tr<HELIX_CS, NCH>(sB, 16 * jb + c16, 4 * s + q, av);
                     x6_read<HELIX_CS, NCH>(sC, 16 * tb + c16, 4 * s + q, bv);
                     d[i] = wx6_mfma(av, bv, d[i]);
+                }
+            }
+        }
+
+        // ---- M[t][j] = (C B^T)[t][j] exp(Lcum_t - Lcum_j), j <= t, per head --
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = wave + 8 * i;
+            if (idx < 10) {
+                const int tb = wx6_tb(idx), jb = wx6_jb(idx);
+                const int t = 16 * tb + c16;
+                const int jq = 16 * jb + 4 * q;
+#pragma unroll
+                for (int hh = 0; hh < HPW; ++hh) {
+                    const double lt = sL[hh][t];
+                    float m[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        m[r] = keep_if_le(d[i][r] * exp2_diff(lt, sL[hh][jq + r]), jq + r, t);
+                    u32x2 mq[3];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        unsigned w0, w1, w2;
+                        split3_pair(m[2 * e], m[2 * e + 1], w0, w1, w2);
+                        mq[0][e] = w0;
+                        mq[1][e] = w1;
+                        mq[2][e] = w2;
+                    }
+#pragma unroll
+                    for (int pl = 0; pl < 3; ++pl)
+                        *reinterpret_cast<u32x2*>(&sM[hh * PL_M + x6_off<HELIX_CS, 8>(pl, t, jq >> 3) + (jq & 7)]) =
+                            mq[pl];
                 }
             }
         }
@@ -380,38 +399,6 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         }
         __syncthreads();   // (2)
 
-        // ---- M[t][j] = (C B^T)[t][j] exp(Lcum_t - Lcum_j), j <= t, per head --
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = wave + 8 * i;
-            if (idx < 10) {
-                const int tb = wx6_tb(idx), jb = wx6_jb(idx);
-                const int t = 16 * tb + c16;
-                const int jq = 16 * jb + 4 * q;
-#pragma unroll
-                for (int hh = 0; hh < HPW; ++hh) {
-                    const double lt = sL[hh][t];
-                    float m[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        m[r] = keep_if_le(d[i][r] * exp2_diff(lt, sL[hh][jq + r]), jq + r, t);
-                    u32x2 mq[3];
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        unsigned w0, w1, w2;
-                        split3_pair(m[2 * e], m[2 * e + 1], w0, w1, w2);
-                        mq[0][e] = w0;
-                        mq[1][e] = w1;
-                        mq[2][e] = w2;
-                    }
-#pragma unroll
-                    for (int pl = 0; pl < 3; ++pl)
-                        *reinterpret_cast<u32x2*>(&sB[hh * PL_M + x6_off<HELIX_CS, 8>(pl, t, jq >> 3) + (jq & 7)]) =
-                            mq[pl];
-                }
-            }
-        }
-
         __builtin_amdgcn_sched_barrier(0);
         stage_c(runs, tlen_of(cn), j0, u, cpos);
 
@@ -430,27 +417,39 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 }
                 x6_split8(xs, xp);
             };
+            // B^T operand by LDS transpose reads of B's planes: K slot 4 h + r
+            // of lane group q in step s is token j = 32 s + 8 q + 4 h + r (the
+            // order of xs); lane 4 r + v names row j and the state indices
+            // 16 nb + 4 v .. + 3, which perm32 keeps together at
+            // 32 (nb / 2) + 8 v + 4 (nb % 2).
+            const int rr4 = c16 >> 2, vv = c16 & 3;
+            auto read_bt = [&](int s, int nb, bf16x8 (&bt)[3]) {
+                const int pos = 32 * (nb >> 1) + 8 * vv + 4 * (nb & 1);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) {
+                    const u32x2 lo = lds_read_tr16(&sB[x6_off_tr<HELIX_CS, NCH>(pl, 32 * s + 8 * q + rr4, pos >> 3) + (pos & 7)]);
+                    const u32x2 hi = lds_read_tr16(&sB[x6_off_tr<HELIX_CS, NCH>(pl, 32 * s + 8 * q + 4 + rr4, pos >> 3) + (pos & 7)]);
+                    bt[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                }
+            };
             constexpr int NI = 2 * NB;
             bf16x8 bt[PF + 1][3], xp[2][3];
 #pragma unroll
-            for (int k = 0; k < PF; ++k) x6_read<NP, 8>(sBt, 16 * (k % NB) + c16, 4 * (k / NB) + q, bt[k]);
+            for (int k = 0; k < PF; ++k) read_bt(k / NB, k % NB, bt[k]);
             split_x(0, xp[0]);
 #pragma unroll
             for (int it = 0; it < NI; ++it) {
                 const int s = it / NB, nb = it % NB;
                 const int nx = it + PF;
-                if (nx < NI) x6_read<NP, 8>(sBt, 16 * (nx % NB) + c16, 4 * (nx / NB) + q, bt[nx % (PF + 1)]);
+                if (nx < NI) read_bt(nx / NB, nx % NB, bt[nx % (PF + 1)]);
                 if (nb == 1 && s == 0) split_x(1, xp[1]);
                 __builtin_amdgcn_sched_barrier(0);
                 R[nb] = wx6_mfma(bt[it % (PF + 1)], xp[s], R[nb]);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        __syncthreads();   // (3)
-
         __builtin_amdgcn_sched_barrier(0);
         split_b(runs, bw);
-        write_bt(bw, j0, u);
         __builtin_amdgcn_sched_barrier(0);
         load_runs_x6(runs, p, B_g, C_g, min(c + 2, c_end - 1), N, j0, u);
 
@@ -475,7 +474,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
             }
         }
         store_y16<float>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
-        __syncthreads();   // (4)
+        __syncthreads();   // (3)
     }
 }
 
