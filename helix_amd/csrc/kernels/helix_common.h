@@ -374,30 +374,11 @@ HELIX_DEV int x6_off(int k, int r, int c) {
     return ((k * ROWS + r) * NCH + (c ^ f)) * 8;
 }
 
-// The same planes with the chunk swizzle f(r) = 4 (r % 4) + (r / 4) % 4 (the
-// two 2-bit fields of r % 16 swapped; 16-chunk rows only). Operand reads of 16
-// consecutive rows still take every chunk position once, and so do LDS
-// transpose reads (lds_read_tr16) whose 16 lanes name rows 4 m + r (r = 0..3)
-// and four consecutive chunks: the rows' low bits move the chunk's high ones.
-template <int ROWS, int NCH>
-HELIX_DEV int x6_off_tr(int k, int r, int c) {
-    static_assert(NCH == 16, "rows of 16 chunks");
-    const int f = ((r & 3) << 2) | ((r >> 2) & 3);
-    return ((k * ROWS + r) * NCH + (c ^ f)) * 8;
-}
-
 // The three planes' chunk c of row r, as MFMA operands.
 template <int ROWS, int NCH>
 HELIX_DEV void x6_read(const __bf16* planes, int r, int c, bf16x8 (&o)[3]) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) o[k] = *reinterpret_cast<const bf16x8*>(&planes[x6_off<ROWS, NCH>(k, r, c)]);
-}
-
-// The same with the x6_off_tr swizzle.
-template <int ROWS, int NCH>
-HELIX_DEV void x6_read_tr(const __bf16* planes, int r, int c, bf16x8 (&o)[3]) {
-#pragma unroll
-    for (int k = 0; k < 3; ++k) o[k] = *reinterpret_cast<const bf16x8*>(&planes[x6_off_tr<ROWS, NCH>(k, r, c)]);
 }
 
 // Split eight fp32 values and store them as chunk c of row r (three planes).

@@ -131,7 +131,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     constexpr int PL_M  = 3 * HELIX_CS * HELIX_CS;
     constexpr int PF = 2;                      // products an operand read runs ahead
     __shared__ __attribute__((aligned(16))) __bf16 sC[PL_CB];
-    __shared__ __attribute__((aligned(16))) __bf16 sB[PL_CB];          // x6_off_tr swizzle
+    __shared__ __attribute__((aligned(16))) __bf16 sBt[3 * NP * HELIX_CS];   // B^T[n][j] planes
     __shared__ __attribute__((aligned(16))) __bf16 sM[HPW * PL_M];     // each head's M[t][j] planes
     __shared__ __attribute__((aligned(16))) float sDt[HPW][HELIX_CS];    // dt_j (0 past tlen)
     __shared__ __attribute__((aligned(16))) float sSd[HPW][HELIX_CS];    // exp(L_end - Lcum_j)
@@ -209,17 +209,17 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 split3_pair(as_f32(rn.b[k][e >> 1][2 * (e & 1)]), as_f32(rn.b[k][e >> 1][2 * (e & 1) + 1]),
                             bw[k][0][e], bw[k][1][e], bw[k][2][e]);
     };
-    auto write_b = [&](const unsigned (&bw)[2][3][4], int j0, int cpos) {
+    // B^T[n][j0 .. j0 + 1], n = 8u + e (natural order): the halves of rows
+    // j0 and j0 + 1 as one 4-byte store.
+    auto write_bt = [&](const unsigned (&bw)[2][3][4], int j0, int u) {
 #pragma unroll
-        for (int k = 0; k < 2; ++k)
+        for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int pos = cpos + 8 * hh;
-                    *reinterpret_cast<u32x2*>(&sB[x6_off_tr<HELIX_CS, NCH>(pl, j0 + k, pos >> 3) + (pos & 7)]) =
-                        u32x2{bw[k][pl][2 * hh], bw[k][pl][2 * hh + 1]};
-                }
+            for (int e = 0; e < 8; ++e) {
+                const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
+                const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
+                *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
+            }
     };
     auto tlen_of = [&](int c) { return min(HELIX_CS, p.n_tok - (p.chunk_base + c) * HELIX_CS); };
 
@@ -256,9 +256,9 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
 
     // Three barriers per chunk: (1) the chunk's planes and records are staged;
     // (2) M is written and G1 and G3 are done with C (the next chunk's C
-    // planes are staged behind it); (3) G4 is done with B (the next chunk's B
-    // planes are written at the top of the loop). G2 reads M after (2); the
-    // next chunk writes M only after its (1).
+    // planes are staged behind it); (3) G1 and G4 are done with B^T (the next
+    // chunk's B^T planes are written at the top of the loop). G2 reads M after
+    // (2); the next chunk writes M only after its (1).
     for (int c = c_begin; c < c_end; ++c) {
         const int t0   = (p.chunk_base + c) * HELIX_CS;
         const int tlen = tlen_of(c);
@@ -273,7 +273,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         const int cpos = wx6_perm32(8 * u);    // K position of 8u; 8u + 4 sits 8 further
         const int pp = 16 * w4 + c16;          // this lane's P column in the slab
 
-        write_b(bw, j0, cpos);
+        write_bt(bw, j0, u);
 
         // ---- decay records of the two heads --------------------------------
         if (w4 == 0) {
@@ -319,8 +319,21 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 const int tb = wx6_tb(idx), jb = wx6_jb(idx);
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
+                    // B rows j = 16 jb + c16 by transpose reads of B^T: K slot
+                    // 4 h + r of lane group q is C's column 32 s + 8 q + 4 h + r,
+                    // state index 32 s + 16 h + 4 q + r (perm32); lane 4 r + v
+                    // names that row of B^T and tokens 16 jb + 4 v .. + 3.
                     bf16x8 av[3], bv[3];
-                    x6_read_tr<HELIX_CS, NCH>(sB, 16 * jb + c16, 4 * s + q, av);
+                    {
+                        const int jc = 16 * jb + 4 * (c16 & 3);
+                        const int nr = 32 * s + 4 * q + (c16 >> 2);
+#pragma unroll
+                        for (int pl = 0; pl < 3; ++pl) {
+                            const u32x2 lo = lds_read_tr16(&sBt[x6_off<NP, 8>(pl, nr, jc >> 3) + (jc & 7)]);
+                            const u32x2 hi = lds_read_tr16(&sBt[x6_off<NP, 8>(pl, nr + 16, jc >> 3) + (jc & 7)]);
+                            av[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                        }
+                    }
                     x6_read<HELIX_CS, NCH>(sC, 16 * tb + c16, 4 * s + q, bv);
                     d[i] = wx6_mfma(av, bv, d[i]);
                 }
@@ -417,20 +430,8 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 }
                 x6_split8(xs, xp);
             };
-            // B^T operand by LDS transpose reads of B's planes: K slot 4 h + r
-            // of lane group q in step s is token j = 32 s + 8 q + 4 h + r (the
-            // order of xs); lane 4 r + v names row j and the state indices
-            // 16 nb + 4 v .. + 3, which perm32 keeps together at
-            // 32 (nb / 2) + 8 v + 4 (nb % 2).
-            const int rr4 = c16 >> 2, vv = c16 & 3;
             auto read_bt = [&](int s, int nb, bf16x8 (&bt)[3]) {
-                const int pos = 32 * (nb >> 1) + 8 * vv + 4 * (nb & 1);
-#pragma unroll
-                for (int pl = 0; pl < 3; ++pl) {
-                    const u32x2 lo = lds_read_tr16(&sB[x6_off_tr<HELIX_CS, NCH>(pl, 32 * s + 8 * q + rr4, pos >> 3) + (pos & 7)]);
-                    const u32x2 hi = lds_read_tr16(&sB[x6_off_tr<HELIX_CS, NCH>(pl, 32 * s + 8 * q + 4 + rr4, pos >> 3) + (pos & 7)]);
-                    bt[pl] = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-                }
+                x6_read<NP, 8>(sBt, 16 * nb + c16, 4 * s + q, bt);
             };
             constexpr int NI = 2 * NB;
             bf16x8 bt[PF + 1][3], xp[2][3];
