@@ -12,26 +12,30 @@
 // registers for the whole sequence: s0 is read once at the start and s1
 // written once at the end.
 //
-// MI355X layout: one workgroup of four waves per (seq, head, 16-channel
-// block of a P slab), on v_mfma_f32_16x16x4_f32, fp32 throughout. Four
-// blocks per slab give four times the workgroups of a slab-wide walk (256 at
-// 64 heads), so a single sequence fills the chip. Wave w produces y's t block
-// w (all 16 channels) and advances state tiles NT/4 w .. NT/4 (w + 1) - 1 (all
-// channels); the state is shared through LDS (sR, 16 x d_state fp32) once per
-// chunk, for every wave's G3. G1 (C B^T, shared by the block's channels) is
-// split over the waves by tile.
+// MI355X layout: one workgroup per (seq, head, 16-channel block of a P slab).
+// Four blocks per slab give four times the workgroups of a slab-wide walk
+// (256 at 64 heads), so a single sequence fills the chip. Two forms:
+//   - d_state <= 128 with fp32 storage (X6): eight waves in two roles (y
+//     waves and state waves, see scan_1pass_impl), every product on six
+//     v_mfma_f32_16x16x32_bf16 of three bf16 split planes (fp32 accuracy),
+//     C, B, the state and M^T shared as planes in LDS, two barriers per
+//     chunk. 150.5 KiB of LDS at d_state 128.
+//   - otherwise (d_state 256, 16-bit storage, diagonal A):
+//     v_mfma_f32_16x16x4_f32, fp32 throughout. With four waves, wave w
+//     produces y's t block w (all 16 channels) and advances state tiles
+//     NT/4 w .. NT/4 (w + 1) - 1; the state is shared through LDS (sR,
+//     16 x d_state fp32) once per chunk for every wave's G3; G1 (C B^T,
+//     shared by the block's channels) is split over the waves by tile; M
+//     reuses B's rows once G1 and G4 are done with them. 150 KiB of LDS at
+//     d_state 256.
 //   16x16x4 layouts: A[i][k]: lane holds A[lane%16][lane/16];
 //                    B[k][j]: lane holds B[lane/16][lane%16];
 //                    D[i][j]: lane, reg r holds D[4*(lane/16) + r][lane%16].
 // The state tile nt is R[n][p] for n = 16 nt .. 16 nt + 15 (M = n, N = p).
-// K order: G1 and G3 step s of a 16-wide K block takes k = 4*(lane/16) + s,
-// so the A operand's four k of a block are one 16-byte LDS read, and so are
-// G3's four state values (sR row p); G2 and G4 take token j = 4 s + lane/16.
-// Both operands of a product use the same order.
-//
-// LDS: C and B rows (fp32, 64 x (np+4)), dtX (64 x 16), the state (16 x
-// (np+4)), the chunk's Lcum in fp64 and two 64-vectors: 150 KiB at d_state
-// 256. M reuses B's rows once G1 and G4 are done with them.
+// K order (fp32 MFMA): G1 and G3 step s of a 16-wide K block takes
+// k = 4*(lane/16) + s, so the A operand's four k of a block are one 16-byte
+// LDS read, and so are G3's four state values (sR row p); G2 and G4 take
+// token j = 4 s + lane/16. Both operands of a product use the same order.
 #include "helix_common.h"
 
 #include "pass_c_stage.h"
