@@ -258,92 +258,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
 
     // The segment's start state, after the first chunk's loads are issued so
     // that their latency overlaps the prologue's tile loads.
-    // R[n][pp], n = 16 nb + 4 q + r, from the slab tile of S_seg(s): in the
-    // tile's unit layout that is unit ((pt NT32 + nb/2) 4 + r4) 64 + lane'
-    // with pt = w4/2, r4 = 2 (nb%2) + q/2, lane' = 32 (q%2) + 16 (w4%2) + c16.
     f32x4 R[NB];
-    {
-        const float* tiles = b.s_seg + seq * p.sg_seq + state_tile_off(p, h, slab);
-        const int vunit = 64 * (q >> 1) + 32 * (q & 1) + 16 * (w4 & 1) + c16;
-        const int pt = w4 >> 1;
-        auto load_tile = [&](int s, f32x4 (&T)[NB]) {
-            const helix_rsrc rg = make_rsrc(tiles + (long long)s * p.sg_seg, 64u * NP * sizeof(float));
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                T[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
-        };
-        if (!p.fuse_b) {
-            // S_seg of the Pass A segment this walk segment starts at, from Pass B.
-            load_tile(seg * (p.walk_len / p.seg_len), R);
-        } else {
-            // Pass B folded in (single-group plans whose walk segments are Pass
-            // A's segments): the tiles hold Pass A's
-            // segment aggregates D_s, and this workgroup runs Pass B's
-            // recurrence (helix_state_scan_f32, same operation order) up to
-            // its own segment:
-            //   carry = s0[ids[seq]];  carry = exp(segld_s) carry + D_s,  s < seg
-            // The last segment's workgroup takes one more step and stores s1.
-            // State index n = 16 nb + 4 q + r of channel p0 + pp; tile
-            // padding (pp >= pw, n >= d_state) starts from zero, as in Pass B.
-            // ids and the segment log-decays come through the scalar unit, so
-            // using them does not wait for the first chunk's vector loads.
-            const int src = p.has_ids ? sload_i32(b.ids, seq) : seq;
-            const long long hs = (long long)h * p.s_s[0];
-            const unsigned sbytes = (unsigned)(((long long)(P - 1) * p.s_s[1] + N) * 4);
-            const int soff = (int)((p0 + pp) * p.s_s[1]) * 4;
-            const helix_rsrc r0 = make_rsrc(b.s0 + src * p.seq_s + hs, sbytes);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const int n = 16 * nb + 4 * q;
-                const int off = store_off_if_lt(soff + 4 * n, pp, pw, n, N);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    R[nb][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r0, off + 4 * r, 0, 0));
-            }
-            const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
-            const bool last = seg == p.n_seg - 1;
-            const int nd = seg + (last ? 1 : 0);
-            // Tiles in flight: four up to d_state 128, two at 256 (32 f32x4
-            // registers either way; four tiles of 16 spill at d_state 256).
-            constexpr int BLK = NB <= 8 ? 4 : 2;
-            for (int sb = 0; sb < nd; sb += BLK) {
-                f32x4 T[BLK][NB];
-                float a[BLK];
-#pragma unroll
-                for (int k = 0; k < BLK; ++k) {
-                    const int s = min(sb + k, nd - 1);
-                    load_tile(s, T[k]);
-                    a[k] = expf(sload_f32(sd, (long long)s * p.n_head));
-                }
-#pragma unroll
-                for (int k = 0; k < BLK; ++k) {
-                    if (sb + k >= nd) break;
-                    if (sb + k < seg) {
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb) R[nb] = a[k] * R[nb] + T[k][nb];
-                    } else if (head_ok) {
-                        // s1[seq] = exp(segld_seg) S_seg(seg) + D_seg
-                        // Element by element: with the quad formed as one
-                        // vector expression, hipcc stored its first element
-                        // four times.
-                        const helix_rsrc r1 = make_rsrc(b.s1 + seq * p.seq_s + hs, sbytes);
-                        const float ak = a[k];
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb) {
-                            const int n = 16 * nb + 4 * q;
-                            const int off = store_off_if_lt(soff + 4 * n, pp, pw, n, N);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float v = ak * R[nb][r] + T[k][nb][r];
-                                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r1,
-                                                                      off + 4 * r, 0, 0);
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    }
+    walk_start_state<NP>(R, p, b, seq, h, slab, seg, p0, pw, pp, q, w4, c16, head_ok);
 
     // Two barriers per chunk: (1) after staging, (2) after G1 has written M.
     // Whatever a wave stages for chunk c+1 was last read before barrier (2)

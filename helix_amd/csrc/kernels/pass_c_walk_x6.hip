@@ -235,21 +235,12 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         load_runs_x6(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u);
     }
 
-    // The segment's start state S_seg from Pass B (its Pass A segment is the
-    // one the walk segment starts at). R[n][pp], n = 16 nb + 4 q + r, from the
-    // slab tile: unit ((pt NT32 + nb/2) 4 + r4) 64 + lane' with pt = w4/2,
-    // r4 = 2 (nb%2) + q/2, lane' = 32 (q%2) + 16 (w4%2) + c16.
+    // The segment's start state: S_seg from Pass B, or Pass B's recurrence
+    // over Pass A's aggregates run here (p.fuse_b).
     f32x4 R[NB];
     {
-        const float* tiles = b.s_seg + seq * p.sg_seq + state_tile_off(p, h, slab) +
-                             (long long)(seg * (p.walk_len / p.seg_len)) * p.sg_seg;
-        const helix_rsrc rg = make_rsrc(tiles, 64u * NP * sizeof(float));
-        const int q = lane >> 4;
-        const int vunit = 64 * (q >> 1) + 32 * (q & 1) + 16 * (w4 & 1) + (lane & 15);
-        const int pt = w4 >> 1;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            R[nb] = buf_unit<float>(rg, vunit, ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64);
+        const int q = lane >> 4, c16 = lane & 15;
+        walk_start_state<NP>(R, p, b, seq, h, slab, seg, p0, pw, 16 * w4 + c16, q, w4, c16, head_ok);
     }
 
     __bf16* const sMh = sM + hw * PL_M;

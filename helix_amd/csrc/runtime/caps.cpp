@@ -140,6 +140,7 @@ struct TraitTable {
                 t.mfma_c = "v_mfma_f32_16x16x32_bf16 (bf16x6 split operands)";
                 t.walk = true;
                 t.walk_hpw = 2;
+                t.walk_fuse_b = true;
                 t.rec_kind = 2;
             }
             for (int io = 0; io < 3; ++io)

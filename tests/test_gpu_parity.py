@@ -73,6 +73,10 @@ MODES = [
     # The fp32 path's chunk-parallel Pass C on per-chunk states stored by
     # Pass A, which d_state 65..128 replaces with the walk by default.
     ("fp32/chunk/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "0"}, True),
+    # The fp32 walk with Pass B launched on its own and with Pass B's segment
+    # scan in its prologue.
+    ("fp32/passB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_FUSE_B": "0"}, True),
+    ("fp32/fuseB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_FUSE_B": "1"}, True),
     ("fp32/chunk/sm", HELIX_BACKEND_SGMMA, 1, "short", {"HELIX_F32_WALK": "0"}, True),
     ("bf16", HELIX_BACKEND_MPP, None, "short", {}, True),
     ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}, True),

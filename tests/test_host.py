@@ -436,10 +436,10 @@ def test_plan_invariants(host, name, backend):
     assert info.walk_len % info.seg_len == 0
     assert info.walks_per_group == -(-info.chunks_per_group // info.walk_len)
     assert walk or info.walk_len == info.seg_len
-    # The bf16 walk runs Pass B's segment scan in its prologue when the plan
-    # has one group of at most four segments that are also its walk segments:
-    # no Pass B launch.
-    fused = walk and backend == HELIX_BACKEND_MPP and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
+    # The walks (bf16, and the fp32 path's at d_state 65..128) run Pass B's
+    # segment scan in their prologue when the plan has one group of at most
+    # four segments that are also its walk segments: no Pass B launch.
+    fused = walk and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
 
