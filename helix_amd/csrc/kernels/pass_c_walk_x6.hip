@@ -29,7 +29,8 @@
 //   B    [64 j][NP n]   perm32 n order             G1; afterwards the region
 //   M    [64 t][64 j]   one per head               holds the heads' M (G2)
 //   B^T  [NP n][64 j]   natural n order            G4
-// and the heads' decay records: 145 KiB at d_state 128, one workgroup per CU.
+// and the heads' decay records: 145 KiB at d_state 128 (one workgroup per
+// CU), 98 KiB at d_state 64.
 // The B operands of G2 and G4 (dt x and decay dt x at the lane's own column
 // and K tokens) and of G3 (R) are split in registers.
 #include "helix_common.h"
@@ -67,14 +68,18 @@ HELIX_DEV int wx6_jb(int idx) {
     return idx - tb * (tb + 1) / 2;
 }
 
-// This lane's B and C runs of one chunk (fp32): state indices 8u .. 8u+7 of
-// rows j0 and j0 + 1, two 16-byte words each.
+// This lane's B and C runs of one chunk (fp32) of rows j0 and j0 + 1: NH
+// 16-byte words per row, state indices 8u + 4 hh .. + 3 for hh = 0 .. NH - 1
+// (d_state 128: NH = 2, the whole run 8u .. 8u + 7) or for hh = hf alone
+// (d_state 64: NH = 1, lanes 8 apart take the run's two halves).
+template <int NH>
 struct RunsWX6 {
-    u32x4 b[2][2], c[2][2];
+    u32x4 b[2][NH], c[2][NH];
 };
 
-__device__ __forceinline__ void load_runs_x6(RunsWX6& r, const HelixScanParams& p, const float* __restrict__ B_g,
-                                             const float* __restrict__ C_g, int c, int N, int j0, int u) {
+template <int NH>
+__device__ __forceinline__ void load_runs_x6(RunsWX6<NH>& r, const HelixScanParams& p, const float* __restrict__ B_g,
+                                             const float* __restrict__ C_g, int c, int N, int j0, int u, int hf) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sb0 = sgpr_fresh((int)p.s_b[0]), sc0 = sgpr_fresh((int)p.s_c[0]);
@@ -85,9 +90,10 @@ __device__ __forceinline__ void load_runs_x6(RunsWX6& r, const HelixScanParams& 
     for (int k = 0; k < 2; ++k) {
         const int jr = min(j0 + k, tlen - 1);
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4 + 16 * w, 0, 0);
-            r.c[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4 + 16 * w, 0, 0);
+        for (int w = 0; w < NH; ++w) {
+            const int hh = NH == 2 ? w : hf;
+            r.b[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rb, (n0 + jr * sb0) * 4 + 16 * hh, 0, 0);
+            r.c[k][w] = __builtin_amdgcn_raw_buffer_load_b128(rc, (n0 + jr * sc0) * 4 + 16 * hh, 0, 0);
         }
     }
 }
@@ -121,7 +127,10 @@ __device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParam
 
 template <int NP>
 __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
-    static_assert(NP == 128, "two rows per lane in the staging: d_state 128");
+    static_assert(NP == 64 || NP == 128, "d_state 64 or 128");
+    // Staging lanes: 16 per pair of rows; a run of eight state indices per
+    // lane at d_state 128 (NH = 2 words per row), half a run at 64 (NH = 1).
+    constexpr int NH = NP / 64;
     constexpr int HPW = 2;                     // heads per workgroup, four waves each
     constexpr int NB  = NP / 16;               // 16-row state tiles of R
     constexpr int KS  = NP / 32;               // K steps over the state
@@ -171,68 +180,73 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     const float* __restrict__ B_g = b.B + seq * p.seq_b + g * p.s_b[1];
     const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
 
-    // Staging: lane (u, rr) holds state indices 8u .. 8u+7 of rows j0 and j0 + 1
-    // (the wave's eight rows, 16 lanes per row). A chunk's planes are staged
+    // Staging: lane (c16, rr) holds its run's state indices (RunsWX6) of rows
+    // j0 and j0 + 1 (the wave's eight rows, 16 lanes per pair). A chunk's planes are staged
     // while the previous chunk's products run: C once G1 and G3 are done with
     // it, B once G4 is. C is zeroed past tlen and d_state, which is all G1 and
     // G3 need; B rows past tlen only meet dt = 0 columns in G4.
-    auto stage_c = [&](const RunsWX6& rn, int tl, int j0, int u, int cpos) {
+    // Word w of a run holds state indices 8u + 4 hh .. + 3, at K position
+    // cpos + 8 hh (perm32 keeps each group of four together).
+    auto half_of = [&](int w, int hf) { return NH == 2 ? w : hf; };
+    auto stage_c = [&](const RunsWX6<NH>& rn, int tl, int j0, int u, int hf, int cpos) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int j = j0 + k;
             const unsigned keep = ~(unsigned)(((tl - 1 - j) | (N - 1 - 8 * u)) >> 31);
-            u32x2 cq[3][2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                unsigned c0, c1, c2;
-                split3_pair(as_f32(rn.c[k][e >> 1][2 * (e & 1)] & keep), as_f32(rn.c[k][e >> 1][2 * (e & 1) + 1] & keep),
-                            c0, c1, c2);
-                cq[0][e >> 1][e & 1] = c0;
-                cq[1][e >> 1][e & 1] = c1;
-                cq[2][e >> 1][e & 1] = c2;
-            }
+            for (int w = 0; w < NH; ++w) {
+                u32x2 cq[3];
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int pos = cpos + 8 * hh;
-                    *reinterpret_cast<u32x2*>(&sC[x6_off<HELIX_CS, NCH>(pl, j, pos >> 3) + (pos & 7)]) = cq[pl][hh];
+                for (int e = 0; e < 2; ++e) {
+                    unsigned c0, c1, c2;
+                    split3_pair(as_f32(rn.c[k][w][2 * e] & keep), as_f32(rn.c[k][w][2 * e + 1] & keep), c0, c1, c2);
+                    cq[0][e] = c0;
+                    cq[1][e] = c1;
+                    cq[2][e] = c2;
                 }
+                const int pos = cpos + 8 * half_of(w, hf);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl)
+                    *reinterpret_cast<u32x2*>(&sC[x6_off<HELIX_CS, NCH>(pl, j, pos >> 3) + (pos & 7)]) = cq[pl];
+            }
         }
     };
-    // B's split planes, bw[row k][plane][pair e] (state indices 8u + 2e, +1).
-    auto split_b = [&](const RunsWX6& rn, unsigned (&bw)[2][3][4]) {
+    // B's split planes, bw[row k][plane][pair e] (state indices 8u + 4 hh +
+    // 2 (e % 2), +1 for word w = e / 2).
+    auto split_b = [&](const RunsWX6<NH>& rn, unsigned (&bw)[2][3][2 * NH]) {
 #pragma unroll
         for (int k = 0; k < 2; ++k)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+            for (int e = 0; e < 2 * NH; ++e)
                 split3_pair(as_f32(rn.b[k][e >> 1][2 * (e & 1)]), as_f32(rn.b[k][e >> 1][2 * (e & 1) + 1]),
                             bw[k][0][e], bw[k][1][e], bw[k][2][e]);
     };
-    // B^T[n][j0 .. j0 + 1], n = 8u + e (natural order): the halves of rows
-    // j0 and j0 + 1 as one 4-byte store.
-    auto write_bt = [&](const unsigned (&bw)[2][3][4], int j0, int u) {
+    // B^T[n][j0 .. j0 + 1] (natural n order): the halves of rows j0 and
+    // j0 + 1 as one 4-byte store.
+    auto write_bt = [&](const unsigned (&bw)[2][3][2 * NH], int j0, int u, int hf) {
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
+            for (int e = 0; e < 4 * NH; ++e) {
                 const unsigned wa = bw[0][pl][e >> 1], wb = bw[1][pl][e >> 1];
                 const unsigned v = (e & 1) ? ((wa >> 16) | (wb & 0xffff0000u)) : ((wa & 0xffffu) | (wb << 16));
-                *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, 8 * u + e, j0 >> 3) + (j0 & 7)]) = v;
+                const int n = 8 * u + 4 * half_of(e >> 2, hf) + (e & 3);
+                *reinterpret_cast<unsigned*>(&sBt[x6_off<NP, 8>(pl, n, j0 >> 3) + (j0 & 7)]) = v;
             }
     };
     auto tlen_of = [&](int c) { return min(HELIX_CS, p.n_tok - (p.chunk_base + c) * HELIX_CS); };
 
-    RunsWX6 runs;
-    unsigned bw[2][3][4];
+    RunsWX6<NH> runs;
+    unsigned bw[2][3][2 * NH];
     StageWX6 st;
     {
-        const int u = lane & 15, rr = lane >> 4, j0 = 8 * wave + 2 * rr;
-        load_runs_x6(runs, p, B_g, C_g, c_begin, N, j0, u);
-        load_stage_x6(st, p, rec_h, x_h, c_begin, lane, rr, 16 * w4 + u, pw);
-        stage_c(runs, tlen_of(c_begin), j0, u, wx6_perm32(8 * u));
+        const int c16 = lane & 15, rr = lane >> 4, j0 = 8 * wave + 2 * rr;
+        const int u = NH == 2 ? c16 : (c16 & 7), hf = NH == 2 ? 0 : (c16 >> 3);
+        load_runs_x6<NH>(runs, p, B_g, C_g, c_begin, N, j0, u, hf);
+        load_stage_x6(st, p, rec_h, x_h, c_begin, lane, rr, 16 * w4 + c16, pw);
+        stage_c(runs, tlen_of(c_begin), j0, u, hf, wx6_perm32(8 * u));
         split_b(runs, bw);
-        load_runs_x6(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u);
+        load_runs_x6<NH>(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u, hf);
     }
 
     // The segment's start state: S_seg from Pass B, or Pass B's recurrence
@@ -259,12 +273,13 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         // loop, the LDS addresses made from them would not fit the registers.
         const int ln = vgpr_opaque(lane);
         const int c16 = ln & 15, q = ln >> 4;  // MFMA operand row, K slot group
-        const int u = c16, rr = q;             // staging run and row pair
+        const int u = NH == 2 ? c16 : (c16 & 7), hf = NH == 2 ? 0 : (c16 >> 3);   // staging run, its half
+        const int rr = q;                      // staging row pair
         const int j0 = 8 * wave + 2 * rr;
         const int cpos = wx6_perm32(8 * u);    // K position of 8u; 8u + 4 sits 8 further
         const int pp = 16 * w4 + c16;          // this lane's P column in the slab
 
-        write_bt(bw, j0, u);
+        write_bt(bw, j0, u, hf);
 
         // ---- decay records of the two heads --------------------------------
         if (w4 == 0) {
@@ -404,7 +419,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         __syncthreads();   // (2)
 
         __builtin_amdgcn_sched_barrier(0);
-        stage_c(runs, tlen_of(cn), j0, u, cpos);
+        stage_c(runs, tlen_of(cn), j0, u, hf, cpos);
 
         // ---- G4: R <- exp(L_end) R + B^T . (decay dt x) (after G3 used R) ---
         // Products (s, nb) in order, B^T's planes read PF products ahead.
@@ -443,7 +458,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         __builtin_amdgcn_sched_barrier(0);
         split_b(runs, bw);
         __builtin_amdgcn_sched_barrier(0);
-        load_runs_x6(runs, p, B_g, C_g, min(c + 2, c_end - 1), N, j0, u);
+        load_runs_x6<NH>(runs, p, B_g, C_g, min(c + 2, c_end - 1), N, j0, u, hf);
 
         // ---- G2: y += M . dtX (t block tb needs j < 16 (tb + 1)) -----------
         // K step s covers j blocks 2s and 2s + 1; for tb = 0 and 2 the second
@@ -476,4 +491,5 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         scan_walk_x6_impl<NP>(p, b);                                                            \
     }
 
+HELIX_PASS_C_WALK_X6(64)
 HELIX_PASS_C_WALK_X6(128)

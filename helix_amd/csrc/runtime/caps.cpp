@@ -31,13 +31,13 @@ namespace {
 //     Pass C helix_chunk_out_x6_n{64,128}  bf16x6 split products
 //            helix_chunk_out_f32_n256      fp32 MFMA (the bf16x6 planes of a
 //                                          d_state 256 tile exceed the LDS)
-//   fp32 path at d_state 65..128 (fp32 storage): Pass C walks each segment's
+//   fp32 path at d_state <= 128 (fp32 storage): Pass C walks each segment's
 //   chunks on bf16x6 products with the state in registers, so Pass A stores no
 //   per-chunk states (HELIX_F32_WALK=0 keeps the chunk-parallel Pass C):
-//     Pass A helix_chunk_state_hb_x6agg_r64_n128  segment aggregates, fp64
-//                                                 decay records
-//     Pass B helix_state_scan_f32
-//     Pass C helix_scan_walk_x6_n128
+//     Pass A helix_chunk_state_hb_x6agg_r64_n{64,128}  segment aggregates,
+//                                                      fp64 decay records
+//     Pass B helix_state_scan_f32 (or the walk's prologue, fuse_b)
+//     Pass C helix_scan_walk_x6_n{64,128}
 //   bf16 path (AUTO or MPP, multipass): Pass C walks each segment's chunks on
 //   bf16 MFMA with the state in registers; Pass A computes the segment
 //   aggregates only, on six split products (fp32 accuracy, the reference's
@@ -68,10 +68,10 @@ int io_index(helix_dtype io) { return io == HELIX_BF16 ? 1 : io == HELIX_F16 ? 2
 // Traits are composed from these choices, once per process; the names live as
 // long as the process.
 struct TraitTable {
-    // [io][k]: single pass; [k]: diagonal A; [k]: fp32 path; the fp32 path's
-    // walk (d_state 128); [io][split6][bccopy][k]: bf16 path (bccopy only with
-    // fp32 storage).
-    HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk, bf16[3][2][2][3];
+    // [io][k]: single pass; [k]: diagonal A; [k]: fp32 path; [k]: the fp32
+    // path's walk (d_state <= 128); [io][split6][bccopy][k]: bf16 path (bccopy
+    // only with fp32 storage).
+    HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk[2], bf16[3][2][2][3];
     std::vector<std::string> names;   // every kernel name, deduplicated
     std::deque<std::string> store;    // backing storage of the strings above
 
@@ -131,8 +131,8 @@ struct TraitTable {
                 t.np = kNps[k];
                 t.rec_kind = x6c ? 2 : 0;
             }
-            if (kNps[k] == 128) {
-                HelixMatmulTraits& t = f32walk;
+            if (k < 2) {
+                HelixMatmulTraits& t = f32walk[k];
                 t = f32[k];
                 t.name = keep("mfma fp32, passes A and C bf16x6, chunk walk" + upto);
                 t.k_chunk_state = kernel("helix_chunk_state_hb_x6agg_r64_n" + np);
@@ -242,7 +242,8 @@ helix_tuning tuning_from_env() {
     t.bccopy = bc == 0 ? 0 : bc > 0 ? 1 : -1;
     t.seg_len = (int)env_long("HELIX_SEG_LEN", 0);
     t.hblk = (int)env_long("HELIX_HBLK", 0);
-    if (env_switch("HELIX_F32_WALK") == 0) t.f32_walk = 0;
+    const int fw = env_switch("HELIX_F32_WALK");
+    if (fw >= 0) t.f32_walk = fw > 0 ? 1 : 0;
     return t;
 }
 
@@ -261,6 +262,10 @@ void set_error(const helix_ctx* ctx, const std::string& msg) {
     t_last_error = msg;
 }
 
+namespace {
+int choose_walk_len(const helix_scan_desc& d, int cpg);
+}
+
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d) {
     const helix_tuning& tu = tuning_of(ctx);
     const TraitTable& tt = table();
@@ -272,7 +277,13 @@ const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_de
     const bool bf16 = (d.backend == HELIX_BACKEND_AUTO || d.backend == HELIX_BACKEND_MPP) && !tu.force_fp32;
     if (!bf16) {
         if (io) return tt.single[io][k];
-        return k == 1 && tu.f32_walk != 0 ? tt.f32walk : tt.f32[k];
+        // A walk of one chunk carries no state between chunks: where the plan
+        // gives one-chunk walks (short sequences of few heads), the
+        // chunk-parallel Pass C is the faster form (config 0: 23.0 against
+        // 24.0 us). HELIX_F32_WALK=0 / 1 pins either form.
+        const bool walk = k < 2 && (tu.f32_walk == 1 ||
+                                    (tu.f32_walk < 0 && choose_walk_len(d, (d.n_tok + HELIX_CS - 1) / HELIX_CS) > 1));
+        return walk ? tt.f32walk[k] : tt.f32[k];
     }
     const int bc = io == 0 && bccopy_on(tu, d) ? 1 : 0;
     return tt.bf16[io][tu.passa_split == 3 ? 0 : 1][bc][k];

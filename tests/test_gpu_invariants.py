@@ -42,8 +42,8 @@ PATHS = [
     # through it), and in its own launch.
     ("bf16/fuseB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "1"}),
     ("bf16/passB", HELIX_BACKEND_MPP, True, {"HELIX_FUSE_B": "0"}),
-    ("fp32/fuseB", HELIX_BACKEND_SGMMA, True, {"HELIX_FUSE_B": "1"}),
-    ("fp32/passB", HELIX_BACKEND_SGMMA, True, {"HELIX_FUSE_B": "0"}),
+    ("fp32/fuseB", HELIX_BACKEND_SGMMA, True, {"HELIX_F32_WALK": "1", "HELIX_FUSE_B": "1"}),
+    ("fp32/passB", HELIX_BACKEND_SGMMA, True, {"HELIX_F32_WALK": "1", "HELIX_FUSE_B": "0"}),
     # The walk on the caller's fp32 B and C, and on Pass A's bf16 copies of
     # them (by default only past eight items per group).
     ("bf16/nocopy", HELIX_BACKEND_MPP, True, {"HELIX_WALK_BCCOPY": "0"}),

@@ -71,12 +71,16 @@ MODES = [
     ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}, True),
     ("fp32/sm/long", HELIX_BACKEND_SGMMA, 1, "long", {}, True),
     # The fp32 path's chunk-parallel Pass C on per-chunk states stored by
-    # Pass A, which d_state 65..128 replaces with the walk by default.
+    # Pass A, which d_state <= 128 replaces with the walk wherever the plan
+    # walks more than one chunk.
     ("fp32/chunk/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "0"}, True),
-    # The fp32 walk with Pass B launched on its own and with Pass B's segment
-    # scan in its prologue.
-    ("fp32/passB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_FUSE_B": "0"}, True),
-    ("fp32/fuseB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_FUSE_B": "1"}, True),
+    # The fp32 walk (pinned: most shapes here plan one-chunk walks) with Pass
+    # B launched on its own, with Pass B's segment scan in its prologue, over
+    # four-chunk walks, and over several chunk groups carried through s1.
+    ("fp32/passB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "1", "HELIX_FUSE_B": "0"}, True),
+    ("fp32/fuseB/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "1", "HELIX_FUSE_B": "1"}, True),
+    ("fp32/walk4/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_F32_WALK": "1", "HELIX_SEG_LEN": "4"}, True),
+    ("fp32/walk/sm", HELIX_BACKEND_SGMMA, 1, "short", {"HELIX_F32_WALK": "1"}, True),
     ("fp32/chunk/sm", HELIX_BACKEND_SGMMA, 1, "short", {"HELIX_F32_WALK": "0"}, True),
     ("bf16", HELIX_BACKEND_MPP, None, "short", {}, True),
     ("bf16/sm", HELIX_BACKEND_MPP, 1, "short", {}, True),

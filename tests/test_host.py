@@ -278,8 +278,8 @@ def test_backend_selection(host):
     assert host.select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_MPP
     assert host.select_backend(mp(shape, HELIX_BACKEND_SGMMA)) == HELIX_BACKEND_SGMMA
     # bf16x6 split products: Pass A on every path, and the fp32 path's Pass C
-    # up to d_state 128, which at d_state 65..128 walks each segment with the
-    # state in registers (HELIX_F32_WALK=0: chunk-parallel on stored states).
+    # up to d_state 128, which walks each segment with the state in registers
+    # (HELIX_F32_WALK=0: chunk-parallel on stored states).
     assert (host.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6, chunk walk (d_state<=128)")
     kw = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
@@ -306,8 +306,21 @@ def test_backend_selection(host):
     assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x3agg_n128"
     assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
-    assert (host.backend_desc(mp((64, 1, 1, 64, 64, 1), HELIX_BACKEND_SGMMA))
-            == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
+    # d_state 64 walks too, where the plan walks more than one chunk; one
+    # chunk (a single-chunk sequence, or config 0's four chunks over eight
+    # heads) keeps the chunk-parallel Pass C unless HELIX_F32_WALK=1.
+    n64 = (8192, 1, 64, 64, 64, 8)
+    assert (host.backend_desc(mp(n64, HELIX_BACKEND_SGMMA))
+            == "mfma fp32, passes A and C bf16x6, chunk walk (d_state<=64)")
+    k64 = host.plan_info(mp(n64, HELIX_BACKEND_SGMMA))
+    assert (k64.kernel_a, k64.kernel_c) == (b"helix_chunk_state_hb_x6agg_r64_n64", b"helix_scan_walk_x6_n64")
+    assert k64.walk_len > 1
+    assert tuned(HELIX_F32_WALK="0").plan_info(mp(n64, HELIX_BACKEND_SGMMA)).kernel_c == b"helix_chunk_out_x6_n64"
+    for short in ((64, 1, 1, 64, 64, 1), CONFIG_SHAPES["cfg0"]):
+        assert (host.backend_desc(mp(short, HELIX_BACKEND_SGMMA))
+                == "mfma fp32, passes A and C bf16x6 (d_state<=64)")
+        kw1 = tuned(HELIX_F32_WALK="1").plan_info(mp(short, HELIX_BACKEND_SGMMA))
+        assert kw1.kernel_c == b"helix_scan_walk_x6_n64" and kw1.walk_len == 1
     # The plan names the kernels each pass launches.
     k = host.plan_info(mp(shape))
     # Eight heads per group: the walk reads the caller's fp32 B and C (no
@@ -423,9 +436,9 @@ def test_plan_invariants(host, name, backend):
     assert info.bf16_state == (backend == HELIX_BACKEND_MPP)
     # The walking Pass C keeps the chunk-local states in registers, so its
     # plan holds no s_local region; it is the bf16 path's Pass C, and the
-    # fp32 path's at d_state 65..128.
+    # fp32 path's at d_state <= 128 where its walks are longer than a chunk.
     walk = b"walk" in info.kernel_c
-    assert walk == (backend == HELIX_BACKEND_MPP or 64 < N <= 128)
+    assert walk == (backend == HELIX_BACKEND_MPP or (N <= 128 and info.walk_len > 1))
     want_sl = state * info.chunks_per_group * 4 if (info.seg_len > 1 and not walk) else 0
     assert info.s_local_bytes == want_sl
     assert info.s_seg_bytes == state * info.segs_per_group * 4
@@ -436,7 +449,7 @@ def test_plan_invariants(host, name, backend):
     assert info.walk_len % info.seg_len == 0
     assert info.walks_per_group == -(-info.chunks_per_group // info.walk_len)
     assert walk or info.walk_len == info.seg_len
-    # The walks (bf16, and the fp32 path's at d_state 65..128) run Pass B's
+    # The walks (bf16, and the fp32 path's at d_state <= 128) run Pass B's
     # segment scan in their prologue when the plan has one group of at most
     # four segments that are also its walk segments: no Pass B launch.
     fused = walk and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
