@@ -62,13 +62,16 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
         const int nb = min(BLK, p.n_seg - s0);
         f32x4 d[BLK];
         float a[BLK];
+        // Loads past the block's end repeat its last segment: no branch
+        // between the loads, so they all issue before the first wait.
 #pragma unroll
         for (int k = 0; k < BLK; ++k) {
-            if (k < nb) {
-                d[k] = base[(long long)(s0 + k) * seg_stride];
-                a[k] = expf(sd[(long long)(s0 + k) * p.n_head]);
-            }
+            const long long sk = s0 + min(k, nb - 1);
+            d[k] = base[sk * seg_stride];
+            a[k] = sd[sk * p.n_head];
         }
+#pragma unroll
+        for (int k = 0; k < BLK; ++k) a[k] = expf(a[k]);
 #pragma unroll
         for (int k = 0; k < BLK; ++k) {
             if (k < nb) {
