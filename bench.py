@@ -37,7 +37,7 @@ PEAK_HBM = 8.0e12           # B/s
 PEAK_FP32_MFMA = 157.3e12   # FLOP/s
 PEAK_BF16_MFMA = 2516.6e12  # FLOP/s (dense)
 # Reference's published number for this metric and path: 3-pass + bf16 Pass C
-# on an Apple M5 Max (BASELINE.md, reference README.md:96-98).
+# on an Apple M5 Max (reference README.md:96-98).
 REF_TOKS = 1315051.0
 
 CFG = dict(L=8192, S=1, H=64, P=64, N=128, G=8)
@@ -368,7 +368,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the scan shards by head or by sequence without collectives, see DESIGN.md",
+              "the scan would shard by head or by sequence, with no collectives",
               file=sys.stderr)
         sys.exit(2)
 

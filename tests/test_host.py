@@ -557,7 +557,7 @@ def test_two_level_algebra(seg_len, cpg, memory):
 
 
 def test_flop_and_byte_counts_match_baseline():
-    # BASELINE.md section 2 / reference bench_scan.mm:205-209.
+    # The reference's own FLOP and byte counts (bench_scan.mm:205-209).
     assert abs(algorithmic_flops(2048, 1, 64, 64, 128) / 1e9 - 5.931) < 1e-3
     assert abs(algorithmic_flops(8192, 1, 64, 64, 128) / 1e9 - 23.723) < 1e-3
     assert abs(algorithmic_bytes(8192, 1, 64, 64, 128, 8) / 1e6 - 341.8) < 0.1
