@@ -292,7 +292,8 @@ const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_de
 // The walk's prologue loads up to segs_per_group segment aggregates per
 // workgroup, four at a time; past four segments the second round of loads
 // costs more than Pass B's own launch (config 2, 8 segments: 149 vs 142 us;
-// configs 4a/4b, 4 segments: 701 vs 712 and 767 vs 782 us).
+// configs 4a/4b, 4 segments, fused against launched: 624 vs 635 and 668 vs
+// 681 us).
 constexpr int kFuseBMaxSegs = 4;
 
 bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const MultipassPlan& plan) {
