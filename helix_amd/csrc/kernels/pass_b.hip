@@ -58,27 +58,37 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
     const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
     const int ratio = p.walk_len / p.seg_len;            // segments per walk
 
-    for (int s0 = 0; s0 < p.n_seg; s0 += BLK) {
-        const int nb = min(BLK, p.n_seg - s0);
-        f32x4 d[BLK];
-        float a[BLK];
-        // Loads past the block's end repeat its last segment: no branch
-        // between the loads, so they all issue before the first wait.
+    // One block of up to K segments from s0: loads past the block's end
+    // repeat its last segment, so there is no branch between the loads and
+    // they all issue before the first wait.
+    auto block = [&](auto kc, int s0) {
+        constexpr int K = decltype(kc)::value;
+        const int nb = min(K, p.n_seg - s0);
+        f32x4 d[K];
+        float a[K];
 #pragma unroll
-        for (int k = 0; k < BLK; ++k) {
+        for (int k = 0; k < K; ++k) {
             const long long sk = s0 + min(k, nb - 1);
             d[k] = base[sk * seg_stride];
             a[k] = sd[sk * p.n_head];
         }
 #pragma unroll
-        for (int k = 0; k < BLK; ++k) a[k] = expf(a[k]);
+        for (int k = 0; k < K; ++k) a[k] = expf(a[k]);
 #pragma unroll
-        for (int k = 0; k < BLK; ++k) {
+        for (int k = 0; k < K; ++k) {
             if (k < nb) {
                 if ((s0 + k) % ratio == 0) base[(long long)(s0 + k) * seg_stride] = carry;
                 carry = a[k] * carry + d[k];
             }
         }
+    };
+    // Blocks of 16 segments; a last block of at most 8 or 4 segments issues
+    // 8 or 4 loads.
+    for (int s0 = 0; s0 < p.n_seg; s0 += BLK) {
+        const int left = p.n_seg - s0;
+        if (left > 8) block(std::integral_constant<int, BLK>{}, s0);
+        else if (left > 4) block(std::integral_constant<int, 8>{}, s0);
+        else block(std::integral_constant<int, 4>{}, s0);
     }
     if (valid) {
         float* cs = b.s1 + seq * p.seq_s + soff;
