@@ -403,6 +403,12 @@ def main():
                                 env={"HELIX_PASSA_SPLIT": "3"}))
         variants.append(Variant("bf16-copies", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_WALK_BCCOPY": "1"}))
+        # The fp32 path at d_state 64 (config 2's shape otherwise): the walk
+        # (default) against the chunk-parallel Pass C on stored states.
+        t64 = make_inputs(1010, dev, dict(CFG, N=64))
+        variants.append(Variant("fp32-dstate64-walk", ctx, HELIX_BACKEND_SGMMA, t64))
+        variants.append(Variant("fp32-dstate64-chunk", ctx, HELIX_BACKEND_SGMMA, t64,
+                                env={"HELIX_F32_WALK": "0"}))
 
     def warm_up(v, ms):
         """W steps, then more until the wall clock has run `ms` (the
