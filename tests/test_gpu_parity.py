@@ -186,3 +186,57 @@ def test_baseline_config(gpu, name, path, memory):
     # The carried state never passes through bf16 on any default path: the
     # fp32 per-element bound (the wider one only for the opt-in bf16x3 Pass A).
     assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
+
+
+# ---------------------------------------------------------------------------
+# The fp32 path at d_state 64 and full length: the walk over 16-chunk
+# segments with Pass B launched (the default there), the chunk-parallel Pass C
+# (HELIX_F32_WALK=0), and the bf16 path; every head against the oracle.
+# ---------------------------------------------------------------------------
+
+D64_SHAPE = (8192, 1, 64, 64, 64, 8)
+D64_CASES = [
+    ("fp32/walk", HELIX_BACKEND_SGMMA, {}),
+    ("fp32/chunk", HELIX_BACKEND_SGMMA, {"HELIX_F32_WALK": "0"}),
+    ("bf16", HELIX_BACKEND_MPP, {}),
+]
+
+
+@functools.lru_cache(maxsize=None)
+def _d64(memory):
+    if memory == "long":
+        p = po.problem_harness(*D64_SHAPE, 1010, "long")
+        p.ids = None
+    else:
+        p = po.problem_gauss(*D64_SHAPE, 1010, 0.0, -1.0, 0.5)
+    y, s1 = po.scan(p, threads=0)
+    return p, y, s1
+
+
+@pytest.mark.parametrize("memory", ["dist", "long"])
+@pytest.mark.parametrize("label,backend,extra", D64_CASES, ids=[c[0] for c in D64_CASES])
+def test_dstate64_full_length(gpu, label, backend, extra, memory):
+    p, y_ref, s_ref = _d64(memory)
+    d = p.d.copy()
+    d.multipass = True
+    d.backend = backend
+    ctx = ctx_for(gpu, **extra)
+    assert ctx.supported(d)
+    info = ctx.plan_info(d)
+    if label == "fp32/walk":
+        assert info.kernel_c == b"helix_scan_walk_x6_n64" and info.walk_len > 1
+        assert info.kernel_b == b"helix_state_scan_f32"
+    elif label == "fp32/chunk":
+        assert info.kernel_c == b"helix_chunk_out_x6_n64"
+    s_rel, s_abs = s1_tolerance(ctx, d)
+    print(f"[d_state 64 {label} {memory}] {ctx.backend_desc(d)}", flush=True)
+    _, y, s1 = run(ctx, p, desc=d)
+    is_bf16 = backend == HELIX_BACKEND_MPP
+    gate = BF16_GATE if is_bf16 else F32_GATE
+    ey, es = po.max_rel_err(y, y_ref), po.max_rel_err(s1, s_ref)
+    print(f"  max|dy|/max|y| = {ey:.3e}   max|ds1|/max|s1| = {es:.3e}   gate {gate:g}", flush=True)
+    assert np.all(np.isfinite(y)) and np.all(np.isfinite(s1))
+    assert ey <= gate and es <= gate
+    rel, ab = (BF16_REL, BF16_ABS) if is_bf16 else (F32_REL, F32_ABS)
+    assert po.allclose_ratio(y, y_ref, rel, ab) <= 1.0
+    assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
