@@ -27,6 +27,8 @@ ABI_SYMBOLS = (
     "helix_scan_encode_into",
 )
 HOST_SYMBOLS = ("helix_ctx_create_host", "helix_scan_plan_info", "helix_scan_encode_noalloc")
+# include/helix/helix_host.h HELIX_PASS_B_*: where Pass B's segment scan runs
+PASS_B_LAUNCHED, PASS_B_IN_C = 0, 1
 # include/helix/helix_host.h HELIX_NOALLOC_SCRATCH_BYTES
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
@@ -54,6 +56,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("rec_bytes", c_uint64),
         ("walk_len", c_int32),
         ("walks_per_group", c_int32),
+        ("pass_b", c_int32),
     ]
 
 

@@ -386,7 +386,8 @@ void layout(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulT
 
 }  // namespace
 
-MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr) {
+MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr,
+                             size_t budget_cap) {
     const helix_tuning& tu = tuning_of(ctx);
     const bool bf16_state = tr.bf16_state;
     MultipassPlan pl;
@@ -398,7 +399,7 @@ MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, con
     // Default budget sized for MI355X's 288 GB: a 64-head 8K-token prefill
     // keeps all of its chunks in one group. HELIX_SCRATCH_MB=1 forces many
     // groups (reference caps.mm:170-176).
-    const size_t budget = (size_t)tu.scratch_mb << 20;
+    const size_t budget = std::min((size_t)tu.scratch_mb << 20, budget_cap);
     const size_t state = (size_t)d.n_seq * d.n_head * ((d.head_dim + HELIX_HD - 1) / HELIX_HD) * 64 *
                          (size_t)tr.np;
     // A walking Pass C keeps no per-chunk state; only segment aggregates

@@ -105,9 +105,6 @@ extern "C" helix_status helix_ctx_create(helix_ctx** out, void* device, const ch
             ctx->kernels[names[i]] = f;
         }
     }
-    // The fixed scratch of helix_scan_encode_noalloc, resolved once per
-    // device while it is current; a failure only disables that entry point.
-    if (st == HELIX_OK) helix::rt::noalloc_setup(dev);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
 
     if (st != HELIX_OK) {

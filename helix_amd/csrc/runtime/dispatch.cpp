@@ -43,10 +43,13 @@ inline void* dptr(helix_tensor t) {
 // scratch_sized: the scratch is the library's own fixed array, already known
 // to hold the plan (helix_scan_encode_noalloc), so its allocation is not
 // queried.
+// budget_cap: the plan's scratch budget is at most this many bytes (the fixed
+// array of helix_scan_encode_noalloc).
 helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
                          helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
                          helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
-                         helix_tensor s1, helix_tensor scratch, bool scratch_sized = false) {
+                         helix_tensor s1, helix_tensor scratch, bool scratch_sized = false,
+                         size_t budget_cap = SIZE_MAX) {
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
@@ -130,7 +133,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_OK;
     }
 
-    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(ctx, *d, tr);
+    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(ctx, *d, tr, budget_cap);
     if (plan.n_chunks <= 0) {
         set_error(ctx, "empty problem");
         return HELIX_ERR_INVALID_ARG;
@@ -322,6 +325,18 @@ extern "C" helix_status helix_scan_encode_into(helix_ctx* ctx, void* encoder, co
                        scratch);
 }
 
+namespace {
+
+// Scratch of the plan helix_scan_encode_noalloc runs (0 for the single pass).
+size_t noalloc_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
+    if (!d->multipass) return 0;
+    const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    if (tr.k_single) return 0;
+    return helix::rt::plan_multipass(ctx, *d, tr, HELIX_NOALLOC_SCRATCH_BYTES).total_bytes;
+}
+
+}  // namespace
+
 extern "C" helix_status helix_scan_encode_noalloc(helix_ctx* ctx, void* stream, const helix_scan_desc* d,
                                                   helix_tensor s0, helix_tensor x, helix_tensor dt,
                                                   helix_tensor A, helix_tensor B, helix_tensor C,
@@ -331,9 +346,13 @@ extern "C" helix_status helix_scan_encode_noalloc(helix_ctx* ctx, void* stream, 
         set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
         return HELIX_ERR_UNSUPPORTED_SHAPE;
     }
-    const size_t need = helix_scan_scratch_size(ctx, d);
+    // Planned for the fixed array: a plan that would exceed it is cut into
+    // more super-chunk groups (carried through s1), as with a lower
+    // HELIX_SCRATCH_MB; only a plan that does not fit even at one chunk per
+    // group is refused.
+    const size_t need = noalloc_scratch_size(ctx, d);
     if (need > HELIX_NOALLOC_SCRATCH_BYTES) {
-        set_error(ctx, "plan needs " + std::to_string(need) + " bytes of scratch, more than the " +
+        set_error(ctx, "plan needs " + std::to_string(need) + " bytes of scratch at one chunk per group, more than the " +
                            std::to_string((size_t)HELIX_NOALLOC_SCRATCH_BYTES) +
                            " of the fixed scratch (HELIX_NOALLOC_SCRATCH_BYTES); use helix_scan_encode");
         return HELIX_ERR_SCRATCH_TOO_SMALL;
@@ -352,7 +371,7 @@ extern "C" helix_status helix_scan_encode_noalloc(helix_ctx* ctx, void* stream, 
         }
     }
     return encode_core(ctx, static_cast<hipStream_t>(stream), d, s0, x, dt, A, B, C, ids, y, s1, scratch,
-                       /*scratch_sized=*/true);
+                       /*scratch_sized=*/true, HELIX_NOALLOC_SCRATCH_BYTES);
 }
 
 extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
@@ -398,5 +417,6 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->kernel_a = tr.k_chunk_state;
     out->kernel_b = fuse_b ? nullptr : tr.k_state_scan;
     out->kernel_c = tr.k_chunk_out;
+    out->pass_b = fuse_b ? HELIX_PASS_B_IN_C : HELIX_PASS_B_LAUNCHED;
     return HELIX_OK;
 }

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 #include <string>
 #include <unordered_map>
 
@@ -125,13 +126,17 @@ struct MultipassPlan {
     size_t total_bytes      = 0;
 };
 
-MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr);
+// budget_cap (bytes) lowers the context's scratch budget for this plan
+// (helix_scan_encode_noalloc plans for its fixed array).
+MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr,
+                             size_t budget_cap = SIZE_MAX);
 
 // Whether the walking Pass C runs Pass B's segment scan itself (no Pass B
 // launch): a single-group plan of at most four segments on a kernel that can;
 // the tuning's fuse_b (HELIX_FUSE_B=0 / 1) turns it off / on for any
 // single-group plan.
 bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const MultipassPlan& plan);
+
 
 // Fills the kernel-side params from the public descriptor. Returns false and
 // sets *why when a launch dimension would exceed the hardware grid limits.
@@ -140,10 +145,9 @@ bool build_params(const helix_scan_desc& d, HelixScanParams* out, std::string* w
 // Thread-local last-error bookkeeping.
 void set_error(const helix_ctx* ctx, const std::string& msg);
 
-// The fixed scratch of helix_scan_encode_noalloc (noalloc.hip): resolve its
-// device address once per device, with that device current (called by
-// helix_ctx_create), and look it up (null, with *why set, if unavailable).
-void noalloc_setup(int device);
+// The fixed scratch of helix_scan_encode_noalloc (noalloc.hip): its device
+// address on `device`, resolved on the entry point's first call there (with
+// that device current) and kept; null, with *why set, if unavailable.
 void* noalloc_scratch(int device, std::string* why);
 
 }  // namespace helix::rt

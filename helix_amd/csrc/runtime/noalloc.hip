@@ -8,7 +8,8 @@
 //
 // In host code `helix_noalloc_scratch` names a host-side stand-in, not device
 // memory: only the address hipGetSymbolAddress returns for it, resolved once
-// per device with that device current, is ever passed to a kernel.
+// per device (on the entry point's first call there, with that device
+// current), is ever passed to a kernel.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -31,27 +32,33 @@ std::string g_err[kMaxDevices];    // why the address could not be resolved
 
 namespace helix::rt {
 
-void noalloc_setup(int device) {
-    if (device < 0 || device >= kMaxDevices) return;
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (g_ptr[device]) return;
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(helix_noalloc_scratch));
-    if (e != hipSuccess || !p) {
-        (void)hipGetLastError();
-        g_err[device] = std::string("hipGetSymbolAddress of the fixed scratch failed: ") + hipGetErrorString(e);
-        return;
-    }
-    g_ptr[device] = p;
-}
-
 void* noalloc_scratch(int device, std::string* why) {
     if (device < 0 || device >= kMaxDevices) {
         *why = "device ordinal beyond the fixed scratch table";
         return nullptr;
     }
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!g_ptr[device]) *why = g_err[device].empty() ? "fixed scratch not set up on this device" : g_err[device];
+    if (!g_ptr[device] && g_err[device].empty()) {
+        // First call on this device: resolve the array's address there, with
+        // the device current.
+        int prev = -1;
+        (void)hipGetDevice(&prev);
+        if (prev != device && hipSetDevice(device) != hipSuccess) {
+            (void)hipGetLastError();
+            *why = "hipSetDevice failed";
+            return nullptr;
+        }
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(helix_noalloc_scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            g_err[device] = std::string("hipGetSymbolAddress of the fixed scratch failed: ") + hipGetErrorString(e);
+        } else {
+            g_ptr[device] = p;
+        }
+        if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    }
+    if (!g_ptr[device]) *why = g_err[device];
     return g_ptr[device];
 }
 

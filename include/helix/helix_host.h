@@ -46,7 +46,13 @@ typedef struct {
     int32_t  walk_len;          /* chunks per walking Pass C workgroup (a
                                    multiple of seg_len; seg_len off the walk)    */
     int32_t  walks_per_group;
+    int32_t  pass_b;            /* where Pass B's segment scan runs: one of
+                                   HELIX_PASS_B_* (kernel_b is NULL unless it
+                                   has a launch of its own)                      */
 } helix_plan_info;
+
+#define HELIX_PASS_B_LAUNCHED 0   /* kernel_b, between Pass A and Pass C         */
+#define HELIX_PASS_B_IN_C     1   /* the walking Pass C's prologue               */
 
 /* Returns HELIX_ERR_UNSUPPORTED_SHAPE when the descriptor is declined. */
 helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
@@ -59,15 +65,17 @@ helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_desc* d,
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc. It has no counterpart in the reference ABI.
  *
- * Same descriptor, tensors, plan, kernels and results as helix_scan_encode;
- * the scratch is a fixed device array of HELIX_NOALLOC_SCRATCH_BYTES that the
- * library holds on every GPU it runs on until the process ends (its address
- * is resolved when a context is created on that GPU). The call allocates and
- * frees nothing. A plan needing more scratch than that
- * (helix_scan_scratch_size(ctx, d) > HELIX_NOALLOC_SCRATCH_BYTES) returns
- * HELIX_ERR_SCRATCH_TOO_SMALL before anything is enqueued; the single pass
- * needs none. No part of the array needs to start at zero: every region a
- * kernel reads is written earlier in the same encode.
+ * Same descriptor, tensors, kernels and results as helix_scan_encode; the
+ * scratch is a fixed device array of HELIX_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU where this entry point has been called, until
+ * the process ends (its address is resolved on the first call on that GPU).
+ * The call allocates and frees nothing. Its plan is made for that array: a
+ * scan whose plan under the context's budget needs more scratch is cut into
+ * more super-chunk groups (carried through s1, as with a lower
+ * HELIX_SCRATCH_MB), and only a scan that does not fit at one chunk per group
+ * returns HELIX_ERR_SCRATCH_TOO_SMALL, before anything is enqueued; the
+ * single pass needs none. No part of the array needs to start at zero: every
+ * region a kernel reads is written earlier in the same encode.
  *
  * Every call on one GPU shares that GPU's array and it keeps the last call's
  * contents: calls whose work overlaps on one GPU (other streams, other

@@ -19,6 +19,7 @@ on the caller's B and C instead of Pass A's bf16 copies; single pass).
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import os
 
 import numpy as np
@@ -326,3 +327,61 @@ def test_side_stream(gpu):
     with torch.cuda.stream(side):
         _, y, s1 = run(gpu, p, desc=_desc(p, HELIX_BACKEND_MPP, True), stream=side)
     assert _rel(y, y_ref) <= BF16_GATE and _rel(s1, s_ref) <= F32_GATE
+
+
+def test_graph_replays(gpu):
+    """helix_scan_encode_noalloc captured into a HIP graph (the callers it is
+    for) and replayed: each replay, with new inputs and eager scans between
+    the replays, matches an eager encode of the same inputs bit for bit (the
+    scan records no memset and keeps nothing between launches but its
+    scratch, which every launch rewrites before reading)."""
+    p = po.problem_harness(2048, 1, 16, 64, 128, 2, 21, "long")
+    d = _desc(p, HELIX_BACKEND_MPP, True)
+    dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+    x0 = dev["x"].clone()
+    y, s1 = torch.empty(p.y_shape(), device="cuda"), torch.empty(p.s_shape(), device="cuda")
+    y_e, s1_e = torch.empty_like(y), torch.empty_like(s1)
+    scratch = torch.empty(gpu.scratch_size(d), dtype=torch.uint8, device="cuda")
+    args = [T(dev[k]) for k in ("s0", "x", "dt", "A", "B", "C")]
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        rc = gpu.encode_noalloc(torch.cuda.current_stream().cuda_stream, d, *args, HELIX_TENSOR_NULL,
+                                T(y), T(s1))
+    assert rc == HELIX_OK, gpu.last_error()
+    stream = torch.cuda.current_stream().cuda_stream
+    for r in range(4):
+        dev["x"].copy_(x0 * (1.0 + 0.25 * r))
+        y.fill_(float("nan"))
+        s1.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert gpu.encode(stream, d, *args, HELIX_TENSOR_NULL, T(y_e), T(s1_e), T(scratch)) == HELIX_OK
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_e) and torch.equal(s1, s1_e), f"replay {r}"
+    # The last replay's inputs, against the oracle.
+    y_ref, s_ref = po.scan(dataclasses.replace(p, x=np.ascontiguousarray(x0.cpu().numpy() * 1.75)))
+    assert _rel(y.cpu().numpy(), y_ref) <= BF16_GATE and _rel(s1.cpu().numpy(), s_ref) <= F32_GATE
+
+
+def test_concurrent_streams(gpu):
+    """Two encodes in flight at once on two streams of one context (each
+    with its own outputs and scratch) match the oracle."""
+    probs = [po.problem_harness(2048, 1, 16, 64, 128, 2, 31 + i, "long") for i in range(2)]
+    refs = [po.scan(p) for p in probs]
+    streams = [torch.cuda.Stream() for _ in probs]
+    bufs = []
+    for p in probs:
+        d = _desc(p, HELIX_BACKEND_MPP, True)
+        dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+        bufs.append((d, dev, torch.empty(p.y_shape(), device="cuda"), torch.empty(p.s_shape(), device="cuda"),
+                     torch.empty(gpu.scratch_size(d), dtype=torch.uint8, device="cuda")))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for (d, dev, y, s1, scr), st in zip(bufs, streams):
+            rc = gpu.encode(st.cuda_stream, d, *[T(dev[k]) for k in ("s0", "x", "dt", "A", "B", "C")],
+                            HELIX_TENSOR_NULL, T(y), T(s1), T(scr))
+            assert rc == HELIX_OK
+    torch.cuda.synchronize()
+    for (d, dev, y, s1, scr), (y_ref, s_ref) in zip(bufs, refs):
+        assert _rel(y.cpu().numpy(), y_ref) <= BF16_GATE and _rel(s1.cpu().numpy(), s_ref) <= F32_GATE

@@ -190,7 +190,7 @@ def test_baseline_config(gpu, name, path, memory):
 
 # ---------------------------------------------------------------------------
 # The fp32 path at d_state 64 and full length: the walk over 16-chunk
-# segments with Pass B launched (the default there), the chunk-parallel Pass C
+# segments (the default there), the chunk-parallel Pass C
 # (HELIX_F32_WALK=0), and the bf16 path; every head against the oracle.
 # ---------------------------------------------------------------------------
 
@@ -225,7 +225,6 @@ def test_dstate64_full_length(gpu, label, backend, extra, memory):
     info = ctx.plan_info(d)
     if label == "fp32/walk":
         assert info.kernel_c == b"helix_scan_walk_x6_n64" and info.walk_len > 1
-        assert info.kernel_b == b"helix_state_scan_f32"
     elif label == "fp32/chunk":
         assert info.kernel_c == b"helix_chunk_out_x6_n64"
     s_rel, s_abs = s1_tolerance(ctx, d)
@@ -240,3 +239,46 @@ def test_dstate64_full_length(gpu, label, backend, extra, memory):
     rel, ab = (BF16_REL, BF16_ABS) if is_bf16 else (F32_REL, F32_ABS)
     assert po.allclose_ratio(y, y_ref, rel, ab) <= 1.0
     assert po.allclose_ratio(s1, s_ref, s_rel, s_abs) <= 1.0
+
+
+# ---------------------------------------------------------------------------
+# Where Pass B's segment scan runs, at full size: its own launch at config 2
+# (the default), also over many super-chunk groups whose walks span two Pass A
+# segments (HELIX_SCRATCH_MB=20: fifteen groups, one-chunk segments,
+# two-chunk walks, carried through s1); and the walk's prologue at config 4a
+# (the default) against its own launch there. Every head against the oracle,
+# s1 at the fp32 per-element bound.
+# ---------------------------------------------------------------------------
+
+PASS_B_CASES = [
+    ("cfg2", "bf16", {"HELIX_SCRATCH_MB": "20"}, "launched", True),
+    ("cfg2", "fp32", {"HELIX_SCRATCH_MB": "20"}, "launched", True),
+    ("cfg4a", "bf16", {"HELIX_FUSE_B": "0"}, "launched", False),
+    ("cfg4a", "bf16", {}, "in_c", False),
+]
+
+
+@pytest.mark.parametrize("name,path,extra,where,multi", PASS_B_CASES,
+                         ids=[f"{c[0]}-{c[1]}-" + ("-".join(f"{k[6:]}={v}" for k, v in c[2].items()) or "default")
+                              for c in PASS_B_CASES])
+def test_pass_b_placement(gpu, name, path, extra, where, multi):
+    from helix_amd.abi import PASS_B_IN_C, PASS_B_LAUNCHED
+    p, y_ref, s_ref = _baseline(name, "dist")
+    d = p.d.copy()
+    d.multipass = True
+    d.backend = HELIX_BACKEND_MPP if path == "bf16" else HELIX_BACKEND_SGMMA
+    ctx = ctx_for(gpu, **extra)
+    info = ctx.plan_info(d)
+    assert info.pass_b == {"in_c": PASS_B_IN_C, "launched": PASS_B_LAUNCHED}[where]
+    if multi:
+        assert info.n_groups > 1 and info.walk_len > info.seg_len
+    print(f"[{name} {path} {extra}] groups {info.n_groups} seg {info.seg_len} walk {info.walk_len} "
+          f"pass_b {info.pass_b}", flush=True)
+    _, y, s1 = run(ctx, p, desc=d)
+    is_bf16 = path == "bf16"
+    ey, es = po.max_rel_err(y, y_ref), po.max_rel_err(s1, s_ref)
+    print(f"  max|dy|/max|y| = {ey:.3e}   max|ds1|/max|s1| = {es:.3e}", flush=True)
+    assert ey <= (BF16_GATE if is_bf16 else F32_GATE) and es <= F32_GATE
+    rel, ab = (BF16_REL, BF16_ABS) if is_bf16 else (F32_REL, F32_ABS)
+    assert po.allclose_ratio(y, y_ref, rel, ab) <= 1.0
+    assert po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0

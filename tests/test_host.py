@@ -202,6 +202,7 @@ def test_16bit_storage_selection(host, io, name):
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
         f"helix_chunk_state_hb_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
+    assert k.pass_b == abi.PASS_B_LAUNCHED
     x3 = tuned(HELIX_PASSA_SPLIT="3")       # Pass A on three split products: opt-in
     assert x3.plan_info(d).kernel_a == f"helix_chunk_state_hb_x3agg_{name}io_n128".encode()
     assert x3.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in), "
@@ -231,14 +232,23 @@ def test_null_context_and_desc():
 
 
 def test_noalloc_host_checks(host):
-    # helix_scan_encode_noalloc refuses, before anything is enqueued, a plan
-    # whose scratch exceeds its fixed array (config 2 at d_state 256 on the
-    # fp32 path, whose Pass A stores every chunk's state: 520 MiB), and a
+    # helix_scan_encode_noalloc plans for its fixed array: a scan whose plan
+    # needs more under the context's budget (config 4a on the bf16 path, 136
+    # MiB; config 2 at d_state 256 on the fp32 path, whose Pass A stores every
+    # chunk's state, 520 MiB) is cut into more groups; only one that does not
+    # fit at one chunk per group is refused, before anything is enqueued. A
     # host-only context has no device for one that fits.
     t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
-    big = mp((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)
-    assert host.scratch_size(big) > abi.NOALLOC_SCRATCH_BYTES
-    assert host.encode_noalloc(0, big, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
+    for shape, backend in ((CONFIG_SHAPES["cfg4a"], HELIX_BACKEND_MPP),
+                           ((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)):
+        d = mp(shape, backend)
+        assert host.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
+        with env(HELIX_SCRATCH_MB=str(abi.NOALLOC_SCRATCH_BYTES >> 20)):
+            capped = abi.Context(host_only=True).plan_info(d)
+        assert capped.n_groups > 1 and capped.total_bytes <= abi.NOALLOC_SCRATCH_BYTES
+        assert host.encode_noalloc(0, d, *t) == HELIX_ERR_NO_DEVICE
+    huge = mp((64, 1, 4096, 64, 256, 1), HELIX_BACKEND_SGMMA)   # one chunk's state is 256 MiB
+    assert host.encode_noalloc(0, huge, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
     assert "HELIX_NOALLOC_SCRATCH_BYTES" in host.last_error()
     fits = mp(CONFIG_SHAPES["cfg2"])
     assert 0 < host.scratch_size(fits) <= abi.NOALLOC_SCRATCH_BYTES
@@ -285,6 +295,7 @@ def test_backend_selection(host):
     kw = host.plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (kw.kernel_a, kw.kernel_b, kw.kernel_c) == (
         b"helix_chunk_state_hb_x6agg_r64_n128", b"helix_state_scan_f32", b"helix_scan_walk_x6_n128")
+    assert kw.pass_b == abi.PASS_B_LAUNCHED and kw.launches == 3
     assert kw.s_local_bytes == 0 and kw.bf16_state == 0 and (kw.seg_len, kw.walk_len) == (8, 16)
     f0 = tuned(HELIX_F32_WALK="0")
     assert (f0.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
@@ -329,7 +340,7 @@ def test_backend_selection(host):
     # HELIX_SEG_LEN=16 runs it there).
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
         b"helix_chunk_state_hb_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
-    assert k.bccopy_bytes == 0
+    assert k.bccopy_bytes == 0 and k.pass_b == abi.PASS_B_LAUNCHED
     # Pass A (head blocks of four heads) runs 8-chunk segments, 16 per
     # sequence; the walk runs 16-chunk ones, each starting at every other
     # Pass A segment.
@@ -338,11 +349,12 @@ def test_backend_selection(host):
     assert tuned(HELIX_FUSE_B="1").plan_info(mp(shape)).kernel_b == b"helix_state_scan_f32"
     kf = tuned(HELIX_FUSE_B="1", HELIX_SEG_LEN="16").plan_info(mp(shape))
     assert kf.kernel_b is None and kf.launches == 2 and kf.seg_len == kf.walk_len == 16
+    assert kf.pass_b == abi.PASS_B_IN_C
     # Config 4a: one group of four segments per sequence, fused by default.
     k4 = host.plan_info(mp(CONFIG_SHAPES["cfg4a"]))
-    assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2
+    assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2 and k4.pass_b == abi.PASS_B_IN_C
     km = tuned(HELIX_SCRATCH_MB="1").plan_info(mp(shape))   # many groups, carried through s1
-    assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32"
+    assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32" and km.pass_b == abi.PASS_B_LAUNCHED
     assert km.launches == 3 * km.n_groups
     L, S, H, P, N, G = shape
     # HELIX_WALK_BCCOPY=1: Pass A writes bf16 copies of B and C that the walk reads.
@@ -455,6 +467,7 @@ def test_plan_invariants(host, name, backend):
     fused = walk and info.n_groups == 1 and info.segs_per_group <= 4 and info.seg_len == info.walk_len
     assert info.launches == (2 if fused else 3 * info.n_groups)
     assert (info.kernel_b is None) == fused
+    assert info.pass_b == (abi.PASS_B_IN_C if fused else abi.PASS_B_LAUNCHED)
 
 
 def test_plan_single_group_for_baseline_configs(host):

@@ -5,7 +5,10 @@ fixed scratch array instead of a caller's buffer, so its outputs must be
 bitwise equal to helix_scan_encode's on the same inputs (the scan is
 deterministic), and within the oracle's tolerance. Two calls in a row, the
 second on a smaller problem, so the second runs on what the first left in the
-array. A plan larger than the array is refused and writes nothing.
+array. A scan whose plan would need more than the array is planned for it
+(more super-chunk groups): bitwise equal to helix_scan_encode under the same
+budget. One that does not fit at one chunk per group is refused and writes
+nothing.
 """
 from __future__ import annotations
 
@@ -17,7 +20,7 @@ from oracle import pyoracle as po
 from helix_amd import abi
 from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA,
                             HELIX_ERR_SCRATCH_TOO_SMALL, HELIX_OK, HELIX_TENSOR_NULL)
-from gpu_harness import BF16_GATE, F32_GATE, T, upload
+from gpu_harness import BF16_GATE, F32_GATE, T, ctx_for, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -63,8 +66,9 @@ def test_noalloc_matches_encode(gpu, path):
 
 
 def test_noalloc_refuses_oversized_plan(gpu):
-    # d_state 256 on the fp32 path: Pass A stores every chunk's state.
-    p = po.problem_harness(8192, 1, 64, 64, 256, 8, 5, "short")
+    # d_state 256 on the fp32 path, 4096 heads: Pass A stores every chunk's
+    # state, 256 MiB for one chunk, so not even one chunk per group fits.
+    p = po.problem_harness(64, 1, 4096, 64, 256, 1, 5, "short")
     d = p.d.copy()
     d.backend = HELIX_BACKEND_SGMMA
     d.multipass = True
@@ -90,3 +94,22 @@ def test_noalloc_headline_shape(gpu):
     y_a, s_a = _encode(gpu, p, d, noalloc=False)
     y_b, s_b = _encode(gpu, p, d, noalloc=True)
     assert np.array_equal(y_a, y_b) and np.array_equal(s_a, s_b)
+
+
+def test_noalloc_capped_plan(gpu):
+    # BASELINE config 4a on the bf16 path: 136 MiB of scratch under the
+    # default budget, so the entry point plans it for its 128 MiB array in
+    # several groups carried through s1, as helix_scan_encode does with
+    # HELIX_SCRATCH_MB=128 (bitwise), and close to the default plan's result.
+    p = po.problem_gauss(4096, 8, 80, 64, 128, 1, 1004, 0.1)
+    d = p.d.copy()
+    d.backend = HELIX_BACKEND_MPP
+    d.multipass = True
+    assert gpu.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
+    capped = ctx_for(gpu, HELIX_SCRATCH_MB=abi.NOALLOC_SCRATCH_BYTES >> 20)
+    assert capped.plan_info(d).n_groups > 1
+    y_n, s_n = _encode(gpu, p, d, noalloc=True)
+    y_c, s_c = _encode(capped, p, d, noalloc=False)
+    assert y_n.tobytes() == y_c.tobytes() and s_n.tobytes() == s_c.tobytes()
+    y_d, s_d = _encode(gpu, p, d, noalloc=False)
+    assert po.max_rel_err(y_n, y_d) <= BF16_GATE and po.max_rel_err(s_n, s_d) <= F32_GATE
