@@ -622,22 +622,23 @@ HELIX_DEV int sload_i32(const int* p, long long i) {
 HELIX_DEV int wave_uniform() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // The decay record of token t = lane of chunk c (group-local) of head h, as
-// the walking Pass C uses it: {dt_t, exp(L_end - Lcum_t), Lcum_t log2(e),
-// exp(Lcum_t)}, with dt and the decay zero past tlen. Pass A forms dt_t,
-// Lcum_t and L_end for its own GEMM; storing these four values once per
-// (seq, chunk, head) spares the walk's four waves per head recomputing the
-// softplus and the fp64 scan every chunk. exp(L_end) is the record of token
-// 63 (Lcum_63 = L_end).
+// the walking Pass C uses it: {dt_t, Lcum_t log2(e)} (HELIX_REC_WALK_BYTES),
+// with dt zero past tlen (padded tokens carry Lcum_{tlen-1}). Pass A forms
+// dt_t and Lcum_t (fp64) for its own GEMM; storing them once per (seq, chunk,
+// head) spares the walk's four waves per head recomputing the softplus and the
+// fp64 scan every chunk. The walk forms exp(L_end - Lcum_t), exp(Lcum_t) and
+// exp(L_end) from the fp32 log2 values with v_exp_f32 (Lcum_63 = L_end): a
+// few ulps of a value that then rounds to a bf16 operand, for half the bytes
+// of storing the exponentials too.
+HELIX_DEV u32x2 walk_record(float dtv, double lcum) {
+    return u32x2{__builtin_bit_cast(unsigned, dtv), __builtin_bit_cast(unsigned, (float)(lcum * 1.4426950408889634074))};
+}
 HELIX_DEV void store_decay_record(const HelixScanParams& p, const HelixScanBuffers& b, int seq, int c, int h,
-                                  int lane, int tlen, float dtv, double lcum, double lend) {
-    const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
-    const float l2 = (float)(lcum * 1.4426950408889634074);
-    const float e = expf((float)lcum);
-    const float* rec = b.pre + (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 4);
-    const helix_rsrc r = make_rsrc(rec, HELIX_CS * 16u);
-    const u32x4 w = {__builtin_bit_cast(unsigned, dtv), __builtin_bit_cast(unsigned, sdec),
-                     __builtin_bit_cast(unsigned, l2), __builtin_bit_cast(unsigned, e)};
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, lane * 16, 0, 0);
+                                  int lane, float dtv, double lcum) {
+    const char* rec = reinterpret_cast<const char*>(b.pre) +
+                      (((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * HELIX_REC_WALK_BYTES);
+    const helix_rsrc r = make_rsrc(rec, HELIX_CS * HELIX_REC_WALK_BYTES);
+    __builtin_amdgcn_raw_buffer_store_b64(walk_record(dtv, lcum), r, lane * HELIX_REC_WALK_BYTES, 0, 0);
 }
 
 // The fp32 path's form of the record (its Pass C forms the intra-chunk decays

@@ -61,6 +61,11 @@
 #define HELIX_N_MAX 256
 /* Threads per workgroup: four wave64s, one per SIMD of a CU. */
 #define HELIX_WG 256
+/* Bytes of one token's decay record (HelixScanBuffers::pre): the walking bf16
+ * Pass C's {dt, Lcum log2(e)}, and the fp32 path's {dt, exp(Lcum), Lcum as
+ * fp64}. */
+#define HELIX_REC_WALK_BYTES 8
+#define HELIX_REC64_BYTES 16
 /* Heads per workgroup of the chunk-walking Pass C (four waves per head):
  * two up to d_state 128; one at 256, where a head's state needs the whole
  * register budget of a wave. */
@@ -144,11 +149,11 @@ typedef struct HelixScanBuffers {
     float*       segld;
     void*        bcopy;   /* bf16 copies of B and C (see the layout above), or null */
     void*        ccopy;
-    float*       pre;     /* per-token decay records [seq][chunk][head][64][4] that
+    float*       pre;     /* per-token decay records [seq][chunk][head][64] that
                              Pass A writes for the Pass C that reads them, or
-                             null: {dt, exp(L_end - Lcum), Lcum log2(e), exp(Lcum)}
-                             for the 16 x 16 walk, {dt, exp(Lcum), Lcum (fp64)}
-                             for the fp32 path's bf16x6 Pass C */
+                             null: {dt, Lcum log2(e)} (HELIX_REC_WALK_BYTES) for
+                             the 16 x 16 walk, {dt, exp(Lcum), Lcum (fp64)}
+                             (HELIX_REC64_BYTES) for the fp32 path's bf16x6 Pass C */
 } HelixScanBuffers;
 
 #endif /* HELIX_PARAMS_H */

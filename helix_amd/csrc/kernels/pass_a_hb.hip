@@ -242,10 +242,8 @@ __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtr
     r.w = keep_if_lt(exp_diff(lend + shift, lcum) * dtv, lane, tlen);
     r.lend = lend;
     if constexpr (MODE == 2 && !R64) {
-        const float sdec = keep_if_lt(exp2_diff(lend, lcum), lane, tlen);
-        const float l2 = (float)(lcum * 1.4426950408889634074);
-        const float e = expf((float)lcum);
-        r.rec = u32x4{as_u32(dtv), as_u32(sdec), as_u32(l2), as_u32(e)};
+        const u32x2 w = walk_record(dtv, lcum);
+        r.rec = u32x4{w[0], w[1], 0u, 0u};
     } else {
         const float e = expf((float)lcum);
         const unsigned long long u = __builtin_bit_cast(unsigned long long, lcum);
@@ -389,10 +387,14 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         // The record's address is formed unconditionally (a select of two
         // pointers becomes a branch); without records its range is zero.
         const bool rec = live && leader && b.pre != nullptr;
+        constexpr int RB = (MODE == 2 && !R64) ? HELIX_REC_WALK_BYTES : HELIX_REC64_BYTES;
         const unsigned long long recp =
-            (unsigned long long)b.pre + (unsigned long long)((((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * 16));
-        __builtin_amdgcn_raw_buffer_store_b128(pr.rec, make_rsrc_u((const void*)recp, rec ? HELIX_CS * 16u : 0u),
-                                               lane * 16, 0, 0);
+            (unsigned long long)b.pre + (unsigned long long)((((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * RB));
+        const helix_rsrc rr = make_rsrc_u((const void*)recp, rec ? HELIX_CS * RB : 0u);
+        if constexpr (RB == 8)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pr.rec[0], pr.rec[1]}, rr, lane * 8, 0, 0);
+        else
+            __builtin_amdgcn_raw_buffer_store_b128(pr.rec, rr, lane * 16, 0, 0);
         if constexpr (MODE == 0) {
             const float* ldp = b.ld + seq * p.ld_seq + (long long)c * p.n_head + h;
             __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && leader ? 4u : 0u),

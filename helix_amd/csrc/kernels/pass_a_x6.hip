@@ -238,7 +238,7 @@ __device__ __forceinline__ void chunk_state_x6_impl(const HelixScanParams& p, co
         float* dst = sPre[(c - c_begin) & 1];
         dst[lane] = keep_if_lt(exp_diff(lend, lcum) * dtv, lane, tlen);
         if (lane == 0) dst[HELIX_CS] = (float)lend;
-        if (MODE == 2 && b.pre && slab == 0) store_decay_record(p, b, seq, c, h, lane, tlen, dtv, lcum, lend);
+        if (MODE == 2 && b.pre && slab == 0) store_decay_record(p, b, seq, c, h, lane, dtv, lcum);
         if (MODE == 0 && b.pre && slab == 0) store_decay_record64(p, b, seq, c, h, lane, dtv, lcum);
     };
 

@@ -54,10 +54,11 @@ HELIX_DEV int g1_jb(int idx) {
 }
 
 // x of tokens 16 wave + i at channel p = lane and the decay record of token
-// lane (Pass A's store_decay_record), prefetched a chunk ahead in storage form.
+// lane (Pass A's store_decay_record: dt, Lcum log2(e)), prefetched a chunk
+// ahead in storage form.
 template <typename IO>
 struct StageW16 {
-    u32x4 rec;
+    u32x2 rec;
     typename IoWord<IO>::type x[16];
 };
 
@@ -69,10 +70,11 @@ __device__ __forceinline__ void load_stage_w16(StageW16<IO>& st, const HelixScan
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
-    const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
+    const helix_rsrc rr = make_rsrc(reinterpret_cast<const char*>(rec_h) + (long long)c * p.n_head * (HELIX_CS * HELIX_REC_WALK_BYTES),
+                                    HELIX_CS * HELIX_REC_WALK_BYTES);
     const helix_rsrc rx  = make_rsrc(x_h + (long long)t0 * p.s_x[0],
                                      ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * (unsigned)sizeof(IO));
-    st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    st.rec = __builtin_amdgcn_raw_buffer_load_b64(rr, lane * HELIX_REC_WALK_BYTES, 0, 0);
     const int xc = min(lane, pw - 1) * sx2;
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.x[i] = io_load_word<IO>(rx, xc, min(16 * wave + i, tlen - 1) * sx0);
@@ -221,7 +223,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
     if (c_begin >= c_end) return;
 
     // Decay records of this head, chunk stride n_head * 64 records.
-    const float* __restrict__ rec_h = b.pre + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * 4);
+    const float* __restrict__ rec_h = reinterpret_cast<const float*>(
+        reinterpret_cast<const char*>(b.pre) + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * HELIX_REC_WALK_BYTES));
     const IO* __restrict__ x_h = reinterpret_cast<const IO*>(b.x) + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
     const BIO* __restrict__ B_g = reinterpret_cast<const BIO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
     const BIO* __restrict__ C_g = reinterpret_cast<const BIO*>(b.C) + seq * p.seq_c + g * p.s_c[1];
@@ -323,11 +326,14 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         load_runs_w16<KQ, RPI, BIO>(runs, p, B_g, C_g, cn, N, jrow, ur);
 
         // ---- decay record, dtX^T and dtXs^T --------------------------------
-        // Pass A's record of token lane: dt (0 past tlen), exp(L_end - Lcum)
-        // (0 past tlen), Lcum log2(e), exp(Lcum); exp(L_end) is token 63's.
+        // Pass A's record of token lane: dt (0 past tlen) and Lcum log2(e);
+        // L_end is token 63's. exp(L_end - Lcum) weights G4's dtXs (its
+        // tokens past tlen have dt 0), exp(Lcum) G3's rows.
         const float dtv = as_f32(st.rec[0]);
-        const float sdec = as_f32(st.rec[1]);
-        const float a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[3], 63));
+        const float l2 = as_f32(st.rec[1]);
+        const float l2_end = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[1], 63));
+        const float sdec = __builtin_amdgcn_exp2f(l2_end - l2);
+        const float a_c = __builtin_amdgcn_exp2f(l2_end);
         {
             // dt and the decay of this wave's 16 tokens, through the wave's own
             // LDS row (one write, four broadcast reads each).
@@ -349,8 +355,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             store16_nat<RSJ>(sXst[hw], lane, 16 * w4, vs);
         }
         if (w4 == 0) {
-            sL2[hw][lane] = as_f32(st.rec[2]);
-            sE[hw][lane] = as_f32(st.rec[3]);
+            sL2[hw][lane] = l2;
+            sE[hw][lane] = __builtin_amdgcn_exp2f(l2);
         }
         load_stage_w16<IO>(st, p, rec_h, x_h, cn, lane, w4, pw);
         __syncthreads();

@@ -379,7 +379,8 @@ void layout(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulT
     pl->off_sd = off; off += align256(pl->sd_elems * sizeof(float));
     pl->off_bc = off; off += align256(pl->bc_elems * 2);
     pl->off_cc = off; off += align256(pl->bc_elems * 2);
-    pl->rec_elems = rec ? (size_t)d.n_seq * (size_t)cpg * d.n_head * HELIX_CS * 4 : 0;
+    const size_t rec_bytes = tr.rec_kind == 1 ? HELIX_REC_WALK_BYTES : HELIX_REC64_BYTES;
+    pl->rec_elems = rec ? (size_t)d.n_seq * (size_t)cpg * d.n_head * HELIX_CS * rec_bytes / sizeof(float) : 0;
     pl->off_rec = off; off += align256(pl->rec_elems * sizeof(float));
     pl->total_bytes = off;
 }
@@ -389,7 +390,6 @@ void layout(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulT
 MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& tr,
                              size_t budget_cap) {
     const helix_tuning& tu = tuning_of(ctx);
-    const bool bf16_state = tr.bf16_state;
     MultipassPlan pl;
     if (d.n_tok <= 0 || d.n_seq <= 0 || d.n_head <= 0 || d.head_dim <= 0 || d.d_state <= 0 ||
         d.n_group <= 0)
@@ -400,19 +400,22 @@ MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, con
     // keeps all of its chunks in one group. HELIX_SCRATCH_MB=1 forces many
     // groups (reference caps.mm:170-176).
     const size_t budget = std::min((size_t)tu.scratch_mb << 20, budget_cap);
-    const size_t state = (size_t)d.n_seq * d.n_head * ((d.head_dim + HELIX_HD - 1) / HELIX_HD) * 64 *
-                         (size_t)tr.np;
-    // A walking Pass C keeps no per-chunk state; only segment aggregates
-    // (about one state per seg_len chunks) count against the budget.
-    const size_t bc_chunk = tr.bccopy ? (size_t)d.n_seq * HELIX_CS * d.n_group * d.d_state * 2 * 2 : 0;
-    const size_t rec_chunk = tr.rec_kind ? (size_t)d.n_seq * d.n_head * HELIX_CS * 16 : 0;
-    const size_t per_chunk = (tr.walk ? state : state * (bf16_state ? 2 : 4)) + bc_chunk + rec_chunk;
-    long cpg = per_chunk ? (long)(budget / per_chunk) : 1;
-    cpg = std::max<long>(1, std::min<long>(cpg, pl.n_chunks));
-    for (;;) {
-        layout(tu, d, tr, (int)cpg, &pl);
-        if (pl.total_bytes <= budget || cpg == 1) break;
-        cpg = std::max<long>(1, cpg - std::max<long>(1, cpg / 8));
+    // The most chunks per group whose layout fits the budget: all of them
+    // when that fits (every BASELINE config under the default budget), else
+    // a binary search (the layout grows with the chunks per group; one chunk
+    // per group is the floor even past the budget).
+    long lo = 1, hi = pl.n_chunks;
+    auto fits = [&](long c) {
+        layout(tu, d, tr, (int)c, &pl);
+        return pl.total_bytes <= budget;
+    };
+    if (!fits(hi)) {
+        while (hi - lo > 1) {
+            const long mid = lo + (hi - lo) / 2;
+            if (fits(mid)) lo = mid;
+            else hi = mid;
+        }
+        layout(tu, d, tr, (int)lo, &pl);
     }
     pl.n_groups = (pl.n_chunks + pl.chunks_per_group - 1) / pl.chunks_per_group;
 

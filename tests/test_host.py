@@ -233,13 +233,15 @@ def test_null_context_and_desc():
 
 def test_noalloc_host_checks(host):
     # helix_scan_encode_noalloc plans for its fixed array: a scan whose plan
-    # needs more under the context's budget (config 4a on the bf16 path, 136
-    # MiB; config 2 at d_state 256 on the fp32 path, whose Pass A stores every
-    # chunk's state, 520 MiB) is cut into more groups; only one that does not
-    # fit at one chunk per group is refused, before anything is enqueued. A
-    # host-only context has no device for one that fits.
+    # needs more under the context's budget (config 4a with ten sequences on
+    # the bf16 path, 145 MiB; config 2 at d_state 256 on the fp32 path, whose
+    # Pass A stores every chunk's state, 520 MiB) is cut into more groups;
+    # only one that does not fit at one chunk per group is refused, before
+    # anything is enqueued. A host-only context has no device for one that
+    # fits. Config 4a itself fits (116 MiB).
     t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
-    for shape, backend in ((CONFIG_SHAPES["cfg4a"], HELIX_BACKEND_MPP),
+    assert 0 < host.scratch_size(mp(CONFIG_SHAPES["cfg4a"])) <= abi.NOALLOC_SCRATCH_BYTES
+    for shape, backend in (((4096, 10, 80, 64, 128, 1), HELIX_BACKEND_MPP),
                            ((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)):
         d = mp(shape, backend)
         assert host.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
@@ -362,11 +364,13 @@ def test_backend_selection(host):
     assert (kc.kernel_a, kc.kernel_c) == (b"helix_chunk_state_hb_x6agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
     assert kc.bccopy_bytes == 2 * (S * L * G * N * 2)
     assert k4.bccopy_bytes > 0   # 80 heads per group: copies by default
-    # Pass A writes one 16-byte decay record per (seq, chunk, head, token) for
-    # the walk and for the fp32 path's bf16x6 Pass C.
-    recs = S * (-(-L // 64)) * H * 64 * 16
-    assert k.rec_bytes == recs
-    assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == recs
+    # Pass A writes one decay record per (seq, chunk, head, token) for the
+    # walk and for the fp32 path's bf16x6 Pass C.
+    # 8 bytes for the walk (dt, Lcum log2 e), 16 for the fp32 path (dt,
+    # exp(Lcum), Lcum in fp64).
+    recs = S * (-(-L // 64)) * H * 64
+    assert k.rec_bytes == 8 * recs
+    assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == 16 * recs
     assert host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
     assert kc.total_bytes >= kc.s_seg_bytes + kc.bccopy_bytes and kc.total_bytes > k.total_bytes
     k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(CONFIG_SHAPES["cfg4a"]))

@@ -96,12 +96,26 @@ def test_noalloc_headline_shape(gpu):
     assert np.array_equal(y_a, y_b) and np.array_equal(s_a, s_b)
 
 
-def test_noalloc_capped_plan(gpu):
-    # BASELINE config 4a on the bf16 path: 136 MiB of scratch under the
-    # default budget, so the entry point plans it for its 128 MiB array in
-    # several groups carried through s1, as helix_scan_encode does with
-    # HELIX_SCRATCH_MB=128 (bitwise), and close to the default plan's result.
+def test_noalloc_config4a(gpu):
+    # BASELINE config 4a on the bf16 path: 116 MiB of scratch, within the
+    # fixed array; the same plan and kernels as helix_scan_encode, bitwise.
     p = po.problem_gauss(4096, 8, 80, 64, 128, 1, 1004, 0.1)
+    d = p.d.copy()
+    d.backend = HELIX_BACKEND_MPP
+    d.multipass = True
+    assert 0 < gpu.scratch_size(d) <= abi.NOALLOC_SCRATCH_BYTES
+    y_a, s_a = _encode(gpu, p, d, noalloc=False)
+    y_b, s_b = _encode(gpu, p, d, noalloc=True)
+    assert y_a.tobytes() == y_b.tobytes() and s_a.tobytes() == s_b.tobytes()
+
+
+def test_noalloc_capped_plan(gpu):
+    # Config 4a's shape with ten sequences on the bf16 path: 145 MiB of
+    # scratch under the default budget, so the entry point plans it for its
+    # 128 MiB array in several groups carried through s1, as
+    # helix_scan_encode does with HELIX_SCRATCH_MB=128 (bitwise), and close to
+    # the default plan's result.
+    p = po.problem_gauss(4096, 10, 80, 64, 128, 1, 1004, 0.1)
     d = p.d.copy()
     d.backend = HELIX_BACKEND_MPP
     d.multipass = True
