@@ -42,6 +42,7 @@ REF_TOKS = 1315051.0
 
 CFG = dict(L=8192, S=1, H=64, P=64, N=128, G=8)
 ARENA_BYTES = 4 << 30   # the headline workload's inputs, outputs and scratch fit
+Y_PLACES, Y_STEP = 4, 1 << 20   # y placements timed for the headline (1 MiB apart)
 
 # BASELINE.json's configurations (config 4 in its two head-dim variants): shape,
 # the paths each is quoted on, and the distributions that differ from the common
@@ -139,6 +140,26 @@ def time_variant(v: Variant, steps: int, stream, only: str | None = None):
         return [a.elapsed_time(b) for a, b in evs]
     finally:
         os.environ.pop("HELIX_ONLY_PASS", None)
+
+
+def time_placements(v: Variant, steps: int, stream, ys):
+    """Per-step event times (ms) of `steps` whole scans, step i writing y at
+    ys[i % len(ys)] (the same output at other addresses). Returns the per-step
+    times and, per placement, the times of its steps."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    y0 = v.y
+    try:
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(evs):
+            v.y = ys[i % len(ys)]
+            a.record(stream)
+            v.encode(stream)
+            b.record(stream)
+        torch.cuda.synchronize()
+    finally:
+        v.y = y0
+    ts = [a.elapsed_time(b) for a, b in evs]
+    return ts, [ts[k::len(ys)] for k in range(len(ys))]
 
 
 def time_passes(v: Variant, steps: int, stream):
@@ -283,8 +304,10 @@ def cpu_baseline(budget_s: float = 20.0):
         t_tot += time.perf_counter() - t0
         n_heads += 1
     per_head = t_tot / n_heads
+    F = algorithmic_flops(L, S, H, P, N)
     out["cpu_baseline"] = {
         "value": S * L / (per_head * H), "unit": "tok/s", "cores": 1,
+        "gflops": F / (per_head * H) / 1e9,
         "kind": "reference" if use_ref else "port",
         "sample": f"{n_heads} of {H} heads of config 2 (L={L}), fp64 sequential "
                   f"{'ref::scan from oracle/_ref' if use_ref else 'oracle_scan'}, 1 thread, "
@@ -298,6 +321,7 @@ def cpu_baseline(budget_s: float = 20.0):
     tm = time.perf_counter() - t0
     out["cpu_baseline_mt"] = {
         "value": S * L / (tm * H / nh), "unit": "tok/s", "cores": ncpu, "kind": "port",
+        "gflops": F / (tm * H / nh) / 1e9,
         "sample": f"{nh} of {H} heads of config 2, fp64 sequential oracle_scan_mt on "
                   f"{ncpu} threads (os.sched_getaffinity), {tm:.1f} s; scaled to {H} heads",
         "hardware_concurrency": os.cpu_count(),
@@ -346,6 +370,74 @@ def config_report(ctx, stream, dev, steps: int, warm_ms: float, names=None):
     return out
 
 
+IMPLS = {
+    # name: (backend, multipass), the reference bench's --impl names
+    # (bench/bench_scan.mm:128-140): "3pass" leaves the backend to AUTO (the
+    # bf16 path here), the suffixes pin the fp32 (SGMMA) or bf16 (MPP) Pass C.
+    "1pass": (HELIX_BACKEND_AUTO, False),
+    "3pass": (HELIX_BACKEND_AUTO, True),
+    "3pass-sgmma": (HELIX_BACKEND_SGMMA, True),
+    "3pass-mpp": (HELIX_BACKEND_MPP, True),
+}
+
+
+def shape_bench(args, dev):
+    """The reference bench's per-shape mode (bench/bench_scan.mm:65-240): one
+    problem of the given shape (BASELINE.json's distributions, seed 99), each
+    implementation in --impl timed interleaved in this process after a
+    wall-clock warm-up; per implementation the fastest and median scan,
+    tok/s and GFLOP/s at the fastest, the max/min spread and the speed-up
+    over 1pass. With --json, one JSON object per implementation."""
+    cfg = dict(CFG)
+    for k, a in (("L", args.L), ("S", args.n_seq), ("H", args.heads), ("P", args.head_dim), ("N", args.d_state),
+                 ("G", args.groups)):
+        if a is not None:
+            cfg[k] = a
+    L, S, H, P, N, G = (cfg[k] for k in "LSHPNG")
+    tensors = make_inputs(99, dev, cfg)
+    ctx = Context(0)
+    stream = torch.cuda.current_stream(dev)
+    variants = []
+    for name in (args.impl or "1pass,3pass").split(","):
+        if name not in IMPLS:
+            print(f"bench.py: unknown impl {name!r} (one of {', '.join(IMPLS)})", file=sys.stderr)
+            sys.exit(2)
+        backend, multipass = IMPLS[name]
+        try:
+            variants.append(Variant(name, ctx, backend, tensors, multipass=multipass))
+        except AssertionError:
+            print(f"bench.py: shape unsupported for impl {name!r}", file=sys.stderr)
+            sys.exit(1)
+    t0 = time.perf_counter()
+    rounds = 0
+    while (time.perf_counter() - t0) * 1e3 < args.warmup_ms or rounds < 3:
+        for v in variants:
+            v.encode(stream)
+        torch.cuda.synchronize()
+        rounds += 1
+    times = {v.name: [] for v in variants}
+    for _ in range(args.iters):
+        for v in variants:
+            times[v.name] += time_variant(v, 1, stream)
+    F = algorithmic_flops(L, S, H, P, N)
+    base = min(times["1pass"]) if "1pass" in times else None
+    if not args.json:
+        print(f"L={L} H={H} P={P} N={N} G={G} seq={S}")
+        print(f"  {'impl':12s} {'ms':>9s} {'median':>9s} {'tok/s':>13s} {'GFLOP/s':>10s} {'spread':>7s} {'vs 1pass':>8s}  kernels")
+    for v in variants:
+        d = dist(times[v.name])
+        sec = d["min"] * 1e-3
+        rel = base / d["min"] if base else None
+        if args.json:
+            print(json.dumps({"impl": v.name, "L": L, "n_seq": S, "heads": H, "head_dim": P, "d_state": N,
+                              "n_group": G, "ms": d["min"], "ms_median": d["median"], "spread": d["spread"],
+                              "tok_per_s": L * S / sec, "gflops": F / sec * 1e-9, "speedup_vs_1pass": rel,
+                              "kernel": v.kernel}), flush=True)
+        else:
+            print(f"  {v.name:12s} {d['min']:9.4f} {d['median']:9.4f} {L * S / sec:13.0f} {F / sec * 1e-9:10.0f} "
+                  f"{d['spread']:6.2f}x {('%.2fx' % rel) if rel else '-':>8s}  {v.kernel}", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +457,16 @@ def main():
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
                     help="also run a plain device copy of this size (a known-traffic kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    shape = ap.add_argument_group("per-shape mode (the reference bench's flags; any of them selects it)")
+    shape.add_argument("--L", type=int, default=None, help="tokens per sequence")
+    shape.add_argument("--n-seq", type=int, default=None)
+    shape.add_argument("--heads", type=int, default=None)
+    shape.add_argument("--head-dim", type=int, default=None)
+    shape.add_argument("--d-state", type=int, default=None)
+    shape.add_argument("--groups", type=int, default=None)
+    shape.add_argument("--impl", default=None, help=f"comma list of {', '.join(IMPLS)} (default 1pass,3pass)")
+    shape.add_argument("--iters", type=int, default=20)
+    shape.add_argument("--json", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -374,6 +476,10 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if any(a is not None for a in (args.L, args.n_seq, args.heads, args.head_dim, args.d_state, args.groups,
+                                   args.impl)):
+        shape_bench(args, dev)
+        return
     ctx = Context(0)
     if args.only_config:
         stream = torch.cuda.current_stream(dev)
@@ -429,23 +535,37 @@ def main():
     F_A = 2.0 * S * H * nch * 64 * N * P
     F_C = F - F_A
     bytes_alg = algorithmic_bytes(L, S, H, P, N, G)
+    # Where the caller's y lands in memory is the caller's choice: the timed
+    # steps of the two paths write y at Y_PLACES placements 1 MiB apart within
+    # one 4 MiB window (the same output tensor shifted), one placement per step
+    # in turn, and the reported time is the median over placements of each
+    # placement's mean.
+    y_bytes = variants[0].y.numel() * 4
+    y_pool = torch.empty(y_bytes + (Y_PLACES - 1) * Y_STEP + 4096, dtype=torch.uint8, device=dev)
+    ys = [y_pool[k * Y_STEP:k * Y_STEP + y_bytes].view(torch.float32).view(variants[0].y.shape)
+          for k in range(Y_PLACES)]
     results = {}
     for i, v in enumerate(variants):
         warm_up(v, args.warmup_ms if i == 0 else min(args.warmup_ms, 200.0))
         # Whole op: K steps bracketed by synchronize; per-step events too.
         torch.cuda.synchronize()
         w0 = time.perf_counter()
-        ts = time_variant(v, args.steps, stream)
+        place = None
+        if v.name in ("bf16", "fp32"):
+            ts, per_place = time_placements(v, args.steps, stream, ys)
+            place = [statistics.fmean(t) for t in per_place]
+        else:
+            ts = time_variant(v, args.steps, stream)
         torch.cuda.synchronize()
         wall = (time.perf_counter() - w0) / args.steps * 1e3
         # Per-pass split (HELIX_ONLY_PASS) exists only for the multipass path.
         passes = time_passes(v, args.steps, stream) if v.multipass else None
         in_scan = time_in_scan(v, args.steps, stream) if v.multipass and v.name == "bf16" else None
         d = dist(ts)
-        ms = statistics.fmean(ts)
+        ms = statistics.median(place) if place else statistics.fmean(ts)
         peak_c = PEAK_BF16_MFMA if v.name == "bf16" else PEAK_FP32_MFMA
         t_roof = max(F_A / PEAK_FP32_MFMA + F_C / peak_c, bytes_alg / PEAK_HBM)
-        results[v.name] = dict(ms=ms, d=d, wall_ms=wall, passes=passes, in_scan=in_scan, t_roof=t_roof,
+        results[v.name] = dict(ms=ms, d=d, wall_ms=wall, passes=passes, in_scan=in_scan, t_roof=t_roof, place=place,
                                kernel=v.kernel, plan=v.plan)
 
     # Dominant kernel of the headline (bf16) path and its roofline. Every pass
@@ -508,6 +628,10 @@ def main():
         "roofline": roof,
         "passes_roofline": passes_roof,
         "timing_ms": {k: round(vv, 5) for k, vv in r["d"].items()},
+        "y_placements": {"offsets_MiB": [k * Y_STEP / 2**20 for k in range(Y_PLACES)],
+                         "ms": [round(t, 5) for t in r["place"]],
+                         "spread": max(r["place"]) / min(r["place"]),
+                         "value_from": "median over placements of each placement's mean step time"},
         # Per-pass kernel times: event-bracketed single-pass encodes less an
         # empty encode between the same events (event_pair_us), and the
         # passes' times inside whole scans (time_in_scan).
@@ -518,6 +642,7 @@ def main():
             "tok_s": S * L / (results["fp32"]["ms"] * 1e-3),
             "gflops": F / (results["fp32"]["ms"] * 1e-3) / 1e9,
             "ms_per_step": results["fp32"]["ms"],
+            "y_placement_ms": [round(t, 5) for t in results["fp32"]["place"]],
             "roofline_frac": results["fp32"]["t_roof"] / (results["fp32"]["ms"] * 1e-3),
             "passes_us": pass_us(results["fp32"]["passes"]),
             "kernel": results["fp32"]["kernel"],
