@@ -22,12 +22,13 @@
 //   - The B planes are double-buffered: the next chunk's are written while
 //     this chunk's are read, so a chunk costs one barrier.
 //   - The decay preamble of each item runs in one of its two waves, a chunk
-//     ahead, and reaches the other through LDS (double-buffered, so the one
-//     barrier per chunk covers it).
-//   - Every memory instruction of the chunk loop runs on every path (masked
-//     stores go through a zero-range resource or an out-of-range offset): on
-//     gfx950 the vmcnt counter counts stores too, and a store on one path only
-//     would make the compiler's waits cover the next chunk's loads.
+//     ahead, the two taking turns, and reaches the other through LDS
+//     (double-buffered, so the one barrier per chunk covers it).
+//   - Every load of the chunk loop runs on every path, and every store but
+//     the preamble's record (masked stores go through a zero-range resource
+//     or an out-of-range offset): on gfx950 the vmcnt counter counts stores
+//     too, and a memory instruction on one path only makes the compiler's
+//     waits at the merge conservative.
 //   - The bf16 copies of B and C for the walking Pass C are written by one
 //     wave per block of its rows per group: wave w of item block ib copies
 //     its block when ib == w % (item blocks per group).
@@ -266,7 +267,8 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     constexpr int NTN = NP / 32;        // 32-row n tiles per wave
     constexpr int PLANES = NS * NP * HB_RS;
     __shared__ __attribute__((aligned(16))) __bf16 sB[2 * PLANES];   // two chunks' planes
-    // Per chunk parity and item: w_j of the chunk's 64 tokens, and L_end at [64].
+    // Per chunk parity and item: w_j of the chunk's 64 tokens, and L_end (fp64
+    // bits) at [64], [65].
     __shared__ __attribute__((aligned(16))) float sW[2][HB][HELIX_CS + 4];
 
     const int tid = threadIdx.x;
@@ -311,7 +313,8 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     const IO* __restrict__ B_g = reinterpret_cast<const IO*>(b.B) + seq * p.seq_b + g * p.s_b[1];
     const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
     const bool copier = BCC && (wave % nib) == ib;
-    const bool leader = item_ok && slab == 0 && pt == 0;   // stores the head's records
+    const bool head_leader = item_ok && slab == 0;           // the head's records come from its first slab
+    const bool leader = head_leader && pt == 0;              // stores the head's log-decay
     const long long tile_off = state_tile_off(p, h, slab);
     const unsigned tile_bytes = item_ok ? 64u * NP * 4u : 0u;   // spare waves store nothing
 
@@ -329,7 +332,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     auto nth = [&](int it) { return MODE == 0 ? min(c_begin + it, c_end - 1) : max(c_end - 1 - it, c_begin); };
     float lam = 0.0f;    // MODE 0: log-decay of the segment before the current chunk
     double mu = 0.0;     // MODE 2: log-decay from the current chunk's end to the segment's end
-    double lend = 0.0;   // L_end of the current chunk, from its preamble a step earlier
+    double lend = 0.0;   // L_end of the current chunk, read from its weight buffer
 
     // B planes of chunk c into `planes` (state indices q4 + k, k0 <= k < k1, of
     // this thread's rows), and the bf16 copies of its B and C rows.
@@ -373,20 +376,26 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     HbRows<NP, IO> rows;
     float dtraw;   // dt of token lane of the chunk the next preamble forms
 
-    // The preamble of chunk c (weights shifted by `shift`), into the chunk's
-    // weight buffer; returns its L_end. Then the chunk's record and (MODE 0)
-    // ld[c] = lam_c, cancelled by a zero range on all but the head's leader
-    // wave, and on every wave when the call only repeats the segment's last
-    // chunk (`live` false: they are already stored). Both waves of an item form
-    // it and write the same weights: the work is balanced over the SIMD's two
-    // waves and the chunk loop has no branch, so the preamble's ALU work can be
-    // scheduled among the MFMAs.
+    // The preamble of chunk c (weights shifted by `shift`) into the chunk's
+    // weight buffer, with its L_end (fp64 bits) at [64] and [65]. Then the
+    // chunk's record and (MODE 0) ld[c] = lam_c, cancelled by a zero range
+    // past the head's first P slab, and when the call only repeats the
+    // segment's last chunk (`live` false: they are already stored). One wave
+    // of an item forms it, the item's two waves taking turns chunk by chunk
+    // (both sit on one SIMD, so forming it in both doubled its ALU work on
+    // that SIMD: 2.4 us of a config-2 scan); the other reads the weights and
+    // L_end from LDS after the chunk's barrier.
     auto preamble = [&](int c, double shift, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
         const HbPre pr = hb_preamble<MODE, R64>(p, dtraw, A_h, c, lane, shift);
         wdst[is][lane] = pr.w;
+        if (lane == 0) {
+            const unsigned long long u = __builtin_bit_cast(unsigned long long, pr.lend);
+            wdst[is][HELIX_CS] = __builtin_bit_cast(float, (unsigned)u);
+            wdst[is][HELIX_CS + 1] = __builtin_bit_cast(float, (unsigned)(u >> 32));
+        }
         // The record's address is formed unconditionally (a select of two
         // pointers becomes a branch); without records its range is zero.
-        const bool rec = live && leader && b.pre != nullptr;
+        const bool rec = live && head_leader && b.pre != nullptr;
         constexpr int RB = (MODE == 2 && !R64) ? HELIX_REC_WALK_BYTES : HELIX_REC64_BYTES;
         const unsigned long long recp =
             (unsigned long long)b.pre + (unsigned long long)((((long long)seq * p.cpg + c) * p.n_head + h) * (HELIX_CS * RB));
@@ -397,10 +406,9 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
             __builtin_amdgcn_raw_buffer_store_b128(pr.rec, rr, lane * 16, 0, 0);
         if constexpr (MODE == 0) {
             const float* ldp = b.ld + seq * p.ld_seq + (long long)c * p.n_head + h;
-            __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && leader ? 4u : 0u),
+            __builtin_amdgcn_raw_buffer_store_b32(as_u32(lam_c), make_rsrc_u(ldp, live && head_leader ? 4u : 0u),
                                                   lane == 0 ? 0 : (int)0x80000000, 0, 0);
         }
-        return pr.lend;
     };
 
     // Chunk nth(it). Its B planes are in `cur` and its weights in `wcur` (both
@@ -414,7 +422,11 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                     float (*wnxt)[HELIX_CS + 4]) {
         const int c = nth(it), cn = nth(it + 1);
         const float* __restrict__ wrow = wcur[is];
+        // L_end of this chunk, from its preamble a step earlier.
+        lend = __builtin_bit_cast(double, (unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS]) |
+                                              ((unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS + 1]) << 32));
         const float lendf = (float)lend;
+        const bool forms = pt == (it & 1);   // this wave forms the next chunk's preamble
         if constexpr (MODE == 0) {
             // R_c, the state entering chunk c from this segment's own chunks
             // (none for its first chunk: a zero range stores nothing).
@@ -507,10 +519,10 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
             if (s == 1) {
                 if constexpr (MODE == 0) {
                     lam += lendf;
-                    lend = preamble(cn, 0.0, lam, wnxt, it + 1 < n_ch);
+                    if (forms) preamble(cn, 0.0, lam, wnxt, it + 1 < n_ch);
                 } else {
                     mu += lend;
-                    lend = preamble(cn, mu, 0.0f, wnxt, it + 1 < n_ch);
+                    if (forms) preamble(cn, mu, 0.0f, wnxt, it + 1 < n_ch);
                 }
             }
             vmem_fence();
@@ -545,7 +557,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c0, lane, wave, N, copier);
 #pragma unroll
     for (int s = 0; s < 4; ++s) hb_load_xs<IO>(xs.v[s], p, x_w, c0, s, lane, pt, pw);
-    lend = preamble(c0, 0.0, 0.0f, sW[0], true);
+    if (pt == 1) preamble(c0, 0.0, 0.0f, sW[0], true);
     stage_planes(rows, sB, 0, 4);
     copy_rows(rows, c0);
     hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c1, lane, wave, N, copier);
