@@ -280,7 +280,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
 
     const int ipg = p.heads_per_group * p.n_pslab;        // items per group
     const int nib = (ipg + HB - 1) / HB;                  // item blocks per group
-    const unsigned total = (unsigned)(p.n_seq * p.n_group * nib * p.n_seg);
+    const unsigned total = (unsigned)p.n_seq * (unsigned)p.n_group * (unsigned)nib * (unsigned)p.n_seg;
     unsigned wid = xcd_logical_id(blockIdx.x, total);
     // Logical order: item block, group, segment, sequence. An XCD's share of
     // the logical ids is then a run of consecutive segments over every group:

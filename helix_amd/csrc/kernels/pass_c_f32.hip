@@ -60,7 +60,7 @@ __device__ __forceinline__ void chunk_out_f32_impl(const HelixScanParams& p, con
     // 1-D grid of n_cg * (n_group * n_hblk) * n_seq workgroups, chunk fastest
     // in the logical order so a segment's chunks (which share S_seg) and a
     // chunk's head blocks (which share B and C) stay on one XCD.
-    const unsigned n_gh  = (unsigned)(p.n_group * p.n_hblk);
+    const unsigned n_gh  = (unsigned)p.n_group * (unsigned)p.n_hblk;
     const unsigned total = (unsigned)p.n_cg * n_gh * (unsigned)p.n_seq;
     const unsigned wid   = xcd_logical_id(blockIdx.x, total);
     const int cg  = (int)(wid % (unsigned)p.n_cg);

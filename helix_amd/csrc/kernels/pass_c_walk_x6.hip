@@ -154,20 +154,23 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     const int hpg = p.heads_per_group;
     const int npair = (hpg + HPW - 1) / HPW;
 
-    // 1-D grid in the logical order (head block, group, slab, sequence, walk
-    // segment). An XCD's share of the logical ids then covers whole walk
+    // 1-D grid in the logical order (head block, group, slab, walk segment,
+    // sequence). An XCD's share of the logical ids then covers whole walk
     // segments over every group: a group's head blocks share the XCD (and the
     // chunk's B and C in its L2), and the XCD's x reads and y writes are whole
-    // token rows of one stretch of the sequence. With the walk segment as the
-    // faster index (an XCD per group, 2 KiB of every 16 KiB token row at
-    // config 2) the fp32 path took 212-215 us; 207-210 us in this order.
-    const unsigned total = (unsigned)(p.n_walk * p.n_group * npair * p.n_pslab * p.n_seq);
+    // token rows of one stretch of a sequence. With the walk segment as the
+    // fastest index after the group (an XCD per group, 2 KiB of every 16 KiB
+    // token row at config 2) the fp32 path took 212-215 us; 207-210 us in this
+    // order. The walk segment sits below the sequence, as in the bf16 walk,
+    // so that an XCD's share stays within one sequence of a batch.
+    const unsigned total = (unsigned)p.n_walk * (unsigned)p.n_group * (unsigned)npair *
+                           (unsigned)p.n_pslab * (unsigned)p.n_seq;
     unsigned wid = xcd_logical_id(blockIdx.x, total);
     const int pair = (int)(wid % (unsigned)npair);    wid /= (unsigned)npair;
     const int g    = (int)(wid % (unsigned)p.n_group); wid /= (unsigned)p.n_group;
     const int slab = (int)(wid % (unsigned)p.n_pslab); wid /= (unsigned)p.n_pslab;
-    const int seq  = (int)(wid % (unsigned)p.n_seq);   wid /= (unsigned)p.n_seq;
-    const int seg  = (int)wid;
+    const int seg  = (int)(wid % (unsigned)p.n_walk); wid /= (unsigned)p.n_walk;
+    const int seq  = (int)wid;
     // A workgroup of the last pair may have one head: its spare waves walk
     // that head again and store nothing.
     const int hslot = HPW * pair + hw;

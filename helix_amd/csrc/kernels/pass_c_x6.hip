@@ -51,7 +51,7 @@ __device__ __forceinline__ void chunk_out_x6_impl(const HelixScanParams& p, cons
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
 
-    const unsigned n_gh  = (unsigned)(p.n_group * p.n_hblk);
+    const unsigned n_gh  = (unsigned)p.n_group * (unsigned)p.n_hblk;
     const unsigned total = (unsigned)p.n_cg * n_gh * (unsigned)p.n_seq;
     const unsigned wid   = xcd_logical_id(blockIdx.x, total);
     const int cg  = (int)(wid % (unsigned)p.n_cg);
