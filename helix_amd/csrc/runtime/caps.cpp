@@ -10,6 +10,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <string>
 #include <vector>
 
@@ -241,6 +244,7 @@ helix_tuning tuning_from_env() {
     const int bc = env_switch("HELIX_WALK_BCCOPY");
     t.bccopy = bc == 0 ? 0 : bc > 0 ? 1 : -1;
     t.seg_len = (int)env_long("HELIX_SEG_LEN", 0);
+    t.walk_len = (int)env_long("HELIX_WALK_LEN", 0);
     t.hblk = (int)env_long("HELIX_HBLK", 0);
     const int fw = env_switch("HELIX_F32_WALK");
     if (fw >= 0) t.f32_walk = fw > 0 ? 1 : 0;
@@ -326,13 +330,122 @@ int choose_walk_len(const helix_scan_desc& d, int cpg) {
     return (int)std::max<long>(1, std::min<long>(len, cpg));
 }
 
+// Dispatch model of a one-workgroup-per-CU launch on MI355X, used to pick
+// the walk length when every walk's start state comes from the walk's own
+// prologue (fused Pass B). Workgroup b runs on XCD b % 8 (the kernels decode
+// their logical id with xcd_logical_id); in each XCD, four shader engines of
+// eight CUs take the XCD's workgroups round-robin, in dispatch order, and a
+// workgroup waits for a CU of its own engine. Every running workgroup moves
+// one chunk step per lat + k * load microseconds, load being the running
+// workgroups over the chip (each weighted by the share of its heads or items
+// that are real). lat and k, and a fixed cost per workgroup (o, plus g per
+// segment aggregate a walk's prologue folds in), were fitted to Pass A and the
+// bf16 walk timed at 19 lengths on S=8 L=4096 H=80 P=64 and H=27 P=192 (N=128):
+// rms errors 1.8 and 2.0 %. Without the per-engine round robin the Pass A fit
+// misses by up to 17 %: at H=27 and two segments, one engine in each XCD got
+// six long and five short workgroups, ran three shorts in a row, and Pass A
+// took the time of one 64-chunk segment.
+struct DispatchCost {
+    double lat, k, o, g;
+};
+constexpr DispatchCost kCostA{3.0, 0.009, 2.0, 0.0};
+constexpr DispatchCost kCostWalk{2.25, 0.007, 0.5, 0.5};
+constexpr int kXcds = 8, kEnginesPerXcd = 4, kCusPerEngine = 8;
+
+// Microseconds for workgroups given in logical-id order as (chunk steps,
+// weight). Every running workgroup advances at the same rate, so each
+// engine's queue is list-scheduled at unit speed (the order of events does not
+// depend on the rate) to the makespan T in chunk steps; the chip is busy
+// throughout, and the integral of lat + k * load over T is
+// lat * T + k * sum(weight * steps).
+double dispatch_us(const std::vector<std::pair<double, double>>& wg, const DispatchCost& c) {
+    const size_t n = wg.size();
+    const size_t per = n / kXcds;
+    double cu[kXcds * kEnginesPerXcd][kCusPerEngine] = {};
+    double T = 0.0, work = 0.0;
+    for (size_t b = 0; b < n; ++b) {
+        const size_t x = b % kXcds, j = b / kXcds;
+        const size_t wid = b < per * kXcds ? x * per + j : b;
+        double* e = cu[x * kEnginesPerXcd + j % kEnginesPerXcd];
+        int m = 0;
+        for (int i = 1; i < kCusPerEngine; ++i)
+            if (e[i] < e[m]) m = i;
+        e[m] += wg[wid].first;
+        T = std::max(T, e[m]);
+        work += wg[wid].first * wg[wid].second;
+    }
+    return c.lat * T + c.k * work;
+}
+
+// Pass A (head-block kernel) and the walk with segments = walks of `len`
+// chunks over a single group of `cpg` chunks: the workgroups of both launches
+// in their kernels' logical order, priced by dispatch_us.
+double fused_lengths_us(const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg, int len) {
+    const int nseg = (cpg + len - 1) / len;
+    const int nslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
+    const int hpg = d.n_head / d.n_group;
+    auto seg_steps = [&](int s) { return (double)std::min(len, cpg - s * len); };
+    std::vector<std::pair<double, double>> wg;
+    // Pass A: (item block, group, segment, sequence), item = (head, P slab).
+    const int ipg = hpg * nslab, nib = (ipg + HELIX_HB - 1) / HELIX_HB;
+    wg.reserve((size_t)d.n_seq * nseg * d.n_group * nib);
+    for (int seq = 0; seq < d.n_seq; ++seq)
+        for (int s = 0; s < nseg; ++s)
+            for (int g = 0; g < d.n_group; ++g)
+                for (int ib = 0; ib < nib; ++ib)
+                    wg.emplace_back(seg_steps(s) + kCostA.o,
+                                    (double)std::min(HELIX_HB, ipg - HELIX_HB * ib) / HELIX_HB);
+    const double a = dispatch_us(wg, kCostA);
+    // Walk: (head block, group, slab, walk, sequence).
+    const int hpw = tr.walk_hpw ? tr.walk_hpw : HELIX_WALK_HPW(tr.np);
+    const int npair = (hpg + hpw - 1) / hpw;
+    wg.clear();
+    for (int seq = 0; seq < d.n_seq; ++seq)
+        for (int s = 0; s < nseg; ++s)
+            for (int sl = 0; sl < nslab; ++sl)
+                for (int g = 0; g < d.n_group; ++g)
+                    for (int pr = 0; pr < npair; ++pr)
+                        wg.emplace_back(seg_steps(s) + kCostWalk.o + kCostWalk.g * s,
+                                        (double)std::min(hpw, hpg - hpw * pr) / hpw);
+    return a + dispatch_us(wg, kCostWalk);
+}
+
+// The walk length (= Pass A's segment) with the least modelled time among
+// those of at most kFuseBMaxSegs walks, from `shortest` up. Memoized: the
+// plan is remade on every encode.
+int fused_walk_len(const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg, int shortest) {
+    using Key = std::tuple<int, int, int, int, int, int, int, int>;
+    static std::mutex mu;
+    static std::map<Key, int> memo;
+    const Key key{d.n_seq, d.n_head, d.head_dim, d.n_group, tr.np, tr.walk_hpw, cpg, shortest};
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        const auto it = memo.find(key);
+        if (it != memo.end()) return it->second;
+    }
+    int best = shortest;
+    double best_us = fused_lengths_us(d, tr, cpg, shortest);
+    for (int len = shortest + 1; len <= cpg; ++len) {
+        const double us = fused_lengths_us(d, tr, cpg, len);
+        if (us < best_us) {
+            best_us = us;
+            best = len;
+        }
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (memo.size() > 4096) memo.clear();
+    memo.emplace(key, best);
+    return best;
+}
+
 // Pass A's segment (seg_len) and the walk's (walk_len, a multiple of it). The
 // head-block Pass A takes the longest divisor of walk_len that still gives
-// ~kTargetWgHb workgroups, so its segments nest in the walk's. HELIX_SEG_LEN
-// sets seg_len, and walk_len is then rounded to a multiple of it.
+// ~kTargetWgHb workgroups, so its segments nest in the walk's. HELIX_WALK_LEN
+// sets walk_len, HELIX_SEG_LEN sets seg_len, and walk_len is then rounded to a
+// multiple of it.
 void choose_lengths(const helix_tuning& tu, const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg,
                     int* seg_len, int* walk_len) {
-    int w = choose_walk_len(d, cpg);
+    int w = tu.walk_len > 0 ? std::min(tu.walk_len, cpg) : choose_walk_len(d, cpg);
     int a = w;
     if (tu.seg_len > 0) {
         a = std::min(tu.seg_len, cpg);
@@ -349,6 +462,17 @@ void choose_lengths(const helix_tuning& tu, const helix_scan_desc& d, const Heli
                 break;
             }
         }
+        // Walks that are Pass A's segments, few enough for the walk's prologue
+        // to fold them in (fused Pass B), over a single group: a longer walk
+        // may balance the one-workgroup-per-CU launches better. At S=8 L=4096
+        // N=128 the model takes 43-chunk walks at H=80 P=64 and 22 at H=27
+        // P=192, in place of 16: whole scans 605 -> 556 and 649 -> 588 us; on
+        // seven other shapes of 2048-4096 tokens x 4-16 sequences it was 21-78
+        // us faster on the bf16 path and no slower on the fp32 one.
+        const int n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
+        if (a == w && tu.walk_len <= 0 && tu.fuse_b != 0 && tr.walk && tr.walk_fuse_b && cpg == n_chunks &&
+            (cpg + w - 1) / w <= kFuseBMaxSegs)
+            a = w = fused_walk_len(d, tr, cpg, w);
     }
     if (!tr.walk) w = a;
     *seg_len = a;

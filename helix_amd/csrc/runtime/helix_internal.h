@@ -28,6 +28,7 @@ struct helix_tuning {
     int  fuse_b      = -1;     // HELIX_FUSE_B=0|1: Pass B in the walk's prologue
     int  bccopy      = -1;     // HELIX_WALK_BCCOPY=0: no bf16 copies of B and C
     int  seg_len     = 0;      // HELIX_SEG_LEN: chunks per Pass A segment
+    int  walk_len    = 0;      // HELIX_WALK_LEN: chunks per walk (rounded to a multiple of seg_len)
     int  hblk        = 0;      // HELIX_HBLK: heads per chunk-parallel Pass C workgroup
     int  f32_walk    = -1;     // HELIX_F32_WALK=0 / 1: the fp32 path's chunk-parallel Pass C / walk
                                // (on per-chunk states stored by Pass A) at d_state 128

@@ -233,15 +233,15 @@ def test_null_context_and_desc():
 
 def test_noalloc_host_checks(host):
     # helix_scan_encode_noalloc plans for its fixed array: a scan whose plan
-    # needs more under the context's budget (config 4a with ten sequences on
-    # the bf16 path, 145 MiB; config 2 at d_state 256 on the fp32 path, whose
+    # needs more under the context's budget (config 4a with fourteen sequences
+    # on the bf16 path, 168 MiB; config 2 at d_state 256 on the fp32 path, whose
     # Pass A stores every chunk's state, 520 MiB) is cut into more groups;
     # only one that does not fit at one chunk per group is refused, before
     # anything is enqueued. A host-only context has no device for one that
-    # fits. Config 4a itself fits (116 MiB).
+    # fits. Config 4a itself fits (76 MiB).
     t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
     assert 0 < host.scratch_size(mp(CONFIG_SHAPES["cfg4a"])) <= abi.NOALLOC_SCRATCH_BYTES
-    for shape, backend in (((4096, 10, 80, 64, 128, 1), HELIX_BACKEND_MPP),
+    for shape, backend in (((4096, 14, 80, 64, 128, 1), HELIX_BACKEND_MPP),
                            ((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)):
         d = mp(shape, backend)
         assert host.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
@@ -352,9 +352,21 @@ def test_backend_selection(host):
     kf = tuned(HELIX_FUSE_B="1", HELIX_SEG_LEN="16").plan_info(mp(shape))
     assert kf.kernel_b is None and kf.launches == 2 and kf.seg_len == kf.walk_len == 16
     assert kf.pass_b == abi.PASS_B_IN_C
-    # Config 4a: one group of four segments per sequence, fused by default.
+    # Configs 4a and 4b: one group, walks that are Pass A's segments, fused by
+    # default. The dispatch model takes 43-chunk walks (43 + 21 per sequence)
+    # at 4a and 22-chunk ones (22 + 22 + 20) at 4b, where a 16-chunk cap gave
+    # four of each.
     k4 = host.plan_info(mp(CONFIG_SHAPES["cfg4a"]))
-    assert k4.segs_per_group == 4 and k4.kernel_b is None and k4.launches == 2 and k4.pass_b == abi.PASS_B_IN_C
+    assert k4.segs_per_group == 2 and k4.kernel_b is None and k4.launches == 2 and k4.pass_b == abi.PASS_B_IN_C
+    assert k4.seg_len == k4.walk_len == 43 and k4.walks_per_group == 2
+    k4b = host.plan_info(mp(CONFIG_SHAPES["cfg4b"]))
+    assert (k4b.seg_len, k4b.walk_len, k4b.segs_per_group, k4b.pass_b) == (22, 22, 3, abi.PASS_B_IN_C)
+    # HELIX_WALK_LEN and HELIX_SEG_LEN override it (the 16-chunk plan), and
+    # HELIX_WALK_LEN alone sets both lengths where Pass A's segment is the walk.
+    k16 = tuned(HELIX_WALK_LEN="16", HELIX_SEG_LEN="16").plan_info(mp(CONFIG_SHAPES["cfg4a"]))
+    assert (k16.seg_len, k16.walk_len, k16.segs_per_group, k16.pass_b) == (16, 16, 4, abi.PASS_B_IN_C)
+    kw = tuned(HELIX_WALK_LEN="32").plan_info(mp(CONFIG_SHAPES["cfg4a"]))
+    assert (kw.seg_len, kw.walk_len, kw.segs_per_group) == (32, 32, 2)
     km = tuned(HELIX_SCRATCH_MB="1").plan_info(mp(shape))   # many groups, carried through s1
     assert km.n_groups > 1 and km.kernel_b == b"helix_state_scan_f32" and km.pass_b == abi.PASS_B_LAUNCHED
     assert km.launches == 3 * km.n_groups
