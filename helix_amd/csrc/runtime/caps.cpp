@@ -610,7 +610,7 @@ bool build_params(const helix_scan_desc& d, HelixScanParams* o, std::string* why
     // Grid y and z are 16-bit on the hardware dispatch packet.
     const long kMaxYZ = 65535;
     const long zA = (long)d.n_seq * o->n_pslab;
-    if (d.n_head > kMaxYZ || zA > kMaxYZ || d.n_seq > kMaxYZ || (long)d.n_head > kMaxYZ) {
+    if (d.n_head > kMaxYZ || zA > kMaxYZ || d.n_seq > kMaxYZ) {
         if (why) *why = "launch grid exceeds 65535 in y or z (n_head or n_seq*n_pslab too large)";
         return false;
     }

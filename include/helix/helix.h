@@ -12,7 +12,8 @@
  *       device            NULL  -> the calling thread's current HIP device
  *                         else  -> (const int*) pointing at a HIP ordinal
  *       code_object_path  NULL  -> $HELIX_HSACO if set, else the gfx950 code
- *                                  object embedded in libhelix.so
+ *                                  object embedded in the library (libhelix.so
+ *                                  or libhelix.a)
  *                         else  -> a gfx950 code object file to load instead
  *   helix_scan_encode(ctx, cmd_buffer, ...)        cmd_buffer is a hipStream_t
  *   helix_scan_encode_into(ctx, encoder, ...)      encoder is a hipStream_t
