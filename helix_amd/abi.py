@@ -57,6 +57,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("walk_len", c_int32),
         ("walks_per_group", c_int32),
         ("pass_b", c_int32),
+        ("state_in_y", c_int32),
     ]
 
 

@@ -654,4 +654,27 @@ HELIX_DEV void store_decay_record64(const HelixScanParams& p, const HelixScanBuf
     __builtin_amdgcn_raw_buffer_store_b128(w, r, lane * 16, 0, 0);
 }
 
+// The single pass run as the three passes without scratch
+// (HelixScanParams::ytile): the tile of (seq, head h, P slab, segment s),
+// Pass A's aggregate D_s and then the start state Pass B writes over it, lies
+// in y's rows of segment s, in the slab's own columns: unit u (four floats of
+// the tile, helix_params.h order) at row u / (pw / 4), columns 4 (u % (pw / 4))
+// .. + 3 of the slab (pw its width, a multiple of 8; y's channel stride is 1).
+// The segment's log-decay takes the unit after the tile, in slab 0. Only the
+// walk of that (head, slab) over those rows writes these columns afterwards,
+// and it has read its start state before (the encoder checks that every
+// segment has the rows and that y overlaps no input).
+HELIX_DEV long long ytile_base(const HelixScanParams& p, int seq, int h, int slab, int seg) {
+    return seq * p.seq_y + (long long)seg * p.seg_len * HELIX_CS * p.s_y[0] + h * p.s_y[1] + (long long)slab * HELIX_HD;
+}
+// Float offset of tile unit u from ytile_base.
+HELIX_DEV long long ytile_unit(const HelixScanParams& p, int u, int pw) {
+    const int upr = pw >> 2;
+    return (long long)(u / upr) * p.s_y[0] + 4 * (u % upr);
+}
+// Float offset in y of the log-decay of segment seg of (seq, h).
+HELIX_DEV long long ytile_segld(const HelixScanParams& p, int seq, int h, int seg) {
+    return ytile_base(p, seq, h, 0, seg) + ytile_unit(p, 16 * p.np, min(HELIX_HD, p.head_dim));
+}
+
 #endif  // HELIX_COMMON_H

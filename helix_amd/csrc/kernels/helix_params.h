@@ -123,6 +123,11 @@ typedef struct HelixScanParams {
     int fuse_b;           /* 1 => no Pass B launch: the walking Pass C forms S_seg
                              from s0 and the aggregates D_s, and its last segment
                              writes s1 (single-group plans only) */
+    int ytile;            /* 1 => the single pass (multipass = false) run as the
+                             three passes with no scratch: the state tiles (Pass
+                             A's aggregates, then the walks' start states) and the
+                             segment log-decays live in y (ytile_* in
+                             helix_common.h); single group, Pass B launched */
 
     /* Scratch strides in elements (see the layout comment above). */
     long long sl_cg, sl_seq;     /* s_local: chunk stride (H*n_pslab*64*np), seq stride */

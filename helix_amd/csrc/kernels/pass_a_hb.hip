@@ -569,7 +569,26 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         step(it, sB + par * PLANES, sB + (PLANES - par * PLANES), sW[par], sW[par ^ 1]);
     }
 
-    // Segment aggregate D_s and the segment's log-decay.
+    // Segment aggregate D_s and the segment's log-decay: in scratch, or in y
+    // for the single pass without scratch (p.ytile; ytile_* in helix_common.h,
+    // the range covering the rows the tile and the log-decay take).
+    if (MODE == 2 && p.ytile) {
+        const int upr = pw >> 2;
+        const unsigned rows = (unsigned)((16 * NP + 1 + upr - 1) / upr);
+        const helix_rsrc ry = make_rsrc_u(b.y + ytile_base(p, seq, h, slab, seg),
+                                          item_ok ? rows * (unsigned)p.s_y[0] * 4u : 0u);
+#pragma unroll
+        for (int i = 0; i < NTN; ++i)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int off = (int)ytile_unit(p, tile_unit(NTN, pt, i, r4, 0) + lane, pw) * 4;
+                const u32x4 w = {as_u32(acc[i][4 * r4]), as_u32(acc[i][4 * r4 + 1]), as_u32(acc[i][4 * r4 + 2]),
+                                 as_u32(acc[i][4 * r4 + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(w, ry, off, 0, 0);
+            }
+        if (leader && lane == 0) b.y[ytile_segld(p, seq, h, seg)] = (float)mu;
+        return;
+    }
     {
         const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
         const helix_rsrc rs = make_rsrc_u(sg, tile_bytes);

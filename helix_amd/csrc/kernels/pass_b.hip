@@ -19,10 +19,13 @@
 //   s1[seq] = carry
 // Pass C starts a walk every walk_len / seg_len segments and reads the start
 // states of those segments only; the others are not stored.
+// YT: the single pass's form without scratch (HelixScanParams::ytile): the
+// tiles and the log-decays are read from, and the start states written to, y
+// (ytile_* in helix_common.h).
 #include "helix_common.h"
 
-extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(HelixScanParams p,
-                                                                           HelixScanBuffers b) {
+template <bool YT>
+__device__ __forceinline__ void state_scan_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     constexpr int BLK = 16;
     const int units_tile = 16 * p.np;                    // 64 * np / 4
     const int per_head = p.n_pslab * units_tile;
@@ -53,10 +56,21 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
     }
 
     f32x4* __restrict__ base =
-        reinterpret_cast<f32x4*>(b.s_seg + seq * p.sg_seq + (long long)h * per_head * 4) + u;
+        YT ? nullptr : reinterpret_cast<f32x4*>(b.s_seg + seq * p.sg_seq + (long long)h * per_head * 4) + u;
     const long long seg_stride = p.sg_seg / 4;           // in units
-    const float* __restrict__ sd = b.segld + seq * p.sd_seq + h;
+    const float* __restrict__ sd = YT ? nullptr : b.segld + seq * p.sd_seq + h;
     const int ratio = p.walk_len / p.seg_len;            // segments per walk
+    // YT: unit q of the slab's tile of segment s, and its log-decay, in y.
+    const int pws = min(HELIX_HD, p.head_dim - slab * HELIX_HD);
+    const long long yq = ytile_unit(p, q, pws);
+    auto d_ptr = [&](long long s) -> f32x4* {
+        if constexpr (YT) return reinterpret_cast<f32x4*>(b.y + ytile_base(p, seq, h, slab, (int)s) + yq);
+        else return base + s * seg_stride;
+    };
+    auto a_ptr = [&](long long s) -> const float* {
+        if constexpr (YT) return b.y + ytile_segld(p, seq, h, (int)s);
+        else return sd + s * p.n_head;
+    };
 
     // One block of up to K segments from s0: loads past the block's end
     // repeat its last segment, so there is no branch between the loads and
@@ -69,15 +83,15 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             const long long sk = s0 + min(k, nb - 1);
-            d[k] = base[sk * seg_stride];
-            a[k] = sd[sk * p.n_head];
+            d[k] = *d_ptr(sk);
+            a[k] = *a_ptr(sk);
         }
 #pragma unroll
         for (int k = 0; k < K; ++k) a[k] = expf(a[k]);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             if (k < nb) {
-                if ((s0 + k) % ratio == 0) base[(long long)(s0 + k) * seg_stride] = carry;
+                if ((s0 + k) % ratio == 0) *d_ptr(s0 + k) = carry;
                 carry = a[k] * carry + d[k];
             }
         }
@@ -95,4 +109,12 @@ extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(Heli
 #pragma unroll
         for (int k = 0; k < 4; ++k) cs[k] = carry[k];
     }
+}
+
+extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_f32(HelixScanParams p, HelixScanBuffers b) {
+    state_scan_impl<false>(p, b);
+}
+
+extern "C" __global__ __launch_bounds__(HELIX_WG) void helix_state_scan_y_f32(HelixScanParams p, HelixScanBuffers b) {
+    state_scan_impl<true>(p, b);
 }

@@ -158,8 +158,9 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
 // = S[16 nb + 4 q + r][p0 + pp] (q = lane / 16, pp = 16 w4 + c16). Without
 // p.fuse_b it is Pass B's S_seg tile of the Pass A segment the walk segment
 // starts at; with p.fuse_b the tiles hold Pass A's segment aggregates and the
-// workgroup runs Pass B's recurrence here.
-template <int NP>
+// workgroup runs Pass B's recurrence here. YT: the single pass without
+// scratch (HelixScanParams::ytile, never with fuse_b): the tile is in y.
+template <int NP, bool YT = false>
 __device__ __forceinline__ void walk_start_state(f32x4 (&R)[NP / 16], const HelixScanParams& p,
                                                  const HelixScanBuffers& b, int seq, int h, int slab, int seg,
                                                  int p0, int pw, int pp, int q, int w4, int c16, bool head_ok) {
@@ -169,9 +170,25 @@ __device__ __forceinline__ void walk_start_state(f32x4 (&R)[NP / 16], const Heli
     // tile's unit layout that is unit ((pt NT32 + nb/2) 4 + r4) 64 + lane'
     // with pt = w4/2, r4 = 2 (nb%2) + q/2, lane' = 32 (q%2) + 16 (w4%2) + c16.
     {
-        const float* tiles = b.s_seg + seq * p.sg_seq + state_tile_off(p, h, slab);
+        const float* tiles = YT ? nullptr : b.s_seg + seq * p.sg_seq + state_tile_off(p, h, slab);
         const int vunit = 64 * (q >> 1) + 32 * (q & 1) + 16 * (w4 & 1) + c16;
         const int pt = w4 >> 1;
+        if constexpr (YT) {
+            // The tile of the walk's first Pass A segment, in y's rows of that
+            // segment and the slab's columns (ytile_unit); the range covers
+            // the rows the tile and its log-decay take.
+            const int s = seg * (p.walk_len / p.seg_len);
+            const int upr = pw >> 2;
+            const unsigned rows = (unsigned)((16 * NP + 1 + upr - 1) / upr);
+            const helix_rsrc ry = make_rsrc(b.y + ytile_base(p, seq, h, slab, s), rows * (unsigned)p.s_y[0] * 4u);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int u = vunit + ((pt * NT32 + (nb >> 1)) * 4 + 2 * (nb & 1)) * 64;
+                R[nb] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      ry, (int)ytile_unit(p, u, pw) * 4, 0, 0));
+            }
+            return;
+        }
         auto load_tile = [&](int s, f32x4 (&T)[NB]) {
             const helix_rsrc rg = make_rsrc(tiles + (long long)s * p.sg_seg, 64u * NP * sizeof(float));
 #pragma unroll

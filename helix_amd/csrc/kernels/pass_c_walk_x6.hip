@@ -100,21 +100,30 @@ __device__ __forceinline__ void load_runs_x6(RunsWX6<NH>& r, const HelixScanPara
 
 // The decay record of token lane (store_decay_record64: dt, exp(Lcum), Lcum
 // in fp64) and x at this lane's P column for its K tokens j = 32 s + 8 q + e
-// (s = 0, 1; e = 0..7), prefetched a chunk ahead.
+// (s = 0, 1; e = 0..7), prefetched a chunk ahead. YT (no records): the raw dt
+// of token lane instead.
 struct StageWX6 {
     u32x4 rec;
+    float dtraw;
     float x[16];
 };
 
+template <bool YT>
 __device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParams& p, const float* __restrict__ rec_h,
-                                              const float* __restrict__ x_h, int c, int lane, int q, int pp,
-                                              int pw) {
+                                              const float* __restrict__ dt_h, const float* __restrict__ x_h, int c,
+                                              int lane, int q, int pp, int pw) {
     const int t0   = (p.chunk_base + c) * HELIX_CS;
     const int tlen = min(HELIX_CS, p.n_tok - t0);
     const int sx0 = sgpr_fresh((int)p.s_x[0]), sx2 = (int)p.s_x[2];
-    const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
     const helix_rsrc rx = make_rsrc(x_h + (long long)t0 * p.s_x[0], ((tlen - 1) * sx0 + (pw - 1) * sx2 + 1) * 4u);
-    st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    if constexpr (YT) {
+        const int sdt = (int)p.s_dt[0];
+        const helix_rsrc rdt = make_rsrc(dt_h + (long long)t0 * p.s_dt[0], ((tlen - 1) * sdt + 1) * 4u);
+        st.dtraw = buf_f32(rdt, min(lane, tlen - 1) * sdt * 4, 0);
+    } else {
+        const helix_rsrc rr = make_rsrc(rec_h + (long long)c * p.n_head * (HELIX_CS * 4), HELIX_CS * 16u);
+        st.rec = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    }
     // Rows past tlen read 0 (past the resource's range) or, with strides under
     // which a token row is shorter than the slab, another element of the
     // chunk: dt is 0 for them either way.
@@ -125,7 +134,11 @@ __device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParam
         for (int e = 0; e < 8; ++e) st.x[8 * s + e] = buf_elem<float>(rx, xv, (32 * s + e) * sx0);
 }
 
-template <int NP>
+// YT: the single pass run as the three passes without scratch
+// (HelixScanParams::ytile): the start state comes from y (walk_start_state)
+// and the decay preamble is formed here from dt, as Pass A forms its records
+// (softplus, fp64 wave scan), since there are no records.
+template <int NP, bool YT = false>
 __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     static_assert(NP == 64 || NP == 128, "d_state 64 or 128");
     // Staging lanes: 16 per pair of rows; a run of eight state indices per
@@ -183,7 +196,9 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     const int c_end   = min(c_begin + p.walk_len, p.n_cg);
     if (c_begin >= c_end) return;
 
-    const float* __restrict__ rec_h = b.pre + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * 4);
+    const float* __restrict__ rec_h = YT ? nullptr : b.pre + ((long long)seq * p.cpg * p.n_head + h) * (HELIX_CS * 4);
+    const float* __restrict__ dt_h = b.dt + seq * p.seq_dt + h * p.s_dt[1];
+    const float A_h = YT ? b.A[(long long)h * p.s_a] : 0.0f;
     const float* __restrict__ x_h = b.x + seq * p.seq_x + h * p.s_x[1] + p0 * p.s_x[2];
     const float* __restrict__ B_g = b.B + seq * p.seq_b + g * p.s_b[1];
     const float* __restrict__ C_g = b.C + seq * p.seq_c + g * p.s_c[1];
@@ -251,7 +266,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         const int c16 = lane & 15, rr = lane >> 4, j0 = 8 * wave + 2 * rr;
         const int u = NH == 2 ? c16 : (c16 & 7), hf = NH == 2 ? 0 : (c16 >> 3);
         load_runs_x6<NH>(runs, p, B_g, C_g, c_begin, N, j0, u, hf);
-        load_stage_x6(st, p, rec_h, x_h, c_begin, lane, rr, 16 * w4 + c16, pw);
+        load_stage_x6<YT>(st, p, rec_h, dt_h, x_h, c_begin, lane, rr, 16 * w4 + c16, pw);
         stage_c(runs, tlen_of(c_begin), j0, u, hf, wx6_perm32(8 * u));
         split_b(runs, bw);
         load_runs_x6<NH>(runs, p, B_g, C_g, min(c_begin + 1, c_end - 1), N, j0, u, hf);
@@ -262,7 +277,16 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
     f32x4 R[NB];
     {
         const int q = lane >> 4, c16 = lane & 15;
-        walk_start_state<NP>(R, p, b, seq, h, slab, seg, p0, pw, 16 * w4 + c16, q, w4, c16, head_ok);
+        walk_start_state<NP, YT>(R, p, b, seq, h, slab, seg, p0, pw, 16 * w4 + c16, q, w4, c16, head_ok);
+        if constexpr (YT) {
+            // The start state lies in y's rows that this workgroup's waves
+            // overwrite from the first chunk on: every wave has it in
+            // registers before the first barrier, which comes before any y
+            // store.
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                asm volatile("" ::"v"(R[nb][0]), "v"(R[nb][1]), "v"(R[nb][2]), "v"(R[nb][3]));
+        }
     }
 
     __bf16* const sMh = sM + hw * PL_M;
@@ -290,19 +314,36 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         write_bt(bw, j0, u, hf);
 
         // ---- decay records of the two heads --------------------------------
-        if (w4 == 0) {
-            const double lcum = __builtin_bit_cast(double, (unsigned long long)st.rec[2] |
-                                                               ((unsigned long long)st.rec[3] << 32));
-            const double lend = __builtin_bit_cast(
-                double, (unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[2], 63) |
-                            ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[3], 63) << 32));
-            sDt[hw][lane] = as_f32(st.rec[0]);
-            sE[hw][lane] = as_f32(st.rec[1]);
-            sSd[hw][lane] = exp2_diff(lend, lcum);
-            sL[hw][lane] = lcum;
+        float a_c;
+        if constexpr (YT) {
+            // dt (0 past tlen), Lcum in fp64 and its exponentials, as Pass A's
+            // hb_preamble forms the records; every wave of the head forms them
+            // (a_c), the first stores them.
+            const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+            const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+            const double lend = bcast(lcum, 63);
+            if (w4 == 0) {
+                sDt[hw][lane] = dtv;
+                sE[hw][lane] = expf((float)lcum);
+                sSd[hw][lane] = exp2_diff(lend, lcum);
+                sL[hw][lane] = lcum;
+            }
+            a_c = expf((float)lend);
+        } else {
+            if (w4 == 0) {
+                const double lcum = __builtin_bit_cast(double, (unsigned long long)st.rec[2] |
+                                                                   ((unsigned long long)st.rec[3] << 32));
+                const double lend = __builtin_bit_cast(
+                    double, (unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[2], 63) |
+                                ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)st.rec[3], 63) << 32));
+                sDt[hw][lane] = as_f32(st.rec[0]);
+                sE[hw][lane] = as_f32(st.rec[1]);
+                sSd[hw][lane] = exp2_diff(lend, lcum);
+                sL[hw][lane] = lcum;
+            }
+            // exp(L_end) = exp(Lcum) of token 63.
+            a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[1], 63));
         }
-        // exp(L_end) = exp(Lcum) of token 63.
-        const float a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[1], 63));
         __syncthreads();   // (1)
 
         // dt x at (K token j = 32 s + 8 q + e, column pp); G4 scales it by the
@@ -320,7 +361,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         // of the registers they fill, and each staging step after the barrier
         // that frees its LDS: hoisted, they wait on loads still in flight.
         __builtin_amdgcn_sched_barrier(0);
-        load_stage_x6(st, p, rec_h, x_h, cn, lane, q, pp, pw);
+        load_stage_x6<YT>(st, p, rec_h, dt_h, x_h, cn, lane, q, pp, pw);
 
         // ---- G1: D[j][t] = (B C^T) of blocks idx = wave, wave + 8 -----------
         // Block idx: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
@@ -499,5 +540,14 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         scan_walk_x6_impl<NP>(p, b);                                                            \
     }
 
+// The single pass without scratch (HelixScanParams::ytile).
+#define HELIX_PASS_C_WALK_X6_Y(NP)                                                              \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * 2) void helix_scan_walk_x6_y_n##NP(       \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk_x6_impl<NP, true>(p, b);                                                      \
+    }
+
 HELIX_PASS_C_WALK_X6(64)
 HELIX_PASS_C_WALK_X6(128)
+HELIX_PASS_C_WALK_X6_Y(64)
+HELIX_PASS_C_WALK_X6_Y(128)

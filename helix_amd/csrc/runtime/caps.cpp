@@ -74,7 +74,7 @@ struct TraitTable {
     // [io][k]: single pass; [k]: diagonal A; [k]: fp32 path; [k]: the fp32
     // path's walk (d_state <= 128); [io][split6][bccopy][k]: bf16 path (bccopy
     // only with fp32 storage).
-    HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk[2], bf16[3][2][2][3];
+    HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk[2], bf16[3][2][2][3], ysingle[2];
     std::vector<std::string> names;   // every kernel name, deduplicated
     std::deque<std::string> store;    // backing storage of the strings above
 
@@ -106,6 +106,25 @@ struct TraitTable {
                 t.np = kNps[k];
                 t.k_single = kernel(std::string("helix_scan_1pass_") + (io == 0 ? "f32_" : kIoTag[io]) + "n" + np);
                 t.single_threads = 64 * HELIX_1PASS_WAVES(kNps[k]);
+            }
+            if (k < 2) {
+                // The single pass (fp32 storage, scalar A) run as the three
+                // passes with its state tiles in y: Pass A's aggregate kernel
+                // (no records), Pass B, and the fp32 path's walk forming its
+                // own decay preamble.
+                HelixMatmulTraits& t = ysingle[k];
+                t = HelixMatmulTraits{};
+                t.backend = HELIX_BACKEND_SGMMA;
+                t.name = keep("mfma fp32, single pass as three launches, state tiles in y" + upto);
+                t.k_chunk_state = kernel("helix_chunk_state_hb_x6agg_n" + np);
+                t.k_state_scan = kernel("helix_state_scan_y_f32");
+                t.k_chunk_out = kernel("helix_scan_walk_x6_y_n" + np);
+                t.mfma_a = "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)";
+                t.mfma_c = "v_mfma_f32_16x16x32_bf16 (bf16x6 split operands)";
+                t.np = kNps[k];
+                t.walk = true;
+                t.walk_hpw = 2;
+                t.a_hb = true;
             }
             if (k < 2) {
                 HelixMatmulTraits& t = diag[k];
@@ -248,6 +267,8 @@ helix_tuning tuning_from_env() {
     t.hblk = (int)env_long("HELIX_HBLK", 0);
     const int fw = env_switch("HELIX_F32_WALK");
     if (fw >= 0) t.f32_walk = fw > 0 ? 1 : 0;
+    const int yt = env_switch("HELIX_1PASS_Y");
+    if (yt >= 0) t.ytile = yt > 0 ? 1 : 0;
     return t;
 }
 
@@ -552,6 +573,56 @@ MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, con
     want_blocks = std::min<long>(want_blocks, hpg);
     pl.hblk = (int)((hpg + want_blocks - 1) / want_blocks);
     pl.n_hblk = (hpg + pl.hblk - 1) / pl.hblk;
+    return pl;
+}
+
+MultipassPlan plan_ytile(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& single,
+                         const HelixMatmulTraits** tr_out) {
+    MultipassPlan pl;
+    *tr_out = nullptr;
+    const helix_tuning& tu = tuning_of(ctx);
+    if (tu.ytile == 0 || !single.k_single || d.a_form != HELIX_A_SCALAR_PER_HEAD || d.io_dtype != HELIX_F32 ||
+        d.d_state > 128 || d.n_tok <= 0 || d.n_seq <= 0 || d.n_head <= 0 || d.head_dim <= 0 || d.n_group <= 0)
+        return pl;
+    // y's rows hold 16-byte tile units: channel stride 1, the others multiples
+    // of four elements (the encoder also checks y's base).
+    if (d.s_y[2] != 1 || (d.s_y[0] | d.s_y[1] | d.seq_y) % 4 != 0) return pl;
+    const HelixMatmulTraits& tr = table().ysingle[np_index(d.d_state)];
+    const long n_chunks = (d.n_tok + HELIX_CS - 1) / HELIX_CS;
+    // Every segment must have the rows its tile and log-decay take, at the
+    // narrowest slab width; the last segment is the shortest.
+    const int n_pslab = (d.head_dim + HELIX_HD - 1) / HELIX_HD;
+    const int pw_min = std::min(HELIX_HD, d.head_dim - (n_pslab - 1) * HELIX_HD);
+    const long upr = pw_min / 4;
+    const long rows = (16L * tr.np + 1 + upr - 1) / upr;
+    auto fits = [&](long sl) {
+        const long n_seg = (n_chunks + sl - 1) / sl;
+        return d.n_tok - (n_seg - 1) * sl * HELIX_CS >= rows;
+    };
+    if (d.n_tok < rows || rows * d.s_y[0] * 4 >= (1LL << 31)) return pl;
+    layout(tu, d, tr, (int)n_chunks, &pl);
+    if (!fits(pl.seg_len)) {
+        // Longer segments (the walk keeps its number of segments): the
+        // shortest that gives every segment its rows. The whole sequence as
+        // one segment always does, since n_tok >= rows.
+        const int ratio = std::max(1, pl.walk_len / std::max(1, pl.seg_len));
+        helix_tuning t2 = tu;
+        for (long sl = std::max<long>(pl.seg_len + 1, (rows + HELIX_CS - 1) / HELIX_CS); sl <= n_chunks; ++sl) {
+            if (!fits(sl)) continue;
+            t2.seg_len = (int)sl;
+            t2.walk_len = (int)std::min<long>(sl * ratio, n_chunks);
+            break;
+        }
+        if (t2.seg_len <= 0) return pl = MultipassPlan{}, pl;
+        layout(t2, d, tr, (int)n_chunks, &pl);
+        if (!fits(pl.seg_len)) return pl = MultipassPlan{}, pl;
+    }
+    pl.n_chunks = (int)n_chunks;
+    pl.n_groups = 1;
+    pl.total_bytes = 0;   // nothing outside y
+    pl.hblk = 1;
+    pl.n_hblk = d.n_head / d.n_group;
+    *tr_out = &tr;
     return pl;
 }
 

@@ -27,6 +27,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 
 #include "helix/helix_host.h"
@@ -38,6 +39,46 @@ using helix::rt::set_error;
 
 inline void* dptr(helix_tensor t) {
     return t.buf ? static_cast<char*>(t.buf) + t.offset : nullptr;
+}
+
+// Byte range [lo, hi) of a tensor of n_seq sequences with the given
+// per-sequence stride and (extent, stride) dimensions, element size es
+// (strides are non-negative: the descriptor gate checks them).
+struct ByteRange {
+    uintptr_t lo = 0, hi = 0;
+    bool overlaps(const ByteRange& o) const { return lo < o.hi && o.lo < hi; }
+};
+ByteRange byte_range(const void* base, long long n_seq, long long seq_stride,
+                     std::initializer_list<std::pair<long long, long long>> dims, size_t es) {
+    long long last = (n_seq - 1) * seq_stride;
+    for (const auto& [n, st] : dims) last += (n - 1) * st;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(base);
+    return {lo, lo + (uintptr_t)(last + 1) * es};
+}
+
+// Whether y shares a byte with anything the single pass without scratch reads
+// or writes besides y once its first launch has written state tiles into y:
+// x, dt, A, B, C, s1, ids, and s0 (its rows 0 .. n_seq - 1 without ids; with
+// ids the rows read are not known to the host and s0 is left out).
+bool y_overlaps_others(const helix_scan_desc& d, const void* y, const void* x, const void* dt, const void* A,
+                       const void* B, const void* C, const void* s0, const void* ids, const void* s1) {
+    const long long T = d.n_tok, S = d.n_seq;
+    const ByteRange ry = byte_range(y, S, d.seq_y, {{T, d.s_y[0]}, {d.n_head, d.s_y[1]}, {d.head_dim, d.s_y[2]}}, 4);
+    auto state = [&](const void* p) {
+        return byte_range(p, S, d.seq_s, {{d.n_head, d.s_s[0]}, {d.head_dim, d.s_s[1]}, {d.d_state, d.s_s[2]}}, 4);
+    };
+    const ByteRange others[] = {
+        byte_range(x, S, d.seq_x, {{T, d.s_x[0]}, {d.n_head, d.s_x[1]}, {d.head_dim, d.s_x[2]}}, 4),
+        byte_range(dt, S, d.seq_dt, {{T, d.s_dt[0]}, {d.n_head, d.s_dt[1]}}, 4),
+        byte_range(A, 1, 0, {{d.n_head, d.s_a}}, 4),
+        byte_range(B, S, d.seq_b, {{T, d.s_b[0]}, {d.n_group, d.s_b[1]}, {d.d_state, d.s_b[2]}}, 4),
+        byte_range(C, S, d.seq_c, {{T, d.s_c[0]}, {d.n_group, d.s_c[1]}, {d.d_state, d.s_c[2]}}, 4),
+        state(s1),
+        ids ? byte_range(ids, S, 1, {}, 4) : state(s0),
+    };
+    for (const ByteRange& r : others)
+        if (ry.overlaps(r)) return true;
+    return false;
 }
 
 // scratch_sized: the scratch is the library's own fixed array, already known
@@ -80,17 +121,30 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_ERR_INVALID_ARG;
     }
 
-    const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    const HelixMatmulTraits* trp = &helix::rt::select_traits(ctx, *d);
     auto fn = [&](const char* name) -> hipFunction_t {
         if (!name) return nullptr;
         auto it = ctx->kernels.find(name);
         return it == ctx->kernels.end() ? nullptr : it->second;
     };
 
-    // Single pass (reference dispatch.mm:122-138): one launch, one workgroup
-    // per (seq, head, 16-channel block of a P slab), the state carried in
-    // registers; no scratch.
-    // Diagonal A always takes this path.
+    // Single pass (reference dispatch.mm:122-138): no scratch. With fp32
+    // storage, scalar A and d_state <= 128 it runs as the fp32 path's three
+    // passes with their state tiles in y (plan_ytile; below), where y allows
+    // it. Otherwise one launch, one workgroup per (seq, head, 16-channel block
+    // of a P slab), the state carried in registers. Diagonal A always takes
+    // the one-launch path.
+    helix::rt::MultipassPlan yplan;
+    bool ytile = false;
+    if (trp->k_single) {
+        const HelixMatmulTraits* ytr = nullptr;
+        yplan = helix::rt::plan_ytile(ctx, *d, *trp, &ytr);
+        ytile = ytr && (reinterpret_cast<uintptr_t>(dptr(y)) & 15) == 0 &&
+                !y_overlaps_others(*d, dptr(y), dptr(x), dptr(dt), dptr(A), dptr(B), dptr(C), dptr(s0), dptr(ids),
+                                   dptr(s1));
+        if (ytile) trp = ytr;
+    }
+    const HelixMatmulTraits& tr = *trp;
     if (tr.k_single) {
         hipFunction_t f1 = fn(tr.k_single);
         if (!f1) {
@@ -133,7 +187,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_OK;
     }
 
-    const helix::rt::MultipassPlan plan = helix::rt::plan_multipass(ctx, *d, tr, budget_cap);
+    const helix::rt::MultipassPlan plan = ytile ? yplan : helix::rt::plan_multipass(ctx, *d, tr, budget_cap);
     if (plan.n_chunks <= 0) {
         set_error(ctx, "empty problem");
         return HELIX_ERR_INVALID_ARG;
@@ -183,6 +237,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     // itself: no Pass B launch.
     const bool fuse_b = helix::rt::fuse_b_on(ctx, tr, plan);
     params.fuse_b  = fuse_b ? 1 : 0;
+    params.ytile   = ytile ? 1 : 0;
 
     HelixScanBuffers bufs;
     std::memset(&bufs, 0, sizeof(bufs));
@@ -195,14 +250,16 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     bufs.ids = static_cast<const int*>(dptr(ids));
     bufs.y   = static_cast<float*>(dptr(y));
     bufs.s1  = static_cast<float*>(dptr(s1));
-    char* sc = static_cast<char*>(dptr(scratch));
-    bufs.s_local = plan.sl_elems ? sc + plan.off_sl : nullptr;
-    bufs.s_seg   = reinterpret_cast<float*>(sc + plan.off_sg);
-    bufs.ld      = reinterpret_cast<float*>(sc + plan.off_ld);
-    bufs.segld   = reinterpret_cast<float*>(sc + plan.off_sd);
-    bufs.bcopy   = plan.bc_elems ? sc + plan.off_bc : nullptr;
-    bufs.ccopy   = plan.bc_elems ? sc + plan.off_cc : nullptr;
-    bufs.pre     = plan.rec_elems ? reinterpret_cast<float*>(sc + plan.off_rec) : nullptr;
+    if (!ytile) {   // ytile: no scratch; the kernels keep their tiles in y
+        char* sc = static_cast<char*>(dptr(scratch));
+        bufs.s_local = plan.sl_elems ? sc + plan.off_sl : nullptr;
+        bufs.s_seg   = reinterpret_cast<float*>(sc + plan.off_sg);
+        bufs.ld      = reinterpret_cast<float*>(sc + plan.off_ld);
+        bufs.segld   = reinterpret_cast<float*>(sc + plan.off_sd);
+        bufs.bcopy   = plan.bc_elems ? sc + plan.off_bc : nullptr;
+        bufs.ccopy   = plan.bc_elems ? sc + plan.off_cc : nullptr;
+        bufs.pre     = plan.rec_elems ? reinterpret_cast<float*>(sc + plan.off_rec) : nullptr;
+    }
 
     // Launch sizes of the largest group, checked in 64 bits before anything is
     // enqueued: the kernels decode their 1-D Pass C grid as a 32-bit count.
@@ -380,7 +437,10 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     std::memset(out, 0, sizeof(*out));
-    if (tr.k_single) {
+    const HelixMatmulTraits* ytr = nullptr;
+    const helix::rt::MultipassPlan yplan =
+        tr.k_single ? helix::rt::plan_ytile(ctx, *d, tr, &ytr) : helix::rt::MultipassPlan{};
+    if (tr.k_single && !ytr) {
         out->n_chunks = (d->n_tok + HELIX_CS - 1) / HELIX_CS;
         out->chunks_per_group = out->n_chunks;
         out->n_groups = 1;
@@ -395,7 +455,14 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->kernel_1pass = tr.k_single;
         return HELIX_OK;
     }
-    const helix::rt::MultipassPlan pl = helix::rt::plan_multipass(ctx, *d, tr);
+    // The single pass with its state tiles in y: the fp32 path's passes, no
+    // scratch (the one-launch kernel stays named as the encoder's fallback).
+    if (ytr) {
+        out->state_in_y = 1;
+        out->kernel_1pass = tr.k_single;
+    }
+    const HelixMatmulTraits& tp = ytr ? *ytr : tr;
+    const helix::rt::MultipassPlan pl = ytr ? yplan : helix::rt::plan_multipass(ctx, *d, tr);
     out->n_chunks = pl.n_chunks;
     out->chunks_per_group = pl.chunks_per_group;
     out->n_groups = pl.n_groups;
@@ -405,18 +472,20 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->walks_per_group = pl.walks_per_group;
     out->hblk = pl.hblk;
     out->n_hblk = pl.n_hblk;
-    out->bf16_state = tr.bf16_state ? 1 : 0;
+    out->bf16_state = tp.bf16_state ? 1 : 0;
     out->total_bytes = pl.total_bytes;
-    out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
-    out->s_seg_bytes = pl.sg_elems * sizeof(float);
-    out->bccopy_bytes = pl.bc_elems * 2 * 2;
-    out->rec_bytes = pl.rec_elems * sizeof(float);
-    const bool fuse_b = helix::rt::fuse_b_on(ctx, tr, pl);   // as helix_scan_encode decides
+    if (!ytr) {   // state_in_y: every region lies in y
+        out->s_local_bytes = pl.sl_elems * pl.sl_elem_bytes;
+        out->s_seg_bytes = pl.sg_elems * sizeof(float);
+        out->bccopy_bytes = pl.bc_elems * 2 * 2;
+        out->rec_bytes = pl.rec_elems * sizeof(float);
+    }
+    const bool fuse_b = helix::rt::fuse_b_on(ctx, tp, pl);   // as helix_scan_encode decides
     out->launches = fuse_b ? 2 : 3 * pl.n_groups;
-    out->np = tr.np;
-    out->kernel_a = tr.k_chunk_state;
-    out->kernel_b = fuse_b ? nullptr : tr.k_state_scan;
-    out->kernel_c = tr.k_chunk_out;
+    out->np = tp.np;
+    out->kernel_a = tp.k_chunk_state;
+    out->kernel_b = fuse_b ? nullptr : tp.k_state_scan;
+    out->kernel_c = tp.k_chunk_out;
     out->pass_b = fuse_b ? HELIX_PASS_B_IN_C : HELIX_PASS_B_LAUNCHED;
     return HELIX_OK;
 }

@@ -32,6 +32,7 @@ struct helix_tuning {
     int  hblk        = 0;      // HELIX_HBLK: heads per chunk-parallel Pass C workgroup
     int  f32_walk    = -1;     // HELIX_F32_WALK=0 / 1: the fp32 path's chunk-parallel Pass C / walk
                                // (on per-chunk states stored by Pass A) at d_state 128
+    int  ytile       = -1;     // HELIX_1PASS_Y=0: the single pass in its one-launch form only
 };
 
 struct helix_ctx {
@@ -137,6 +138,16 @@ MultipassPlan plan_multipass(const helix_ctx* ctx, const helix_scan_desc& d, con
 // the tuning's fuse_b (HELIX_FUSE_B=0 / 1) turns it off / on for any
 // single-group plan.
 bool fuse_b_on(const helix_ctx* ctx, const HelixMatmulTraits& tr, const MultipassPlan& plan);
+
+// The single pass (multipass = false, fp32 storage, scalar A, d_state <= 128)
+// run as the three passes of the fp32 path with no scratch: the state tiles
+// and segment log-decays live in y (HelixScanParams::ytile), one group, Pass B
+// launched. Returns the plan and sets *tr_out to its traits, or returns an
+// empty plan (n_chunks 0) where the shape does not allow it: y's strides, a
+// last segment too short for a tile, or HELIX_1PASS_Y=0. The encoder also
+// needs y 16-byte aligned and overlapping no input.
+MultipassPlan plan_ytile(const helix_ctx* ctx, const helix_scan_desc& d, const HelixMatmulTraits& single,
+                         const HelixMatmulTraits** tr_out);
 
 
 // Fills the kernel-side params from the public descriptor. Returns false and

@@ -21,8 +21,9 @@ extern "C" {
 helix_status helix_ctx_create_host(helix_ctx** out);
 
 /* The plan helix_scan_encode would use for `d`. With multipass = false, or a
- * diagonal A, it is one launch of kernel_1pass: one group, no scratch,
- * kernel_a/b/c NULL. */
+ * diagonal A, it needs no scratch: one launch of kernel_1pass (one group,
+ * kernel_a/b/c NULL), or, where state_in_y is 1, the three passes with their
+ * state tiles in y. */
 typedef struct {
     int32_t  n_chunks;          /* ceil(n_tok / 64)                              */
     int32_t  chunks_per_group;  /* chunks per super-chunk group (scratch bound)  */
@@ -49,6 +50,13 @@ typedef struct {
     int32_t  pass_b;            /* where Pass B's segment scan runs: one of
                                    HELIX_PASS_B_* (kernel_b is NULL unless it
                                    has a launch of its own)                      */
+    int32_t  state_in_y;        /* 1: the single pass runs as kernel_a, kernel_b
+                                   and kernel_c with their state tiles in y, no
+                                   scratch (fp32 storage, scalar A, d_state
+                                   <= 128, and a last segment long enough for a
+                                   tile); helix_scan_encode runs kernel_1pass
+                                   alone instead when y is not 16-byte aligned
+                                   or overlaps x, dt, A, B, C, s0, ids or s1    */
 } helix_plan_info;
 
 #define HELIX_PASS_B_LAUNCHED 0   /* kernel_b, between Pass A and Pass C         */

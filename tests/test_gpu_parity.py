@@ -66,6 +66,10 @@ MODES = [
     # (label, backend, scratch_mb, memory, extra environment, multipass)
     ("1pass", HELIX_BACKEND_AUTO, None, "short", {}, False),
     ("1pass/long", HELIX_BACKEND_AUTO, None, "long", {}, False),
+    # The single pass in its one-launch form everywhere (by default the
+    # shapes with rows for a state tile run the three passes with the tiles
+    # in y, test_gpu_single_y.py).
+    ("1pass/1launch/long", HELIX_BACKEND_AUTO, None, "long", {"HELIX_1PASS_Y": "0"}, False),
     ("fp32", HELIX_BACKEND_SGMMA, None, "short", {}, True),
     ("fp32/sm", HELIX_BACKEND_SGMMA, 1, "short", {}, True),
     ("fp32/long", HELIX_BACKEND_SGMMA, None, "long", {}, True),

@@ -404,13 +404,38 @@ def test_backend_selection(host):
     assert host.backend_desc(d) == "mfma fp32, single pass (d_state<=128)"
     d.backend = HELIX_BACKEND_MPP
     assert host.backend_desc(d) == "declined (shape unsupported)"
-    for n, want in ((64, 64), (40, 64), (96, 128), (256, 256)):
+    # With fp32 storage, scalar A and d_state <= 128 the single pass runs as
+    # the fp32 path's three passes with their state tiles in y (state_in_y),
+    # where every segment has the rows of a tile: 65 rows at d_state 64 and a
+    # 64-channel slab, 129 at 128. 100 tokens leave only d_state 64 there; the
+    # one-launch kernel stays named as the encoder's fallback.
+    for n, want, in_y in ((64, 64, 1), (40, 64, 1), (96, 128, 0), (256, 256, 0)):
         d = mp((100, 1, 2, 64, n, 1))
         d.multipass = False
         k = host.plan_info(d)
-        assert (k.np, k.launches, k.total_bytes, k.n_groups) == (want, 1, 0, 1)
+        assert (k.np, k.launches, k.total_bytes, k.n_groups, k.state_in_y) == (want, 3 if in_y else 1, 0, 1, in_y)
         assert k.kernel_1pass == b"helix_scan_1pass_f32_n%d" % want
-        assert k.kernel_a is None and k.kernel_b is None and k.kernel_c is None
+        if in_y:
+            assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
+                b"helix_chunk_state_hb_x6agg_n64", b"helix_state_scan_y_f32", b"helix_scan_walk_x6_y_n64")
+            assert k.s_seg_bytes == k.rec_bytes == 0
+        else:
+            assert k.kernel_a is None and k.kernel_b is None and k.kernel_c is None
+    # Config 2: Pass A's 8-chunk segments, 16-chunk walks, as the fp32 path;
+    # HELIX_1PASS_Y=0 keeps the one-launch kernel.
+    d = mp(CONFIG_SHAPES["cfg2"])
+    d.multipass = False
+    k = host.plan_info(d)
+    assert (k.state_in_y, k.launches, k.seg_len, k.walk_len, k.total_bytes) == (1, 3, 8, 16, 0)
+    k0 = tuned(HELIX_1PASS_Y="0").plan_info(d)
+    assert (k0.state_in_y, k0.launches, k0.kernel_a) == (0, 1, None)
+    # Config 1: the planner's 2-chunk segments are shorter than a tile's 129
+    # rows, and 3-chunk ones leave a last segment of 128 tokens; the segments
+    # grow to 4 chunks and the walks keep two of them.
+    d = mp(CONFIG_SHAPES["cfg1"])
+    d.multipass = False
+    k = host.plan_info(d)
+    assert (k.state_in_y, k.seg_len, k.walk_len) == (1, 4, 8)
     assert host.plan_info(mp(shape)).kernel_1pass is None
     assert tuned(HELIX_FORCE_BACKEND="sgmma").select_backend(mp(shape, HELIX_BACKEND_MPP)) == HELIX_BACKEND_SGMMA
 
