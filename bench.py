@@ -503,7 +503,12 @@ def main():
                 Variant("fp32", ctx, HELIX_BACKEND_SGMMA, tensors)]
     if args.variants:
         # Alternative kernel choices, timed interleaved in the same process.
+        # The single pass (multipass = false, the descriptor default): by
+        # default the fp32 path's passes with their state tiles in y; and its
+        # one-launch kernel (what it falls back to when y overlaps an input).
         variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
+        variants.append(Variant("single-pass-1launch", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False,
+                                env={"HELIX_1PASS_Y": "0"}))
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
         variants.append(Variant("bf16-passA-x3-optin", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_PASSA_SPLIT": "3"}))
