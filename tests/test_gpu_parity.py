@@ -286,3 +286,28 @@ def test_pass_b_placement(gpu, name, path, extra, where, multi):
     rel, ab = (BF16_REL, BF16_ABS) if is_bf16 else (F32_REL, F32_ABS)
     assert po.allclose_ratio(y, y_ref, rel, ab) <= 1.0
     assert po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS) <= 1.0
+
+
+# ---------------------------------------------------------------------------
+# A walk length the dispatch model picks (caps.cpp fused_walk_len) on a
+# batched shape with two B/C groups: 25-chunk walks, 25 + 7 chunks per
+# sequence, Pass B in the walk's prologue, on both paths. Harness inputs in
+# LONG memory, every head against the oracle.
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", ["bf16", "fp32"])
+def test_model_walk_length(gpu, path):
+    from helix_amd.abi import PASS_B_IN_C
+    p = po.problem_harness(2048, 8, 96, 64, 128, 2, 4848, "long")
+    y_ref, s_ref = po.scan(p, threads=0)
+    d = p.d.copy()
+    d.multipass = True
+    d.backend = HELIX_BACKEND_MPP if path == "bf16" else HELIX_BACKEND_SGMMA
+    info = gpu.plan_info(d)
+    assert (info.n_groups, info.seg_len, info.walk_len, info.segs_per_group, info.pass_b) == (1, 25, 25, 2, PASS_B_IN_C)
+    _, y, s1 = run(gpu, p, desc=d)
+    is_bf16 = path == "bf16"
+    rel, ab = (BF16_REL, BF16_ABS) if is_bf16 else (F32_REL, F32_ABS)
+    ry, rs = po.allclose_ratio(y, y_ref, rel, ab), po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS)
+    print(f"[model walk {path}] y ratio {ry:.3f}  s1 ratio {rs:.3f}", flush=True)
+    assert ry <= 1.0 and rs <= 1.0
