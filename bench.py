@@ -446,8 +446,9 @@ def main():
     ap.add_argument("--warmup-ms", type=float, default=800.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--variants", action="store_true",
-                    help="also time alternative kernel choices (reported under 'variants')")
+    ap.add_argument("--variants", nargs="?", const="all", default=None, metavar="NAMES",
+                    help="also time alternative kernel choices (reported under 'variants'); "
+                         "a comma list names which (default: all)")
     ap.add_argument("--config-steps", type=int, default=20,
                     help="event-timed encodes per config and path in the per-config report "
                          "(0 skips the report)")
@@ -499,14 +500,19 @@ def main():
     del _arena
     tensors = make_inputs(1002, dev)
     stream = torch.cuda.current_stream(dev)
+    # The headline (bf16 path), the fp32 path, and the single pass
+    # (multipass = false, the descriptor default: by default the fp32 path's
+    # passes with their state tiles in y, no scratch).
     variants = [Variant("bf16", ctx, HELIX_BACKEND_MPP, tensors),
-                Variant("fp32", ctx, HELIX_BACKEND_SGMMA, tensors)]
+                Variant("fp32", ctx, HELIX_BACKEND_SGMMA, tensors),
+                Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False)]
     if args.variants:
-        # Alternative kernel choices, timed interleaved in the same process.
-        # The single pass (multipass = false, the descriptor default): by
-        # default the fp32 path's passes with their state tiles in y; and its
-        # one-launch kernel (what it falls back to when y overlaps an input).
-        variants.append(Variant("single-pass", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False))
+        # Alternative kernel choices, timed interleaved in the same process
+        # (--variants alone: all of them; --variants a,b: those named).
+        wanted = None if args.variants == "all" else set(args.variants.split(","))
+        n0 = len(variants)
+        # The single pass's one-launch kernel (what it falls back to when y
+        # overlaps an input).
         variants.append(Variant("single-pass-1launch", ctx, HELIX_BACKEND_AUTO, tensors, multipass=False,
                                 env={"HELIX_1PASS_Y": "0"}))
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
@@ -520,6 +526,12 @@ def main():
         variants.append(Variant("fp32-dstate64-walk", ctx, HELIX_BACKEND_SGMMA, t64))
         variants.append(Variant("fp32-dstate64-chunk", ctx, HELIX_BACKEND_SGMMA, t64,
                                 env={"HELIX_F32_WALK": "0"}))
+        if wanted is not None:
+            unknown = wanted - {v.name for v in variants[n0:]}
+            if unknown:
+                print(f"bench.py: unknown variant(s) {sorted(unknown)}", file=sys.stderr)
+                sys.exit(2)
+            variants = variants[:n0] + [v for v in variants[n0:] if v.name in wanted]
 
     def warm_up(v, ms):
         """W steps, then more until the wall clock has run `ms` (the
@@ -653,7 +665,18 @@ def main():
             "kernel": results["fp32"]["kernel"],
         },
     }
-    extra = [v for v in variants if v.name not in ("bf16", "fp32")]
+    sp = results["single-pass"]
+    out["single_pass"] = {
+        "tok_s": S * L / (sp["ms"] * 1e-3),
+        "gflops": F / (sp["ms"] * 1e-3) / 1e9,
+        "ms_per_step": sp["ms"],
+        "form": ("three launches, state tiles in y (no scratch)" if sp["plan"].state_in_y
+                 else "one launch (no scratch)"),
+        "kernels": ([k.decode() for k in (sp["plan"].kernel_a, sp["plan"].kernel_b, sp["plan"].kernel_c)]
+                    if sp["plan"].state_in_y else [sp["plan"].kernel_1pass.decode()]),
+        "kernel": sp["kernel"],
+    }
+    extra = [v for v in variants if v.name not in ("bf16", "fp32", "single-pass")]
     if extra:
         out["variants"] = {}
         for v in extra:
