@@ -314,21 +314,22 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         write_bt(bw, j0, u, hf);
 
         // ---- decay records of the two heads --------------------------------
-        float a_c;
+        float a_c = 0.0f;
         if constexpr (YT) {
             // dt (0 past tlen), Lcum in fp64 and its exponentials, as Pass A's
-            // hb_preamble forms the records; every wave of the head forms them
-            // (a_c), the first stores them.
-            const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
-            const double lcum = wave_incl_sum((double)A_h * (double)dtv);
-            const double lend = bcast(lcum, 63);
-            if (w4 == 0) {
+            // hb_preamble forms the records, by one wave of each head: wave
+            // w4 == hw, so the two heads' preambles run on different SIMDs.
+            // The others read exp(L_end) (token 63's exp(Lcum)) from sE after
+            // the barrier below.
+            if (w4 == hw) {
+                const float dtv = keep_if_lt(helix_dt(p, st.dtraw), lane, tlen);
+                const double lcum = wave_incl_sum((double)A_h * (double)dtv);
+                const double lend = bcast(lcum, 63);
                 sDt[hw][lane] = dtv;
                 sE[hw][lane] = expf((float)lcum);
                 sSd[hw][lane] = exp2_diff(lend, lcum);
                 sL[hw][lane] = lcum;
             }
-            a_c = expf((float)lend);
         } else {
             if (w4 == 0) {
                 const double lcum = __builtin_bit_cast(double, (unsigned long long)st.rec[2] |
@@ -345,6 +346,7 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
             a_c = __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)st.rec[1], 63));
         }
         __syncthreads();   // (1)
+        if constexpr (YT) a_c = sE[hw][HELIX_CS - 1];
 
         // dt x at (K token j = 32 s + 8 q + e, column pp); G4 scales it by the
         // decay when it needs it.
