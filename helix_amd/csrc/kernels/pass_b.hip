@@ -60,15 +60,18 @@ __device__ __forceinline__ void state_scan_impl(const HelixScanParams& p, const 
     const long long seg_stride = p.sg_seg / 4;           // in units
     const float* __restrict__ sd = YT ? nullptr : b.segld + seq * p.sd_seq + h;
     const int ratio = p.walk_len / p.seg_len;            // segments per walk
-    // YT: unit q of the slab's tile of segment s, and its log-decay, in y.
+    // YT: unit q of the slab's tile of segment s, and its log-decay, in y:
+    // segment 0's addresses plus s segments of rows.
     const int pws = min(HELIX_HD, p.head_dim - slab * HELIX_HD);
-    const long long yq = ytile_unit(p, q, pws);
+    float* const yd0 = YT ? b.y + ytile_base(p, seq, h, slab, 0) + ytile_unit(p, q, pws) : nullptr;
+    const float* const ya0 = YT ? b.y + ytile_segld(p, seq, h, 0) : nullptr;
+    const long long yseg = (long long)p.seg_len * HELIX_CS * p.s_y[0];   // floats per segment of rows
     auto d_ptr = [&](long long s) -> f32x4* {
-        if constexpr (YT) return reinterpret_cast<f32x4*>(b.y + ytile_base(p, seq, h, slab, (int)s) + yq);
+        if constexpr (YT) return reinterpret_cast<f32x4*>(yd0 + s * yseg);
         else return base + s * seg_stride;
     };
     auto a_ptr = [&](long long s) -> const float* {
-        if constexpr (YT) return b.y + ytile_segld(p, seq, h, (int)s);
+        if constexpr (YT) return ya0 + s * yseg;
         else return sd + s * p.n_head;
     };
 
