@@ -435,6 +435,14 @@ double fused_lengths_us(const helix_scan_desc& d, const HelixMatmulTraits& tr, i
 // those of at most kFuseBMaxSegs walks, from `shortest` up. Memoized: the
 // plan is remade on every encode.
 int fused_walk_len(const helix_scan_desc& d, const HelixMatmulTraits& tr, int cpg, int shortest) {
+    // Past 64 rounds of one-workgroup-per-CU walks, how the last round falls
+    // is a small part of the time, and pricing every length would make the
+    // first plan of a large batch slow: keep the default length.
+    const long hpg = d.n_head / d.n_group;
+    const long hpw = tr.walk_hpw ? tr.walk_hpw : HELIX_WALK_HPW(tr.np);
+    const long walk_wg = (long)d.n_seq * d.n_group * ((hpg + hpw - 1) / hpw) *
+                         ((d.head_dim + HELIX_HD - 1) / HELIX_HD) * ((cpg + shortest - 1) / shortest);
+    if (walk_wg > 64L * kXcds * kEnginesPerXcd * kCusPerEngine) return shortest;
     using Key = std::tuple<int, int, int, int, int, int, int, int>;
     static std::mutex mu;
     static std::map<Key, int> memo;
