@@ -504,12 +504,15 @@ HELIX_DEV float io_widen(typename IoWord<IO>::type w) {
     else
         return io_f32<IO>((unsigned short)w);
 }
-// Cache policy of a buffer access (the instruction's aux operand): 0 is the
-// default; HELIX_NT marks it non-temporal. y is written once and never read
-// back by the scan: storing it non-temporal keeps it from displacing the
-// inputs still being read, which measured 15-25% faster on the walking
-// Pass C at config 2.
-#define HELIX_NT 2
+// Cache policy of a buffer access (the instruction's aux operand, gfx950 bits:
+// 1 sc0, 2 nt, 16 sc1): 0 is the default. y is written once and never read
+// back by the scan, so its stores carry HELIX_NT = nt | sc1: non-temporal,
+// which keeps y from displacing the inputs still being read (15-25% faster
+// than the default on the walking Pass C at config 2), at device scope, which
+// measured a further 5% on the walks (bf16 61.1 -> 58.3 us, fp32 155.5 ->
+// 147.9 us at config 2). sc1 without nt, or with sc0, measured slower than
+// the default; the same bits on loads or on the scratch stores gave nothing.
+#define HELIX_NT 18
 template <typename IO, int AUX = 0>
 HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
     if constexpr (sizeof(IO) == 4) {
