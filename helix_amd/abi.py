@@ -58,6 +58,7 @@ class HelixPlanInfo(ctypes.Structure):
         ("walks_per_group", c_int32),
         ("pass_b", c_int32),
         ("state_in_y", c_int32),
+        ("state_blocks", c_int32),
     ]
 
 

@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "helix_params.h"
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -522,6 +524,25 @@ HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, h), r, voff_bytes, soff_bytes,
                                               AUX);
     }
+}
+// One element of y at (voff, soff) of resource r: stored with HELIX_NT, or,
+// with ACC (HelixScanParams::y_acc: fp32 storage, the second and later blocks
+// of state indices of a d_state above HELIX_N_MAX), added to the value y
+// holds first. Callers test y_acc once around a run of stores
+// (with_y_acc), so the common path has no branch per store.
+template <typename IO, bool ACC>
+HELIX_DEV void y_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
+    if constexpr (ACC && sizeof(IO) == 4)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff_bytes, soff_bytes, 0));
+    io_store<IO, HELIX_NT>(r, v, voff_bytes, soff_bytes);
+}
+// f(std::bool_constant<p.y_acc>{}).
+template <typename F>
+HELIX_DEV void with_y_acc(const HelixScanParams& p, F&& f) {
+    if (p.y_acc)
+        f(std::true_type{});
+    else
+        f(std::false_type{});
 }
 // Eight consecutive elements starting at byte offset voff, widened to fp32:
 // two 16-byte loads for fp32, one for 16-bit storage.

@@ -57,8 +57,12 @@
 #define HELIX_CS 64
 /* Head-dim slab width handled by one workgroup. */
 #define HELIX_HD 64
-/* Largest d_state served (padded up to 64 / 128 / 256 inside the kernels). */
+/* Largest d_state one kernel launch serves (padded up to 64 / 128 / 256
+ * inside the kernels). The host runs a larger d_state as blocks of state
+ * indices, at most HELIX_N_BLOCK each, adding each block's share of y into y
+ * (HelixScanParams::y_acc). */
 #define HELIX_N_MAX 256
+#define HELIX_N_BLOCK 128
 /* Threads per workgroup: four wave64s, one per SIMD of a CU. */
 #define HELIX_WG 256
 /* Bytes of one token's decay record (HelixScanBuffers::pre): the walking bf16
@@ -128,6 +132,9 @@ typedef struct HelixScanParams {
                              A's aggregates, then the walks' start states) and the
                              segment log-decays live in y (ytile_* in
                              helix_common.h); single group, Pass B launched */
+    int y_acc;            /* 1 => y += this launch's result (a block of state
+                             indices after the first: y is the sum over the
+                             blocks of C_n h_n); 0 => y = result */
 
     /* Scratch strides in elements (see the layout comment above). */
     long long sl_cg, sl_seq;     /* s_local: chunk stride (H*n_pslab*64*np), seq stride */

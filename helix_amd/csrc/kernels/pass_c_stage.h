@@ -118,14 +118,17 @@ __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanP
                                     bytes);
     const int pp = pb * 32 + lo;
     const int voff = (4 * hi * sy0 + pp * sy2) * ES;
+    with_y_acc(p, [&](auto acc_on) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int t = tb * 32 + acc_row(r, hi);
-        // The element goes through a float value: a bit cast applied to a
-        // vector element in place reads element 0 with this compiler.
-        const float v = acc[r];
-        io_store<IO, HELIX_NT>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * ES);
-    }
+        for (int r = 0; r < 16; ++r) {
+            const int t = tb * 32 + acc_row(r, hi);
+            // The element goes through a float value: a bit cast applied to a
+            // vector element in place reads element 0 with this compiler.
+            const float v = acc[r];
+            y_store<IO, decltype(acc_on)::value>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw),
+                                                 (tb * 32 + 8 * (r >> 2) + (r & 3)) * sy0 * ES);
+        }
+    });
 }
 
 // Store a walking wave's y tile of one chunk (16 x 16 MFMA layout, lane
@@ -143,14 +146,17 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
                                         (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                     bytes);
     const int voff = (4 * q * sy0 + pp * sy2) * ES;
+    with_y_acc(p, [&](auto acc_on) {
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
+        for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = 16 * tb + 4 * q + r;
-            const float v = acc[tb][r];
-            io_store<IO, HELIX_NT>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw), (16 * tb + r) * sy0 * ES);
-        }
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tb + 4 * q + r;
+                const float v = acc[tb][r];
+                y_store<IO, decltype(acc_on)::value>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw),
+                                                     (16 * tb + r) * sy0 * ES);
+            }
+    });
 }
 
 

@@ -232,21 +232,24 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
                                  (long long)p0 * p.s_x[2];
 
     // State entering the sequence, s0[ids[seq]] in the caller's [P][N] rows
-    // (s_s[1] == d_state): register r of tile i holds n = 16 (NTW sw + i) +
+    // of s_s[1] elements (d_state, or more when this launch serves a block of
+    // the state indices): register r of tile i holds n = 16 (NTW sw + i) +
     // 4 g4 + r at channel p0 + l16. Channels past the block read 0 through the
-    // range check; n past d_state is masked (it would read the next row).
-    // Waves that carry no state load an empty range.
+    // range check; n past d_state is masked (its index is clamped into the
+    // row). Waves that carry no state load an empty range.
     const int src = p.has_ids ? b.ids[seq] : seq;
+    const int sN = (int)p.s_s[1];    // d_state, or the whole row for a block of state indices
+    const unsigned srow_bytes = (unsigned)((pw - 1) * sN + N) * 4u;
     f32x4 R[NTW];
     {
-        const helix_rsrc rs = make_rsrc(b.s0 + src * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
-                                        swave ? (unsigned)(pw * N) * 4u : 0u);
+        const helix_rsrc rs = make_rsrc(b.s0 + src * p.seq_s + h * p.s_s[0] + (long long)p0 * sN,
+                                        swave ? srow_bytes : 0u);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int n = 16 * (NTW * max(sw, 0) + i) + 4 * g4 + r;
-                R[i][r] = keep_if_lt(buf_f32(rs, (l16 * N + n) * 4, 0), n, N);
+                R[i][r] = keep_if_lt(buf_f32(rs, (l16 * sN + min(n, N - 1)) * 4, 0), n, N);
             }
     }
     // Every wave's G3 reads the whole state: it is shared through sR, written
@@ -654,11 +657,14 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
                                                 (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                             bytes);
+            with_y_acc(p, [&](auto acc_on) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * tb + 4 * g4 + r;
-                io_store<IO, HELIX_NT>(ry, ya[r], store_off_if_lt((t * sy0 + l16 * sy2) * ES, t, tlen, l16, pw), 0);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tb + 4 * g4 + r;
+                    y_store<IO, decltype(acc_on)::value>(
+                        ry, ya[r], store_off_if_lt((t * sy0 + l16 * sy2) * ES, t, tlen, l16, pw), 0);
+                }
+            });
         }
         }
         // The next chunk's staging overwrites C, B/M and dtX. X6 needs no
@@ -671,15 +677,15 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
 
     // Final state to s1[seq], same register layout as the s0 read (the state
     // waves; the others store to an empty range).
-    const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * N,
-                                    swave ? (unsigned)(pw * N) * 4u : 0u);
+    const helix_rsrc ro = make_rsrc(b.s1 + seq * p.seq_s + h * p.s_s[0] + (long long)p0 * sN,
+                                    swave ? srow_bytes : 0u);
 #pragma unroll
     for (int i = 0; i < NTW; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int n = 16 * (NTW * max(sw, 0) + i) + 4 * g4 + r;
             __builtin_amdgcn_raw_buffer_store_b32(as_u32(R[i][r]), ro,
-                                                  store_off_if_lt((l16 * N + n) * 4, n, N, l16, pw), 0, 0);
+                                                  store_off_if_lt((l16 * sN + n) * 4, n, N, l16, pw), 0, 0);
         }
 }
 

@@ -291,7 +291,32 @@ namespace {
 int choose_walk_len(const helix_scan_desc& d, int cpg);
 }
 
+int n_state_blocks(const helix_scan_desc& d) {
+    if (d.d_state <= HELIX_N_MAX) return 1;
+    const int nb0 = (d.d_state + HELIX_N_BLOCK - 1) / HELIX_N_BLOCK;
+    const int base = ((d.d_state + nb0 - 1) / nb0 + 7) / 8 * 8;   // <= HELIX_N_BLOCK
+    return (d.d_state + base - 1) / base;
+}
+
+helix_scan_desc state_block(const helix_scan_desc& d, int k, int* n0) {
+    helix_scan_desc b = d;
+    const int nb = n_state_blocks(d);
+    if (nb > 1) {
+        const int base = ((d.d_state + nb - 1) / nb + 7) / 8 * 8;
+        b.d_state = std::min(base, d.d_state - k * base);
+        b.backend = HELIX_BACKEND_SGMMA;
+        if (n0) *n0 = k * base;
+    } else if (n0) {
+        *n0 = 0;
+    }
+    return b;
+}
+
+helix_scan_desc plan_desc(const helix_scan_desc& d) { return state_block(d, 0, nullptr); }
+
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d) {
+    // d_state above HELIX_N_MAX: the fp32 path's kernels of its blocks.
+    if (d.d_state > HELIX_N_MAX) return select_traits(ctx, plan_desc(d));
     const helix_tuning& tu = tuning_of(ctx);
     const TraitTable& tt = table();
     const int k = np_index(d.d_state);
@@ -732,7 +757,14 @@ extern "C" bool helix_scan_supported(helix_ctx* ctx, const helix_scan_desc* d) {
         if ((d->s_b[0] | d->s_b[1] | d->seq_b | d->s_c[0] | d->s_c[1] | d->seq_c) & 1) return false;
     }
     if (d->d_state % 8 != 0 || d->head_dim % 8 != 0) return false;
-    if (d->d_state > HELIX_N_MAX) return false;
+    // A larger d_state runs as blocks of state indices on the fp32 path, each
+    // adding its share into y (helix::rt::state_block): fp32 storage and
+    // scalar A only, and no explicit bf16 request (the reference serves its
+    // bf16 Pass C at d_state 128 and 256 only, caps.mm:65-73; AUTO takes the
+    // fp32 path there too, caps.mm:89-93).
+    if (d->d_state > HELIX_N_MAX &&
+        (d->io_dtype != HELIX_F32 || d->a_form != HELIX_A_SCALAR_PER_HEAD || d->backend == HELIX_BACKEND_MPP))
+        return false;
     // B, C rows and state rows are staged as contiguous d_state vectors.
     if (d->s_b[2] != 1 || d->s_c[2] != 1 || d->s_s[2] != 1) return false;
     if (d->s_s[1] != d->d_state) return false;
@@ -751,7 +783,9 @@ extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc*
     if (!d || !d->multipass) return 0;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     if (tr.k_single) return 0;
-    return helix::rt::plan_multipass(ctx, *d, tr).total_bytes;
+    // Above HELIX_N_MAX the blocks run one after another in the same
+    // scratch: the largest block's plan.
+    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(*d), tr).total_bytes;
 }
 
 extern "C" helix_backend helix_ctx_select_backend(helix_ctx* ctx, const helix_scan_desc* d) {

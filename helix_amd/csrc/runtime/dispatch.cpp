@@ -81,21 +81,25 @@ bool y_overlaps_others(const helix_scan_desc& d, const void* y, const void* x, c
     return false;
 }
 
+// One launch sequence for d_state <= HELIX_N_MAX, or for one block of state
+// indices of a larger d_state (block: d is helix::rt::state_block's
+// descriptor, already gated as part of the caller's; y_acc: add into y).
 // scratch_sized: the scratch is the library's own fixed array, already known
 // to hold the plan (helix_scan_encode_noalloc), so its allocation is not
 // queried.
 // budget_cap: the plan's scratch budget is at most this many bytes (the fixed
 // array of helix_scan_encode_noalloc).
-helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
-                         helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
-                         helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
-                         helix_tensor s1, helix_tensor scratch, bool scratch_sized = false,
-                         size_t budget_cap = SIZE_MAX) {
+// dry: run every check, enqueue nothing.
+helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
+                        helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
+                        helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
+                        helix_tensor s1, helix_tensor scratch, bool scratch_sized, size_t budget_cap,
+                        bool block, bool y_acc, bool dry) {
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
     }
-    if (!helix_scan_supported(ctx, d)) {
+    if (!block && !helix_scan_supported(ctx, d)) {
         set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
         return HELIX_ERR_UNSUPPORTED_SHAPE;
     }
@@ -111,6 +115,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         return HELIX_ERR_INVALID_ARG;
     }
     params.has_ids = ids.buf ? 1 : 0;
+    params.y_acc = y_acc ? 1 : 0;
 
     // 16-bit storage: B and C rows are read as 16-byte runs of eight
     // elements, which needs their bases 4-byte aligned (the gate keeps the
@@ -136,7 +141,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     // the one-launch path.
     helix::rt::MultipassPlan yplan;
     bool ytile = false;
-    if (trp->k_single) {
+    if (trp->k_single && !block) {   // a block adds into y: no tiles there
         const HelixMatmulTraits* ytr = nullptr;
         yplan = helix::rt::plan_ytile(ctx, *d, *trp, &ytr);
         ytile = ytr && (reinterpret_cast<uintptr_t>(dptr(y)) & 15) == 0 &&
@@ -157,6 +162,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             return HELIX_ERR_INVALID_ARG;
         }
         params.np = tr.np;
+        if (dry) return HELIX_OK;
         HelixScanBuffers bufs;
         std::memset(&bufs, 0, sizeof(bufs));
         bufs.s0  = static_cast<const float*>(dptr(s0));
@@ -283,6 +289,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             return HELIX_ERR_INVALID_ARG;
         }
     }
+    if (dry) return HELIX_OK;
 
     // Debug-only per-pass timing split (reference dispatch.mm:207-216):
     // HELIX_ONLY_PASS=A|B|C enqueues just that pass, and a set of letters
@@ -360,6 +367,52 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     return st;
 }
 
+// The encoder behind every entry point. d_state above HELIX_N_MAX runs as
+// helix::rt::n_state_blocks blocks of state indices in stream order, block k
+// reading B, C and s0 and writing s1 at its first state index n0 and adding
+// its share of y into y; every block is checked before the first is
+// enqueued. y then must not overlap an input: a later block would read what
+// an earlier one wrote.
+helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_desc* d,
+                         helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
+                         helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
+                         helix_tensor s1, helix_tensor scratch, bool scratch_sized = false,
+                         size_t budget_cap = SIZE_MAX) {
+    const int nb = helix::rt::n_state_blocks(*d);
+    if (nb == 1)
+        return encode_one(ctx, stream, d, s0, x, dt, A, B, C, ids, y, s1, scratch, scratch_sized, budget_cap,
+                          /*block=*/false, /*y_acc=*/false, /*dry=*/false);
+    if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
+        set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
+        return HELIX_ERR_INVALID_ARG;
+    }
+    if (!helix_scan_supported(ctx, d)) {
+        set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
+        return HELIX_ERR_UNSUPPORTED_SHAPE;
+    }
+    if (y_overlaps_others(*d, dptr(y), dptr(x), dptr(dt), dptr(A), dptr(B), dptr(C), dptr(s0), dptr(ids),
+                          dptr(s1))) {
+        set_error(ctx, "y overlaps an input or s1; with d_state above " + std::to_string(HELIX_N_MAX) +
+                           " y accumulates over blocks of state indices and must be a buffer of its own");
+        return HELIX_ERR_INVALID_ARG;
+    }
+    for (int pass = 0; pass < 2; ++pass) {   // pass 0 checks every block, pass 1 enqueues them
+        for (int k = 0; k < nb; ++k) {
+            int n0 = 0;
+            const helix_scan_desc sub = helix::rt::state_block(*d, k, &n0);
+            auto at_n0 = [n0](helix_tensor t) {
+                if (t.buf) t.offset += (uint64_t)n0 * sizeof(float);
+                return t;
+            };
+            const helix_status st = encode_one(ctx, stream, &sub, at_n0(s0), x, dt, A, at_n0(B), at_n0(C), ids, y,
+                                               at_n0(s1), scratch, scratch_sized, budget_cap, /*block=*/true,
+                                               /*y_acc=*/k > 0, /*dry=*/pass == 0);
+            if (st != HELIX_OK) return st;
+        }
+    }
+    return HELIX_OK;
+}
+
 }  // namespace
 
 extern "C" helix_status helix_scan_encode(helix_ctx* ctx, void* cmd_buffer, const helix_scan_desc* d,
@@ -389,7 +442,7 @@ size_t noalloc_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
     if (!d->multipass) return 0;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     if (tr.k_single) return 0;
-    return helix::rt::plan_multipass(ctx, *d, tr, HELIX_NOALLOC_SCRATCH_BYTES).total_bytes;
+    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(*d), tr, HELIX_NOALLOC_SCRATCH_BYTES).total_bytes;
 }
 
 }  // namespace
@@ -437,9 +490,14 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     if (!helix_scan_supported(ctx, d)) return HELIX_ERR_UNSUPPORTED_SHAPE;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     std::memset(out, 0, sizeof(*out));
+    // Above HELIX_N_MAX: the plan of one block (the largest), run once per
+    // block; the blocks add into y, so the single pass keeps no tiles there.
+    const int nb = helix::rt::n_state_blocks(*d);
+    const helix_scan_desc pd = helix::rt::plan_desc(*d);
+    out->state_blocks = nb;
     const HelixMatmulTraits* ytr = nullptr;
     const helix::rt::MultipassPlan yplan =
-        tr.k_single ? helix::rt::plan_ytile(ctx, *d, tr, &ytr) : helix::rt::MultipassPlan{};
+        tr.k_single && nb == 1 ? helix::rt::plan_ytile(ctx, pd, tr, &ytr) : helix::rt::MultipassPlan{};
     if (tr.k_single && !ytr) {
         out->n_chunks = (d->n_tok + HELIX_CS - 1) / HELIX_CS;
         out->chunks_per_group = out->n_chunks;
@@ -450,7 +508,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->walks_per_group = 1;
         out->hblk = 1;
         out->n_hblk = d->n_head / d->n_group;
-        out->launches = 1;
+        out->launches = nb;
         out->np = tr.np;
         out->kernel_1pass = tr.k_single;
         return HELIX_OK;
@@ -462,7 +520,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->kernel_1pass = tr.k_single;
     }
     const HelixMatmulTraits& tp = ytr ? *ytr : tr;
-    const helix::rt::MultipassPlan pl = ytr ? yplan : helix::rt::plan_multipass(ctx, *d, tr);
+    const helix::rt::MultipassPlan pl = ytr ? yplan : helix::rt::plan_multipass(ctx, pd, tr);
     out->n_chunks = pl.n_chunks;
     out->chunks_per_group = pl.chunks_per_group;
     out->n_groups = pl.n_groups;
@@ -481,7 +539,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->rec_bytes = pl.rec_elems * sizeof(float);
     }
     const bool fuse_b = helix::rt::fuse_b_on(ctx, tp, pl);   // as helix_scan_encode decides
-    out->launches = fuse_b ? 2 : 3 * pl.n_groups;
+    out->launches = (fuse_b ? 2 : 3 * pl.n_groups) * nb;
     out->np = tp.np;
     out->kernel_a = tp.k_chunk_state;
     out->kernel_b = fuse_b ? nullptr : tp.k_state_scan;

@@ -150,6 +150,21 @@ MultipassPlan plan_ytile(const helix_ctx* ctx, const helix_scan_desc& d, const H
                          const HelixMatmulTraits** tr_out);
 
 
+// d_state above HELIX_N_MAX (fp32 storage, scalar A): the recurrence is
+// independent per state index and y sums C_n h_n over them, so the scan runs
+// once per block of state indices, each block adding its share into y
+// (HelixScanParams::y_acc). n_state_blocks is 1 up to HELIX_N_MAX; otherwise
+// the blocks are equal (multiples of 8, at most HELIX_N_BLOCK, which runs the
+// d_state <= 128 kernels). state_block is block k's descriptor: d_state the
+// block's size, strides unchanged (s_s[1] stays the caller's d_state, the
+// row length of s0 and s1), backend the fp32 path; *n0 (if given) is its
+// first state index, the element offset of B, C, s0 and s1.
+int n_state_blocks(const helix_scan_desc& d);
+helix_scan_desc state_block(const helix_scan_desc& d, int k, int* n0);
+// The descriptor the plan and kernels are chosen for: block 0 above
+// HELIX_N_MAX (the largest block), else d itself.
+helix_scan_desc plan_desc(const helix_scan_desc& d);
+
 // Fills the kernel-side params from the public descriptor. Returns false and
 // sets *why when a launch dimension would exceed the hardware grid limits.
 bool build_params(const helix_scan_desc& d, HelixScanParams* out, std::string* why);

@@ -57,6 +57,12 @@ typedef struct {
                                    tile); helix_scan_encode runs kernel_1pass
                                    alone instead when y is not 16-byte aligned
                                    or overlaps x, dt, A, B, C, s0, ids or s1    */
+    int32_t  state_blocks;      /* 1 up to d_state 256; above it, the number of
+                                   blocks of state indices (equal, multiples of
+                                   8, at most 128) the scan runs as, one after
+                                   another on the fp32 path, each adding its
+                                   share into y. The other fields describe one
+                                   block (the largest), launches all of them  */
 } helix_plan_info;
 
 #define HELIX_PASS_B_LAUNCHED 0   /* kernel_b, between Pass A and Pass C         */

@@ -136,7 +136,10 @@ def _declined(host, mutate):
     ("bf16 compute dtype", lambda d: setattr(d, "compute_dtype", HELIX_BF16)),
     ("d_state not a multiple of 8", lambda d: setattr(d, "d_state", 60)),
     ("head_dim not a multiple of 8", lambda d: setattr(d, "head_dim", 60)),
-    ("d_state above 256", lambda d: setattr(d, "d_state", 264)),
+    ("d_state above 256 with explicit MPP",
+     lambda d: (setattr(d, "d_state", 264), d.s_s.__setitem__(1, 264), setattr(d, "backend", HELIX_BACKEND_MPP))),
+    ("d_state above 256 with bf16 storage",
+     lambda d: (setattr(d, "d_state", 264), d.s_s.__setitem__(1, 264), setattr(d, "io_dtype", HELIX_BF16))),
     ("strided B state", lambda d: d.s_b.__setitem__(2, 2)),
     ("strided C state", lambda d: d.s_c.__setitem__(2, 2)),
     ("strided s state", lambda d: d.s_s.__setitem__(2, 2)),
@@ -160,6 +163,51 @@ def test_gate_accepts_ragged_strided_and_odd_shapes(host):
     d.s_y[2] = 1
     d.chunk = 64
     assert host.supported(d)
+
+
+@pytest.mark.parametrize("n,blocks,size", [(264, 3, 88), (384, 3, 128), (512, 4, 128), (520, 5, 104),
+                                            (1000, 8, 128), (4104, 33, 128)])
+@pytest.mark.parametrize("multipass", [True, False])
+def test_state_blocks_above_256(host, n, blocks, size, multipass):
+    """d_state above 256 (the reference gate takes any multiple of 8,
+    caps.mm:129) runs as equal blocks of at most 128 state indices on the
+    fp32 path; the plan is one block's, launched once per block."""
+    d = abi.desc_init_c(300, 2, 4, 64, n, 2)
+    d.multipass = multipass
+    assert host.supported(d)
+    assert host.select_backend(d) == HELIX_BACKEND_SGMMA
+    k = host.plan_info(d)
+    assert k.state_blocks == blocks
+    assert k.state_in_y == 0
+    b = abi.desc_init_c(300, 2, 4, 64, size, 2)
+    b.multipass = multipass
+    b.backend = HELIX_BACKEND_SGMMA
+    kb = host.plan_info(b)
+    assert kb.state_blocks == 1
+    assert k.np == kb.np == 128
+    assert host.scratch_size(d) == host.scratch_size(b)
+    if multipass:
+        assert k.kernel_a == kb.kernel_a and k.kernel_c == kb.kernel_c and k.seg_len == kb.seg_len
+        assert k.launches == blocks * kb.launches
+        assert host.scratch_size(d) > 0
+    else:
+        assert k.kernel_1pass == kb.kernel_1pass == b"helix_scan_1pass_f32_n128"
+        assert k.launches == blocks
+        assert host.scratch_size(d) == 0
+    for mutate in (lambda x: setattr(x, "backend", HELIX_BACKEND_MPP),
+                   lambda x: setattr(x, "io_dtype", HELIX_F16),
+                   lambda x: setattr(x, "a_form", HELIX_A_DIAG_PER_CHANNEL),
+                   lambda x: x.s_s.__setitem__(1, n + 8)):
+        e = abi.desc_init_c(300, 2, 4, 64, n, 2)
+        e.multipass = multipass
+        mutate(e)
+        assert not host.supported(e)
+
+
+def test_state_blocks_up_to_256_unchanged(host):
+    for n in (8, 128, 136, 256):
+        k = host.plan_info(mp((300, 2, 4, 64, n, 2)))
+        assert k.state_blocks == 1
 
 
 def test_diagonal_a_runs_the_single_pass_walk(host):

@@ -63,6 +63,43 @@ def test_generator_matches_reference_harness(shape, memory):
 
 
 @needs_ref
+@pytest.mark.parametrize("shape", [(70, 2, 2, 16, 264, 1), (130, 1, 2, 8, 512, 2)],
+                         ids=lambda s: "L%d_S%d_H%d_P%d_N%d_G%d" % s)
+def test_scan_bitexact_vs_reference_above_256(shape):
+    # d_state above 256: the reference gate takes any multiple of 8
+    # (caps.mm:129); its ref::scan is the same loop at every d_state.
+    L, S, H, P, N, G = shape
+    p = po.problem_harness(L, S, H, P, N, G, 778, "long")
+    y, s1 = po.scan(p)
+    yr, sr = po.ref_scan(p)
+    assert np.array_equal(bits(y), bits(yr)) and np.array_equal(bits(s1), bits(sr))
+
+
+def test_state_blocks_sum_to_the_scan():
+    # What the encoder relies on above d_state 256: each state index evolves
+    # on its own (h_n <- a h_n + B_n dt x) and y sums C_n h_n over n, so the
+    # scans of blocks of state indices give s1 by concatenation and y by
+    # summation. Checked on the oracle for the blocks the encoder would use
+    # at d_state 264 (three of 88).
+    L, S, H, P, N, G = 150, 2, 4, 16, 264, 2
+    p = po.problem_harness(L, S, H, P, N, G, 779, "long")
+    p.s0 = np.random.default_rng(7).standard_normal(p.s0.shape).astype(np.float32) * 0.3
+    y, s1 = po.scan(p)
+    y_sum = np.zeros(y.shape, np.float64)
+    for n0 in (0, 88, 176):
+        sl = slice(n0, n0 + 88)
+        q = po.Problem(po.desc_init(L, S, H, P, 88, G), np.ascontiguousarray(p.s0[..., sl]), p.x, p.dt, p.A,
+                       np.ascontiguousarray(p.B[..., sl]), np.ascontiguousarray(p.C[..., sl]), p.ids)
+        yq, sq = po.scan(q)
+        assert np.array_equal(bits(sq), bits(np.ascontiguousarray(s1[..., sl]))), n0
+        y_sum += yq
+    # y of each block is rounded to fp32 once; the full scan rounds the sum once.
+    assert np.allclose(y_sum, y, rtol=1e-6, atol=1e-7)
+    # A dropped block is not within that bound.
+    assert not np.allclose(y_sum - yq, y, rtol=1e-6, atol=1e-7)
+
+
+@needs_ref
 @pytest.mark.parametrize("memory", ["short", "long"])
 @pytest.mark.parametrize("shape", ALGEBRA_SHAPES, ids=lambda s: "L%d_S%d_H%d_P%d_N%d_G%d_c%d" % s)
 def test_scan_bitexact_vs_reference(shape, memory):
