@@ -411,6 +411,61 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         }
     };
 
+    // R[n][p] += sum_j B^T[n][j] (w_j x[j][p]) over four K steps of 16 tokens,
+    // in groups of two n tiles.
+    constexpr int NG = NTN / 2;                 // groups of two n tiles per K step
+    auto read_group = [&](const __bf16* planes, int s, int i0, bf16x8 (&bp)[2][NS]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int k = 0; k < NS; ++k)
+                bp[i][k] = *reinterpret_cast<const bf16x8*>(&planes[hb_off<NP>(k, 32 * (i0 + i) + lo, 2 * s + hi)]);
+    };
+    auto read_w = [&](const float* __restrict__ wrow, int s, f32x4& w0, f32x4& w1) {
+        w0 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi]);
+        w1 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi + 4]);
+    };
+    // Smallest terms first, the two accumulators interleaved so no MFMA
+    // waits on the one before it.
+    auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NS], const bf16x8 (&xp)[NS]) {
+        if constexpr (NS == 3) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][2], xp[0], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[1], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[2], acc[i0 + i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[0], acc[i0 + i]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[1], acc[i0 + i]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[0], acc[i0 + i]);
+    };
+    // The x operand planes of K step s of the chunk in xs, weighted by w0, w1.
+    auto split_x = [&](int s, const f32x4& w0, const f32x4& w1, bf16x8 (&xp)[NS]) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = mul_legacy(w0[e], io_widen<IO>(xs.v[s][e]));
+            v[4 + e] = mul_legacy(w1[e], io_widen<IO>(xs.v[s][4 + e]));
+        }
+        u32x4 xq[NS];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            unsigned w[3];
+            if constexpr (NS == 3)
+                split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
+            else
+                split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) xq[k][e] = w[k];
+        }
+#pragma unroll
+        for (int k = 0; k < NS; ++k) xp[k] = __builtin_bit_cast(bf16x8, xq[k]);
+    };
+
     // Chunk nth(it). Its B planes are in `cur` and its weights in `wcur` (both
     // staged a step earlier), its x in xs; `rows` holds the B (and C) rows and
     // dtraw the dt of the chunk after it, cn. Every memory instruction runs on
@@ -442,44 +497,13 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         }
         const float a_c = MODE == 0 ? expf(lendf) : 1.0f;
 
-        // R[n][p] += sum_j B^T[n][j] (w_j x[j][p]) over four K steps of 16 tokens,
-        // in groups of two n tiles. The B planes of the next group and the
-        // weights of the next K step are read from LDS while the current
-        // group's MFMAs run, so no MFMA waits on the LDS.
-        constexpr int NG = NTN / 2;                 // groups of two n tiles per K step
-        auto read_group = [&](int s, int i0, bf16x8 (&bp)[2][NS]) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int k = 0; k < NS; ++k)
-                    bp[i][k] = *reinterpret_cast<const bf16x8*>(&cur[hb_off<NP>(k, 32 * (i0 + i) + lo, 2 * s + hi)]);
-        };
-        auto read_w = [&](int s, f32x4& w0, f32x4& w1) {
-            w0 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi]);
-            w1 = *reinterpret_cast<const f32x4*>(&wrow[16 * s + 8 * hi + 4]);
-        };
-        // Smallest terms first, the two accumulators interleaved so no MFMA
-        // waits on the one before it.
-        auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NS], const bf16x8 (&xp)[NS]) {
-            if constexpr (NS == 3) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][2], xp[0], acc[i0 + i]);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[1], acc[i0 + i]);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[2], acc[i0 + i]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][1], xp[0], acc[i0 + i]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[1], acc[i0 + i]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][0], xp[0], acc[i0 + i]);
-        };
+        // The B planes of the next group and the weights of the next K step
+        // are read from LDS while the current group's MFMAs run, so no MFMA
+        // waits on the LDS.
         bf16x8 bq[2][2][NS];        // the B planes of two groups, in turn
         f32x4 w0, w1;
-        read_group(0, 0, bq[0]);
-        read_w(0, w0, w1);
+        read_group(cur, 0, 0, bq[0]);
+        read_w(wrow, 0, w0, w1);
         // MODE 0: the decay of the state carried in, on each group's
         // accumulators just before their first products of the chunk.
         if constexpr (MODE == 0) {
@@ -488,27 +512,9 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = mul_legacy(w0[e], io_widen<IO>(xs.v[s][e]));
-                v[4 + e] = mul_legacy(w1[e], io_widen<IO>(xs.v[s][4 + e]));
-            }
-            u32x4 xq[NS];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                unsigned w[3];
-                if constexpr (NS == 3)
-                    split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
-                else
-                    split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
-#pragma unroll
-                for (int k = 0; k < NS; ++k) xq[k][e] = w[k];
-            }
             bf16x8 xp[NS];
-#pragma unroll
-            for (int k = 0; k < NS; ++k) xp[k] = __builtin_bit_cast(bf16x8, xq[k]);
-            if (s + 1 < 4) read_w(s + 1, w0, w1);
+            split_x(s, w0, w1, xp);
+            if (s + 1 < 4) read_w(wrow, s + 1, w0, w1);
             // K step s of the next chunk's x into the registers just split:
             // it has a whole chunk step to arrive.
             vmem_fence();
@@ -534,7 +540,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 const int q = (s * NG + gi) & 1;          // buffer of this group
                 const int s_n = gi + 1 < NG ? s : s + 1;  // the next group's K step
                 const int g_n = gi + 1 < NG ? gi + 1 : 0;
-                if (s_n < 4) read_group(s_n, 2 * g_n, bq[q ^ 1]);
+                if (s_n < 4) read_group(cur, s_n, 2 * g_n, bq[q ^ 1]);
                 if (MODE == 0 && s == 0 && gi > 0) {
                     acc[2 * gi] *= a_c;
                     acc[2 * gi + 1] *= a_c;
@@ -563,43 +569,83 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c1, lane, wave, N, copier);
     dtraw = hb_load_dt(p, dt_h, c1, lane);
     __syncthreads();
+    // MODE 2 takes the segment's last chunk out of the loop (last_step).
+    const int n_loop = MODE == 2 ? n_ch - 1 : n_ch;
 #pragma unroll 1
-    for (int it = 0; it < n_ch; ++it) {
+    for (int it = 0; it < n_loop; ++it) {
         const int par = it & 1;
         step(it, sB + par * PLANES, sB + (PLANES - par * PLANES), sW[par], sW[par ^ 1]);
     }
 
-    // Segment aggregate D_s and the segment's log-decay: in scratch, or in y
-    // for the single pass without scratch (p.ytile; ytile_* in helix_common.h,
-    // the range covering the rows the tile and the log-decay take).
-    if (MODE == 2 && p.ytile) {
-        const int upr = pw >> 2;
-        const unsigned rows = (unsigned)((16 * NP + 1 + upr - 1) / upr);
-        const helix_rsrc ry = make_rsrc_u(b.y + ytile_base(p, seq, h, slab, seg),
-                                          item_ok ? rows * (unsigned)p.s_y[0] * 4u : 0u);
+    // Accumulator tiles i0 .. i1 - 1 of the segment aggregate D_s: in scratch,
+    // or in y for the single pass without scratch (p.ytile; ytile_* in
+    // helix_common.h, the range covering the rows the tile and the log-decay
+    // take).
+    auto store_tiles = [&](int i0, int i1) {
+        if (MODE == 2 && p.ytile) {
+            const int upr = pw >> 2;
+            const unsigned yrows = (unsigned)((16 * NP + 1 + upr - 1) / upr);
+            const helix_rsrc ry = make_rsrc_u(b.y + ytile_base(p, seq, h, slab, seg),
+                                              item_ok ? yrows * (unsigned)p.s_y[0] * 4u : 0u);
 #pragma unroll
-        for (int i = 0; i < NTN; ++i)
+            for (int i = i0; i < i1; ++i)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int off = (int)ytile_unit(p, tile_unit(NTN, pt, i, r4, 0) + lane, pw) * 4;
-                const u32x4 w = {as_u32(acc[i][4 * r4]), as_u32(acc[i][4 * r4 + 1]), as_u32(acc[i][4 * r4 + 2]),
-                                 as_u32(acc[i][4 * r4 + 3])};
-                __builtin_amdgcn_raw_buffer_store_b128(w, ry, off, 0, 0);
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int off = (int)ytile_unit(p, tile_unit(NTN, pt, i, r4, 0) + lane, pw) * 4;
+                    const u32x4 w = {as_u32(acc[i][4 * r4]), as_u32(acc[i][4 * r4 + 1]),
+                                     as_u32(acc[i][4 * r4 + 2]), as_u32(acc[i][4 * r4 + 3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(w, ry, off, 0, 0);
+                }
+        } else {
+            const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
+            const helix_rsrc rs = make_rsrc_u(sg, tile_bytes);
+#pragma unroll
+            for (int i = i0; i < i1; ++i)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    buf_store_unit<float>(rs, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2],
+                                          acc[i][4 * r4 + 3], lane, tile_unit(NTN, pt, i, r4, 0));
+        }
+    };
+
+    if constexpr (MODE == 2) {
+        // The segment's last chunk (the first in time): the step's products
+        // without the next chunk's loads, preamble and staging (nothing would
+        // read them), taken group of n tiles by group with each tile's
+        // products in the step's order, so the aggregate is the same, and a
+        // group's tiles are stored while the next group's MFMAs run. Its B
+        // planes and weights are in the buffers of parity n_loop; it writes
+        // no LDS, so it needs no barrier.
+        const int par = n_loop & 1;
+        const __bf16* cur = sB + par * PLANES;
+        const float* __restrict__ wrow = sW[par][is];
+        lend = __builtin_bit_cast(double, (unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS]) |
+                                              ((unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS + 1]) << 32));
+        mu += lend;
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+            bf16x8 bq[2][2][NS];
+            read_group(cur, 0, 2 * gi, bq[0]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                f32x4 w0, w1;
+                read_w(wrow, s, w0, w1);
+                bf16x8 xp[NS];
+                split_x(s, w0, w1, xp);
+                if (s + 1 < 4) read_group(cur, s + 1, 2 * gi, bq[(s + 1) & 1]);
+                mfma_group(2 * gi, bq[s & 1], xp);
             }
-        if (leader && lane == 0) b.y[ytile_segld(p, seq, h, seg)] = (float)mu;
+            store_tiles(2 * gi, 2 * gi + 2);
+        }
+        if (p.ytile) {
+            if (leader && lane == 0) b.y[ytile_segld(p, seq, h, seg)] = (float)mu;
+        } else {
+            if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = (float)mu;
+        }
         return;
     }
-    {
-        const float* sg = b.s_seg + seq * p.sg_seq + (long long)seg * p.sg_seg + tile_off;
-        const helix_rsrc rs = make_rsrc_u(sg, tile_bytes);
-#pragma unroll
-        for (int i = 0; i < NTN; ++i)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                buf_store_unit<float>(rs, acc[i][4 * r4], acc[i][4 * r4 + 1], acc[i][4 * r4 + 2], acc[i][4 * r4 + 3],
-                                      lane, tile_unit(NTN, pt, i, r4, 0));
-    }
-    if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = MODE == 0 ? lam : (float)mu;
+    store_tiles(0, NTN);
+    if (leader && lane == 0) b.segld[seq * p.sd_seq + (long long)seg * p.n_head + h] = lam;
 }
 
 #define HELIX_PASS_A_HB(NP)                                                                           \
