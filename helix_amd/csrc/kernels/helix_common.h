@@ -512,9 +512,14 @@ HELIX_DEV float io_widen(typename IoWord<IO>::type w) {
 // which keeps y from displacing the inputs still being read (15-25% faster
 // than the default on the walking Pass C at config 2), at device scope, which
 // measured a further 5% on the walks (bf16 61.1 -> 58.3 us, fp32 155.5 ->
-// 147.9 us at config 2). sc1 without nt, or with sc0, measured slower than
-// the default; the same bits on loads or on the scratch stores gave nothing.
+// 147.9 us at config 2). The walk that reads Pass A's bf16 copies of B and C
+// (many heads per group, all reading the copies through L2) stores with nt
+// alone, HELIX_NT_L2: there the device-scope bit cost 7% (config 4a walk
+// 342 -> 366 us; 4b unchanged). sc1 without nt, or with sc0, measured slower
+// than the default; the same bits on loads or on the scratch stores gave
+// nothing.
 #define HELIX_NT 18
+#define HELIX_NT_L2 2
 template <typename IO, int AUX = 0>
 HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
     if constexpr (sizeof(IO) == 4) {
@@ -530,11 +535,11 @@ HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
 // of state indices of a d_state above HELIX_N_MAX), added to the value y
 // holds first. Callers test y_acc once around a run of stores
 // (with_y_acc), so the common path has no branch per store.
-template <typename IO, bool ACC>
+template <typename IO, bool ACC, int AUX = HELIX_NT>
 HELIX_DEV void y_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
     if constexpr (ACC && sizeof(IO) == 4)
         v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff_bytes, soff_bytes, 0));
-    io_store<IO, HELIX_NT>(r, v, voff_bytes, soff_bytes);
+    io_store<IO, AUX>(r, v, voff_bytes, soff_bytes);
 }
 // f(std::bool_constant<p.y_acc>{}).
 template <typename F>

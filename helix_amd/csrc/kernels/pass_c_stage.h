@@ -134,8 +134,10 @@ __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanP
 // Store a walking wave's y tile of one chunk (16 x 16 MFMA layout, lane
 // (q, c16) of P column pp): acc[tb] register r holds
 // y[t = 16 tb + 4 q + r][pp]. Rows past tlen and columns past the slab width
-// are dropped by the range check; with tlen <= 0 nothing is stored.
-template <typename IO>
+// are dropped by the range check; with tlen <= 0 nothing is stored. AUX: the
+// stores' cache policy (HELIX_NT, or HELIX_NT_L2 for the walk on Pass A's
+// bf16 copies of B and C).
+template <typename IO, int AUX = HELIX_NT>
 __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScanParams& p,
                                           const HelixScanBuffers& b, int seq, int h, int t0, int tlen,
                                           int p0, int pw, int pp, int q) {
@@ -153,8 +155,8 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * tb + 4 * q + r;
                 const float v = acc[tb][r];
-                y_store<IO, decltype(acc_on)::value>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw),
-                                                     (16 * tb + r) * sy0 * ES);
+                y_store<IO, decltype(acc_on)::value, AUX>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw),
+                                                          (16 * tb + r) * sy0 * ES);
             }
     });
 }

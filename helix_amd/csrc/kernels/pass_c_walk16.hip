@@ -461,7 +461,9 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
                     acc[tb] = mfma16(ma, xb[s], acc[tb]);
                 }
         }
-        store_y16<IO>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        // Reading Pass A's bf16 copies (fp32 storage, BIO bf16): nt alone.
+        constexpr int YAUX = sizeof(IO) == 4 && __is_same(BIO, __bf16) ? HELIX_NT_L2 : HELIX_NT;
+        store_y16<IO, YAUX>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
 
         if constexpr (M_IN_B) __syncthreads();
     }
