@@ -535,11 +535,13 @@ HELIX_DEV void io_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
 // of state indices of a d_state above HELIX_N_MAX), added to the value y
 // holds first. Callers test y_acc once around a run of stores
 // (with_y_acc), so the common path has no branch per store.
+// 16-bit y is stored with nt alone: with the device-scope bit its 2-byte
+// stores made the bf16-storage walk 67% slower (config 2: 51 -> 86 us).
 template <typename IO, bool ACC, int AUX = HELIX_NT>
 HELIX_DEV void y_store(helix_rsrc r, float v, int voff_bytes, int soff_bytes) {
     if constexpr (ACC && sizeof(IO) == 4)
         v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff_bytes, soff_bytes, 0));
-    io_store<IO, AUX>(r, v, voff_bytes, soff_bytes);
+    io_store<IO, sizeof(IO) == 4 ? AUX : HELIX_NT_L2>(r, v, voff_bytes, soff_bytes);
 }
 // f(std::bool_constant<p.y_acc>{}).
 template <typename F>
