@@ -136,8 +136,9 @@ __device__ __forceinline__ void store_y_tile(const f32x16& acc, const HelixScanP
 // y[t = 16 tb + 4 q + r][pp]. Rows past tlen and columns past the slab width
 // are dropped by the range check; with tlen <= 0 nothing is stored. AUX: the
 // stores' cache policy (HELIX_NT, or HELIX_NT_L2 for the walk on Pass A's
-// bf16 copies of B and C).
-template <typename IO, int AUX = HELIX_NT>
+// bf16 copies of B and C). RT_ACC: add what y holds when p.y_acc is set (off
+// for a caller that loaded it ahead with load_y16 and added it to acc).
+template <typename IO, int AUX = HELIX_NT, bool RT_ACC = true>
 __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScanParams& p,
                                           const HelixScanBuffers& b, int seq, int h, int t0, int tlen,
                                           int p0, int pw, int pp, int q) {
@@ -148,7 +149,7 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
                                         (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                     bytes);
     const int voff = (4 * q * sy0 + pp * sy2) * ES;
-    with_y_acc(p, [&](auto acc_on) {
+    auto put = [&](auto acc_on) {
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
@@ -158,7 +159,31 @@ __device__ __forceinline__ void store_y16(const f32x4 (&acc)[4], const HelixScan
                 y_store<IO, decltype(acc_on)::value, AUX>(ry, v, store_off_if_lt(voff, t, tlen, pp, pw),
                                                           (16 * tb + r) * sy0 * ES);
             }
-    });
+    };
+    if constexpr (RT_ACC)
+        with_y_acc(p, put);
+    else
+        put(std::false_type{});
+}
+
+// What y holds at the elements store_y16 would store (fp32 storage), 0 where
+// it would store nothing: for a walk that adds into y (HelixScanParams::y_acc),
+// loaded a chunk's work ahead of the stores so the loads' latency is hidden.
+__device__ __forceinline__ void load_y16(f32x4 (&yv)[4], const HelixScanParams& p, const HelixScanBuffers& b,
+                                         int seq, int h, int t0, int tlen, int p0, int pw, int pp, int q) {
+    const int sy0 = sgpr_fresh((int)p.s_y[0]), sy2 = (int)p.s_y[2];
+    const unsigned bytes = tlen > 0 ? ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u : 0u;
+    const helix_rsrc ry = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
+                                        (long long)p0 * p.s_y[2],
+                                    bytes);
+    const int voff = (4 * q * sy0 + pp * sy2) * 4;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 16 * tb + 4 * q + r;
+            yv[tb][r] = buf_f32(ry, store_off_if_lt(voff, t, tlen, pp, pw), (16 * tb + r) * sy0 * 4);
+        }
 }
 
 

@@ -150,8 +150,12 @@ HELIX_DEV void store16_nat(__bf16* buf, int row, int col0, const float (&v)[16])
 // IO: the caller's storage type of x, B, C and y (dt, A and the states are
 // fp32). BIO: the type B and C are read in; __bf16 with fp32 storage when
 // they come from Pass A's bf16 copies (the host points B and C there).
-template <int NP, int HPW, typename IO = float, typename BIO = IO>
+// YACC: the kernel of a block of state indices after the first (fp32
+// storage, p.y_acc): y of each chunk is loaded with the next chunk's inputs
+// and added to the chunk's result.
+template <int NP, int HPW, typename IO = float, typename BIO = IO, bool YACC = false>
 __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(!YACC || sizeof(IO) == 4, "y accumulates in fp32 storage only");
     constexpr int NW  = 4 * HPW;              // HPW heads per workgroup, four waves each
     constexpr int NB  = NP / 16;              // 16-row state tiles of R
     constexpr int KS  = NP / 32;              // K steps over the state
@@ -363,6 +367,8 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
             sE[hw][lane] = __builtin_amdgcn_exp2f(l2);
         }
         load_stage_w16<IO>(st, p, rec_h, x_h, cn, lane, w4, pw);
+        f32x4 yprev[4];
+        if constexpr (YACC) load_y16(yprev, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
         __syncthreads();
 
         // ---- G1: C B^T once for the workgroup's heads (they share B and C);
@@ -463,7 +469,13 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
         }
         // Reading Pass A's bf16 copies (fp32 storage, BIO bf16): nt alone.
         constexpr int YAUX = sizeof(IO) == 4 && __is_same(BIO, __bf16) ? HELIX_NT_L2 : HELIX_NT;
-        store_y16<IO, YAUX>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        if constexpr (YACC) {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) acc[tb] += yprev[tb];
+            store_y16<IO, YAUX, false>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        } else {
+            store_y16<IO, YAUX>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        }
 
         if constexpr (M_IN_B) __syncthreads();
     }
@@ -490,3 +502,18 @@ __device__ __forceinline__ void scan_walk16_impl(const HelixScanParams& p, const
 HELIX_PASS_C_WALK16(64)
 HELIX_PASS_C_WALK16(128)
 HELIX_PASS_C_WALK16(256)
+
+// The walks of the second and later blocks of state indices (blocks are at
+// most HELIX_N_BLOCK = 128 wide): y of each chunk loaded ahead and added.
+#define HELIX_PASS_C_WALK16_ACC(NP)                                                             \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_acc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP), float, float, true>(p, b);                   \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * HELIX_WALK16_HPW(NP)) void helix_scan_walk16_bf16_bc_acc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk16_impl<NP, HELIX_WALK16_HPW(NP), float, __bf16, true>(p, b);                  \
+    }
+
+HELIX_PASS_C_WALK16_ACC(64)
+HELIX_PASS_C_WALK16_ACC(128)

@@ -138,7 +138,10 @@ __device__ __forceinline__ void load_stage_x6(StageWX6& st, const HelixScanParam
 // (HelixScanParams::ytile): the start state comes from y (walk_start_state)
 // and the decay preamble is formed here from dt, as Pass A forms its records
 // (softplus, fp64 wave scan), since there are no records.
-template <int NP, bool YT = false>
+// YACC: the walk of a block of state indices after the first (p.y_acc): y of
+// each chunk is loaded with the next chunk's inputs and added to the chunk's
+// result.
+template <int NP, bool YT = false, bool YACC = false>
 __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     static_assert(NP == 64 || NP == 128, "d_state 64 or 128");
     // Staging lanes: 16 per pair of rows; a run of eight state indices per
@@ -364,6 +367,8 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         // that frees its LDS: hoisted, they wait on loads still in flight.
         __builtin_amdgcn_sched_barrier(0);
         load_stage_x6<YT>(st, p, rec_h, dt_h, x_h, cn, lane, q, pp, pw);
+        f32x4 yprev[4];
+        if constexpr (YACC) load_y16(yprev, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
 
         // ---- G1: D[j][t] = (B C^T) of blocks idx = wave, wave + 8 -----------
         // Block idx: D[j = 16 jb + 4 q + r][t = 16 tb + c16].
@@ -531,7 +536,13 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
                 acc[tb] = wx6_mfma(mv, xp, acc[tb]);
             }
         }
-        store_y16<float>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        if constexpr (YACC) {
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) acc[tb] += yprev[tb];
+            store_y16<float, HELIX_NT, false>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        } else {
+            store_y16<float>(acc, p, b, seq, h, t0, head_ok ? tlen : 0, p0, pw, pp, q);
+        }
         __syncthreads();   // (3)
     }
 }
@@ -549,7 +560,16 @@ __device__ __forceinline__ void scan_walk_x6_impl(const HelixScanParams& p, cons
         scan_walk_x6_impl<NP, true>(p, b);                                                      \
     }
 
+// The walks of the second and later blocks of state indices.
+#define HELIX_PASS_C_WALK_X6_ACC(NP)                                                            \
+    extern "C" __global__ __launch_bounds__(HELIX_WG * 2) void helix_scan_walk_x6_acc_n##NP(     \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_walk_x6_impl<NP, false, true>(p, b);                                               \
+    }
+
 HELIX_PASS_C_WALK_X6(64)
 HELIX_PASS_C_WALK_X6(128)
+HELIX_PASS_C_WALK_X6_ACC(64)
+HELIX_PASS_C_WALK_X6_ACC(128)
 HELIX_PASS_C_WALK_X6_Y(64)
 HELIX_PASS_C_WALK_X6_Y(128)

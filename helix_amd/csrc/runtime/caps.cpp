@@ -159,6 +159,7 @@ struct TraitTable {
                 t.name = keep("mfma fp32, passes A and C bf16x6, chunk walk" + upto);
                 t.k_chunk_state = kernel("helix_chunk_state_hb_x6agg_r64_n" + np);
                 t.k_chunk_out = kernel("helix_scan_walk_x6_n" + np);
+                t.k_chunk_out_acc = kernel("helix_scan_walk_x6_acc_n" + np);
                 t.mfma_c = "v_mfma_f32_16x16x32_bf16 (bf16x6 split operands)";
                 t.walk = true;
                 t.walk_hpw = 2;
@@ -183,6 +184,9 @@ struct TraitTable {
                         t.k_state_scan = kernel("helix_state_scan_f32");
                         t.k_chunk_out = kernel(std::string("helix_scan_walk16_bf16_") + (bc ? "bc_" : kIoTag[io]) +
                                                "n" + np);
+                        if (io == 0 && kNps[k] <= HELIX_N_BLOCK)
+                            t.k_chunk_out_acc = kernel(std::string("helix_scan_walk16_bf16_") + (bc ? "bc_" : "") +
+                                                       "acc_n" + np);
                         t.bf16_state = true;
                         t.mfma_a = s6 ? "v_mfma_f32_32x32x16_bf16 (bf16x6 split operands)"
                                       : "v_mfma_f32_32x32x16_bf16 (bf16x3 split operands)";
@@ -269,6 +273,8 @@ helix_tuning tuning_from_env() {
     if (fw >= 0) t.f32_walk = fw > 0 ? 1 : 0;
     const int yt = env_switch("HELIX_1PASS_Y");
     if (yt >= 0) t.ytile = yt > 0 ? 1 : 0;
+    const int sb = env_switch("HELIX_STATE_BLOCKS");
+    if (sb >= 0) t.state_blocks = sb > 0 ? 1 : 0;
     return t;
 }
 
@@ -291,20 +297,33 @@ namespace {
 int choose_walk_len(const helix_scan_desc& d, int cpg);
 }
 
-int n_state_blocks(const helix_scan_desc& d) {
-    if (d.d_state <= HELIX_N_MAX) return 1;
+namespace {
+bool state_blocks_on(const helix_ctx* ctx, const helix_scan_desc& d) {
+    if (d.d_state > HELIX_N_MAX) return true;   // the gate admits fp32 storage and scalar A only
+    if (d.d_state <= HELIX_N_BLOCK || d.io_dtype != HELIX_F32 || d.a_form != HELIX_A_SCALAR_PER_HEAD)
+        return false;
+    // Measured at L=8192 H=64 P=64 G=8, d_state 160, 192 and 256: blocks of
+    // 128 and less took 0.28-0.30 ms against 0.39-0.41 on the bf16 path, and
+    // 0.54-0.55 against 0.71-0.72 on the fp32 path (the d_state 256 kernels
+    // are the per-item Pass A and, on the fp32 path, an fp32-MFMA Pass C).
+    return tuning_of(ctx).state_blocks != 0;
+}
+}  // namespace
+
+int n_state_blocks(const helix_ctx* ctx, const helix_scan_desc& d) {
+    if (!state_blocks_on(ctx, d)) return 1;
     const int nb0 = (d.d_state + HELIX_N_BLOCK - 1) / HELIX_N_BLOCK;
     const int base = ((d.d_state + nb0 - 1) / nb0 + 7) / 8 * 8;   // <= HELIX_N_BLOCK
     return (d.d_state + base - 1) / base;
 }
 
-helix_scan_desc state_block(const helix_scan_desc& d, int k, int* n0) {
+helix_scan_desc state_block(const helix_ctx* ctx, const helix_scan_desc& d, int k, int* n0) {
     helix_scan_desc b = d;
-    const int nb = n_state_blocks(d);
+    const int nb = n_state_blocks(ctx, d);
     if (nb > 1) {
         const int base = ((d.d_state + nb - 1) / nb + 7) / 8 * 8;
         b.d_state = std::min(base, d.d_state - k * base);
-        b.backend = HELIX_BACKEND_SGMMA;
+        if (d.d_state > HELIX_N_MAX) b.backend = HELIX_BACKEND_SGMMA;
         if (n0) *n0 = k * base;
     } else if (n0) {
         *n0 = 0;
@@ -312,11 +331,15 @@ helix_scan_desc state_block(const helix_scan_desc& d, int k, int* n0) {
     return b;
 }
 
-helix_scan_desc plan_desc(const helix_scan_desc& d) { return state_block(d, 0, nullptr); }
+helix_scan_desc plan_desc(const helix_ctx* ctx, const helix_scan_desc& d) { return state_block(ctx, d, 0, nullptr); }
 
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d) {
-    // d_state above HELIX_N_MAX: the fp32 path's kernels of its blocks.
-    if (d.d_state > HELIX_N_MAX) return select_traits(ctx, plan_desc(d));
+    // Blocks of state indices: the kernels of their blocks.
+    if (n_state_blocks(ctx, d) > 1) return select_traits_unblocked(ctx, plan_desc(ctx, d));
+    return select_traits_unblocked(ctx, d);
+}
+
+const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d) {
     const helix_tuning& tu = tuning_of(ctx);
     const TraitTable& tt = table();
     const int k = np_index(d.d_state);
@@ -783,9 +806,10 @@ extern "C" size_t helix_scan_scratch_size(helix_ctx* ctx, const helix_scan_desc*
     if (!d || !d->multipass) return 0;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     if (tr.k_single) return 0;
-    // Above HELIX_N_MAX the blocks run one after another in the same
-    // scratch: the largest block's plan.
-    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(*d), tr).total_bytes;
+    // Blocks run one after another in the same scratch: the largest block's
+    // plan. (Where y overlaps an input, up to HELIX_N_MAX, the encoder runs
+    // the one-launch single pass instead, which needs none.)
+    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(ctx, *d), tr).total_bytes;
 }
 
 extern "C" helix_backend helix_ctx_select_backend(helix_ctx* ctx, const helix_scan_desc* d) {

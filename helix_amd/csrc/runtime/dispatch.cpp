@@ -82,8 +82,9 @@ bool y_overlaps_others(const helix_scan_desc& d, const void* y, const void* x, c
 }
 
 // One launch sequence for d_state <= HELIX_N_MAX, or for one block of state
-// indices of a larger d_state (block: d is helix::rt::state_block's
-// descriptor, already gated as part of the caller's; y_acc: add into y).
+// indices (inner: d is helix::rt::state_block's descriptor or the single-pass
+// form of the caller's, already gated as part of it; no state tiles in y;
+// y_acc: add into y; unblocked: d itself even where blocks would apply).
 // scratch_sized: the scratch is the library's own fixed array, already known
 // to hold the plan (helix_scan_encode_noalloc), so its allocation is not
 // queried.
@@ -94,12 +95,12 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
                         helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
                         helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
                         helix_tensor s1, helix_tensor scratch, bool scratch_sized, size_t budget_cap,
-                        bool block, bool y_acc, bool dry) {
+                        bool inner, bool y_acc, bool dry, bool unblocked = false) {
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
     }
-    if (!block && !helix_scan_supported(ctx, d)) {
+    if (!inner && !helix_scan_supported(ctx, d)) {
         set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
         return HELIX_ERR_UNSUPPORTED_SHAPE;
     }
@@ -126,7 +127,9 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
         return HELIX_ERR_INVALID_ARG;
     }
 
-    const HelixMatmulTraits* trp = &helix::rt::select_traits(ctx, *d);
+    // unblocked: d itself, where blocks of state indices would otherwise apply.
+    const HelixMatmulTraits* trp =
+        unblocked ? &helix::rt::select_traits_unblocked(ctx, *d) : &helix::rt::select_traits(ctx, *d);
     auto fn = [&](const char* name) -> hipFunction_t {
         if (!name) return nullptr;
         auto it = ctx->kernels.find(name);
@@ -141,7 +144,7 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
     // the one-launch path.
     helix::rt::MultipassPlan yplan;
     bool ytile = false;
-    if (trp->k_single && !block) {   // a block adds into y: no tiles there
+    if (trp->k_single && !inner) {   // inner: a block adds into y, or y overlaps an input; no tiles there
         const HelixMatmulTraits* ytr = nullptr;
         yplan = helix::rt::plan_ytile(ctx, *d, *trp, &ytr);
         ytile = ytr && (reinterpret_cast<uintptr_t>(dptr(y)) & 15) == 0 &&
@@ -219,7 +222,8 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
         }
     }
 
-    hipFunction_t fA = fn(tr.k_chunk_state), fB = fn(tr.k_state_scan), fC = fn(tr.k_chunk_out);
+    hipFunction_t fA = fn(tr.k_chunk_state), fB = fn(tr.k_state_scan),
+                  fC = fn(y_acc && tr.k_chunk_out_acc ? tr.k_chunk_out_acc : tr.k_chunk_out);
     if (!fA || !fB || !fC) {
         set_error(ctx, "kernel not resolved in code object");
         return HELIX_ERR_PIPELINE;
@@ -378,10 +382,27 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
                          helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
                          helix_tensor s1, helix_tensor scratch, bool scratch_sized = false,
                          size_t budget_cap = SIZE_MAX) {
-    const int nb = helix::rt::n_state_blocks(*d);
+    const int nb = helix::rt::n_state_blocks(ctx, *d);
     if (nb == 1)
         return encode_one(ctx, stream, d, s0, x, dt, A, B, C, ids, y, s1, scratch, scratch_sized, budget_cap,
-                          /*block=*/false, /*y_acc=*/false, /*dry=*/false);
+                          /*inner=*/false, /*y_acc=*/false, /*dry=*/false);
+    // Up to HELIX_N_MAX blocks are a choice: where y overlaps an input (in
+    // place over x, say) d runs as the one-launch single pass instead, which
+    // reads each chunk of x before it writes that chunk's y and needs no
+    // scratch (helix_scan_scratch_size sizes the blocks' plan only).
+    const bool overlap = y_overlaps_others(*d, dptr(y), dptr(x), dptr(dt), dptr(A), dptr(B), dptr(C), dptr(s0),
+                                           dptr(ids), dptr(s1));
+    if (overlap && d->d_state <= HELIX_N_MAX) {
+        if (!helix_scan_supported(ctx, d)) {
+            set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
+            return HELIX_ERR_UNSUPPORTED_SHAPE;
+        }
+        helix_scan_desc one = *d;
+        one.multipass = false;
+        one.backend = HELIX_BACKEND_SGMMA;
+        return encode_one(ctx, stream, &one, s0, x, dt, A, B, C, ids, y, s1, scratch, scratch_sized, budget_cap,
+                          /*inner=*/true, /*y_acc=*/false, /*dry=*/false, /*unblocked=*/true);
+    }
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
@@ -390,8 +411,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         set_error(ctx, "descriptor not supported (see helix_ctx_backend_desc)");
         return HELIX_ERR_UNSUPPORTED_SHAPE;
     }
-    if (y_overlaps_others(*d, dptr(y), dptr(x), dptr(dt), dptr(A), dptr(B), dptr(C), dptr(s0), dptr(ids),
-                          dptr(s1))) {
+    if (overlap) {
         set_error(ctx, "y overlaps an input or s1; with d_state above " + std::to_string(HELIX_N_MAX) +
                            " y accumulates over blocks of state indices and must be a buffer of its own");
         return HELIX_ERR_INVALID_ARG;
@@ -399,13 +419,13 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     for (int pass = 0; pass < 2; ++pass) {   // pass 0 checks every block, pass 1 enqueues them
         for (int k = 0; k < nb; ++k) {
             int n0 = 0;
-            const helix_scan_desc sub = helix::rt::state_block(*d, k, &n0);
+            const helix_scan_desc sub = helix::rt::state_block(ctx, *d, k, &n0);
             auto at_n0 = [n0](helix_tensor t) {
                 if (t.buf) t.offset += (uint64_t)n0 * sizeof(float);
                 return t;
             };
             const helix_status st = encode_one(ctx, stream, &sub, at_n0(s0), x, dt, A, at_n0(B), at_n0(C), ids, y,
-                                               at_n0(s1), scratch, scratch_sized, budget_cap, /*block=*/true,
+                                               at_n0(s1), scratch, scratch_sized, budget_cap, /*inner=*/true,
                                                /*y_acc=*/k > 0, /*dry=*/pass == 0);
             if (st != HELIX_OK) return st;
         }
@@ -442,7 +462,7 @@ size_t noalloc_scratch_size(helix_ctx* ctx, const helix_scan_desc* d) {
     if (!d->multipass) return 0;
     const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
     if (tr.k_single) return 0;
-    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(*d), tr, HELIX_NOALLOC_SCRATCH_BYTES).total_bytes;
+    return helix::rt::plan_multipass(ctx, helix::rt::plan_desc(ctx, *d), tr, HELIX_NOALLOC_SCRATCH_BYTES).total_bytes;
 }
 
 }  // namespace
@@ -492,8 +512,8 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     std::memset(out, 0, sizeof(*out));
     // Above HELIX_N_MAX: the plan of one block (the largest), run once per
     // block; the blocks add into y, so the single pass keeps no tiles there.
-    const int nb = helix::rt::n_state_blocks(*d);
-    const helix_scan_desc pd = helix::rt::plan_desc(*d);
+    const int nb = helix::rt::n_state_blocks(ctx, *d);
+    const helix_scan_desc pd = helix::rt::plan_desc(ctx, *d);
     out->state_blocks = nb;
     const HelixMatmulTraits* ytr = nullptr;
     const helix::rt::MultipassPlan yplan =

@@ -33,6 +33,8 @@ struct helix_tuning {
     int  f32_walk    = -1;     // HELIX_F32_WALK=0 / 1: the fp32 path's chunk-parallel Pass C / walk
                                // (on per-chunk states stored by Pass A) at d_state 128
     int  ytile       = -1;     // HELIX_1PASS_Y=0: the single pass in its one-launch form only
+    int  state_blocks = -1;    // HELIX_STATE_BLOCKS=0|1: d_state 129..256 (fp32 storage,
+                               // scalar A) as blocks of at most 128 state indices, or not
 };
 
 struct helix_ctx {
@@ -56,6 +58,9 @@ struct HelixMatmulTraits {
     const char*   k_chunk_state;   // Pass A
     const char*   k_state_scan;    // Pass B
     const char*   k_chunk_out;     // Pass C
+    // Pass C of a block of state indices after the first, which adds into y
+    // with y loaded ahead (null: k_chunk_out adds through y_acc itself).
+    const char*   k_chunk_out_acc;
     bool          bf16_state;      // s_local kept in bf16 (Pass C takes bf16 operands)
     const char*   mfma_a;          // MFMA instruction of Pass A
     const char*   mfma_c;          // MFMA instruction of Pass C
@@ -100,6 +105,9 @@ const char* const* all_kernel_names(size_t* count);
 // not serviceable. A pure function of the context's tuning and the
 // descriptor; ctx == nullptr plans with the default tuning.
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d);
+// The same for d run in one launch sequence (d_state <= HELIX_N_MAX), whether
+// or not blocks of state indices would apply.
+const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d);
 
 // How the multipass scan is tiled over the sequence (see helix_params.h):
 // super-chunk groups bound live scratch; segments of seg_len chunks are the
@@ -150,20 +158,24 @@ MultipassPlan plan_ytile(const helix_ctx* ctx, const helix_scan_desc& d, const H
                          const HelixMatmulTraits** tr_out);
 
 
-// d_state above HELIX_N_MAX (fp32 storage, scalar A): the recurrence is
-// independent per state index and y sums C_n h_n over them, so the scan runs
-// once per block of state indices, each block adding its share into y
-// (HelixScanParams::y_acc). n_state_blocks is 1 up to HELIX_N_MAX; otherwise
-// the blocks are equal (multiples of 8, at most HELIX_N_BLOCK, which runs the
-// d_state <= 128 kernels). state_block is block k's descriptor: d_state the
-// block's size, strides unchanged (s_s[1] stays the caller's d_state, the
-// row length of s0 and s1), backend the fp32 path; *n0 (if given) is its
-// first state index, the element offset of B, C, s0 and s1.
-int n_state_blocks(const helix_scan_desc& d);
-helix_scan_desc state_block(const helix_scan_desc& d, int k, int* n0);
-// The descriptor the plan and kernels are chosen for: block 0 above
-// HELIX_N_MAX (the largest block), else d itself.
-helix_scan_desc plan_desc(const helix_scan_desc& d);
+// Blocks of state indices (fp32 storage, scalar A): the recurrence is
+// independent per state index and y sums C_n h_n over them, so the scan can
+// run once per block of state indices, each block adding its share into y
+// (HelixScanParams::y_acc). Above HELIX_N_MAX it must (one launch serves at
+// most 256); from HELIX_N_BLOCK + 1 up to HELIX_N_MAX it may, where the
+// blocks' d_state <= 128 kernels beat the d_state 256 ones
+// (HELIX_STATE_BLOCKS pins it). n_state_blocks is 1 where no blocks apply;
+// otherwise the blocks are equal (multiples of 8, at most HELIX_N_BLOCK).
+// state_block is block k's descriptor: d_state the block's size, strides
+// unchanged (s_s[1] stays the caller's d_state, the row length of s0 and
+// s1), backend the fp32 path above HELIX_N_MAX (the caller's otherwise); *n0
+// (if given) is its first state index, the element offset of B, C, s0 and
+// s1.
+int n_state_blocks(const helix_ctx* ctx, const helix_scan_desc& d);
+helix_scan_desc state_block(const helix_ctx* ctx, const helix_scan_desc& d, int k, int* n0);
+// The descriptor the plan and kernels are chosen for: block 0 (the largest)
+// where blocks apply, else d itself.
+helix_scan_desc plan_desc(const helix_ctx* ctx, const helix_scan_desc& d);
 
 // Fills the kernel-side params from the public descriptor. Returns false and
 // sets *why when a launch dimension would exceed the hardware grid limits.

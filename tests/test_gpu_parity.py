@@ -100,6 +100,11 @@ MODES = [
     ("bf16/nocopy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_WALK_BCCOPY": "0"}, True),
     ("bf16/copy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_WALK_BCCOPY": "1"}, True),
     ("bf16/copy/sm", HELIX_BACKEND_MPP, 1, "short", {"HELIX_WALK_BCCOPY": "1"}, True),
+    # d_state 129..256 runs as blocks of at most 128 state indices by default;
+    # these pin one launch sequence on the d_state 256 kernels.
+    ("fp32/n256/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_STATE_BLOCKS": "0"}, True),
+    ("bf16/n256/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_STATE_BLOCKS": "0"}, True),
+    ("1pass/n256/long", HELIX_BACKEND_AUTO, None, "long", {"HELIX_STATE_BLOCKS": "0", "HELIX_1PASS_Y": "0"}, False),
     # Opt-in: Pass A on two split planes (three products), s1 at the wider bound.
     ("bf16/x3", HELIX_BACKEND_MPP, None, "short", {"HELIX_PASSA_SPLIT": "3"}, True),
     ("bf16/x3/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA_SPLIT": "3"}, True),

@@ -1,14 +1,17 @@
-"""d_state above 256: the scan runs as blocks of at most 128 state indices on
-the fp32 path, block k reading B, C and s0 and writing s1 at its first state
-index and adding its share of y into y (HelixScanParams::y_acc).
+"""Blocks of state indices: above d_state 256 the scan runs as blocks of at
+most 128 state indices on the fp32 path, and from 129 to 256 (fp32 storage,
+scalar A) on whichever path the descriptor asks for; block k reads B, C and
+s0 and writes s1 at its first state index and adds its share of y into y
+(HelixScanParams::y_acc; the walks of the later blocks load y ahead).
 
 Parity against the fp64 oracle (pinned at these d_state against the
 reference's own ref::scan and for the block decomposition itself in
 tests/test_oracle.py) at the fp32 per-element bound, on the multipass plan,
 the single pass, a plan of many super-chunk groups carried through s1, ids
-with a nonzero s0, and the no-allocation entry point; and the encoder's
-refusal of a y that overlaps an input, which the blocks would read after an
-earlier block had written y.
+with a nonzero s0, and the no-allocation entry point; the encoder's refusal
+of a y that overlaps an input above 256, which the blocks would read after an
+earlier block had written y, and its fallback to the one-launch single pass
+for such a y up to 256.
 """
 from __future__ import annotations
 
@@ -17,8 +20,9 @@ import pytest
 import torch
 
 from oracle import pyoracle as po
-from helix_amd.desc import HELIX_BACKEND_SGMMA, HELIX_ERR_INVALID_ARG, HELIX_OK, HELIX_TENSOR_NULL
-from gpu_harness import F32_ABS, F32_REL, T, ctx_for, run, upload
+from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_ERR_INVALID_ARG,
+                            HELIX_OK, HELIX_TENSOR_NULL)
+from gpu_harness import BF16_ABS, BF16_REL, F32_ABS, F32_REL, T, ctx_for, run, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +108,66 @@ def test_state_blocks_refuse_y_over_x(gpu, multipass):
     torch.cuda.synchronize()
     assert np.array_equal(xy.cpu().numpy(), p.x)
     assert torch.isnan(s1).all()
+
+
+# d_state 129..256: blocks by default, on the path the descriptor asks for.
+MID_SHAPES = [
+    (600, 2, 4, 64, 256, 2, "N=256: two blocks of 128"),
+    (700, 1, 4, 96, 192, 2, "N=192, P=96: two blocks of 96"),
+    (333, 2, 2, 64, 160, 1, "N=160: two blocks of 80, ragged last chunk"),
+]
+MID_MODES = [("bf16", HELIX_BACKEND_MPP, True), ("fp32", HELIX_BACKEND_SGMMA, True),
+             ("single", HELIX_BACKEND_AUTO, False)]
+
+
+@pytest.mark.parametrize("mode", MID_MODES, ids=[m[0] for m in MID_MODES])
+@pytest.mark.parametrize("shape", MID_SHAPES, ids=[s[-1] for s in MID_SHAPES])
+def test_blocks_up_to_256_parity(gpu, shape, mode):
+    label, backend, multipass = mode
+    p, d = _problem(shape, 5161, multipass)
+    d.backend = backend
+    assert gpu.plan_info(d).state_blocks == 2
+    y_ref, s_ref = po.scan(p, threads=0)
+    _, y, s1 = run(gpu, p, desc=d)
+    rel, ab = (BF16_REL, BF16_ABS) if label == "bf16" else (F32_REL, F32_ABS)
+    ry = po.allclose_ratio(y, y_ref, rel, ab)
+    rs = po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS)
+    print(f"{shape[-1]:44s} {label:6s} y ratio {ry:.3f}  s1 ratio {rs:.3f}", flush=True)
+    assert ry <= 1.0 and rs <= 1.0, (ry, rs)
+
+
+@pytest.mark.parametrize("backend", [HELIX_BACKEND_AUTO, HELIX_BACKEND_SGMMA], ids=["auto", "fp32"])
+def test_blocks_up_to_256_y_over_x_runs_one_launch(gpu, backend):
+    # y in place over x at d_state 256: the blocks cannot run (the second would
+    # read x where the first wrote y), so the encoder runs the one-launch
+    # single pass, which reads each chunk of x before it writes its y and
+    # needs no scratch. fp32-accurate, whatever the descriptor's backend.
+    shape = (500, 1, 4, 64, 256, 2, "in place")
+    p, d = _problem(shape, 5162)
+    d.backend = backend
+    assert list(d.s_x) == list(d.s_y) and d.seq_x == d.seq_y
+    y_ref, s_ref = po.scan(p, threads=0)
+    xy = upload(p.x)
+    s1 = torch.full(p.s_shape(), float("nan"), device="cuda")
+    dev = {k: upload(getattr(p, k)) for k in ("s0", "dt", "A", "B", "C")}
+    n = gpu.scratch_size(d)
+    scratch = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    rc = gpu.encode(torch.cuda.current_stream().cuda_stream, d, T(dev["s0"]), T(xy), T(dev["dt"]), T(dev["A"]),
+                    T(dev["B"]), T(dev["C"]), HELIX_TENSOR_NULL, T(xy), T(s1), T(scratch))
+    assert rc == HELIX_OK, gpu.last_error()
+    torch.cuda.synchronize()
+    _check(xy.cpu().numpy(), s1.cpu().numpy(), y_ref, s_ref, "N=256 y over x: one launch")
+
+
+def test_blocks_match_one_launch_sequence(gpu):
+    # Blocks and the d_state 256 kernels (HELIX_STATE_BLOCKS=0) agree on the
+    # fp32 path to the fp32 bound.
+    shape = (900, 2, 4, 64, 256, 2, "blocks vs one sequence")
+    p, d = _problem(shape, 5163)
+    d.backend = HELIX_BACKEND_SGMMA
+    native = ctx_for(gpu, HELIX_STATE_BLOCKS="0")
+    assert gpu.plan_info(d).state_blocks == 2 and native.plan_info(d).state_blocks == 1
+    _, y_a, s_a = run(gpu, p, desc=d)
+    _, y_b, s_b = run(native, p, desc=d)
+    assert po.allclose_ratio(y_a, y_b, F32_REL, F32_ABS) <= 1.0
+    assert po.allclose_ratio(s_a, s_b, F32_REL, F32_ABS) <= 1.0

@@ -204,10 +204,32 @@ def test_state_blocks_above_256(host, n, blocks, size, multipass):
         assert not host.supported(e)
 
 
-def test_state_blocks_up_to_256_unchanged(host):
-    for n in (8, 128, 136, 256):
-        k = host.plan_info(mp((300, 2, 4, 64, n, 2)))
-        assert k.state_blocks == 1
+def test_state_blocks_from_129(host):
+    # From d_state 129 to 256 blocks of at most 128 are the default with fp32
+    # storage and scalar A (faster than the d_state 256 kernels);
+    # HELIX_STATE_BLOCKS=0 keeps one launch sequence there.
+    native = tuned(HELIX_STATE_BLOCKS="0")
+    for n, blocks in ((8, 1), (128, 1), (136, 2), (192, 2), (256, 2)):
+        for backend in (HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA):
+            d = mp((300, 2, 4, 64, n, 2), backend)
+            k = host.plan_info(d)
+            assert k.state_blocks == blocks, (n, backend)
+            assert k.np == (64 if n <= 64 else 128)
+            assert native.plan_info(d).state_blocks == 1
+            # The caller's backend is kept up to 256.
+            assert host.select_backend(d) == (HELIX_BACKEND_SGMMA if backend == HELIX_BACKEND_SGMMA
+                                              else HELIX_BACKEND_MPP)
+    d = mp((300, 2, 4, 64, 256, 2))
+    assert host.plan_info(d).kernel_c == b"helix_scan_walk16_bf16_n128"
+    assert native.plan_info(d).kernel_c == b"helix_scan_walk16_bf16_n256"
+    # 16-bit storage and diagonal A keep one launch sequence.
+    e = mp((300, 2, 4, 64, 256, 2))
+    e.io_dtype = HELIX_BF16
+    assert host.plan_info(e).state_blocks == 1
+    f = abi.desc_init_c(300, 2, 4, 64, 256, 2)
+    f.multipass = False
+    assert host.plan_info(f).state_blocks == 2 and host.plan_info(f).launches == 2
+    native.close()
 
 
 def test_diagonal_a_runs_the_single_pass_walk(host):
@@ -287,19 +309,25 @@ def test_noalloc_host_checks(host):
     # only one that does not fit at one chunk per group is refused, before
     # anything is enqueued. A host-only context has no device for one that
     # fits. Config 4a itself fits (76 MiB).
+    # (d_state 256 cases with one launch sequence, HELIX_STATE_BLOCKS=0: in
+    # blocks of 128 the same shapes need far less.)
     t = [HelixTensor(0x1000 * (i + 1), 0) for i in range(9)]
+    native = tuned(HELIX_STATE_BLOCKS="0")
     assert 0 < host.scratch_size(mp(CONFIG_SHAPES["cfg4a"])) <= abi.NOALLOC_SCRATCH_BYTES
-    for shape, backend in (((4096, 14, 80, 64, 128, 1), HELIX_BACKEND_MPP),
-                           ((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)):
+    for shape, backend, c in (((4096, 14, 80, 64, 128, 1), HELIX_BACKEND_MPP, host),
+                              ((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA, native)):
         d = mp(shape, backend)
-        assert host.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
-        with env(HELIX_SCRATCH_MB=str(abi.NOALLOC_SCRATCH_BYTES >> 20)):
+        assert c.scratch_size(d) > abi.NOALLOC_SCRATCH_BYTES
+        with env(HELIX_SCRATCH_MB=str(abi.NOALLOC_SCRATCH_BYTES >> 20),
+                 HELIX_STATE_BLOCKS="0" if c is native else None):
             capped = abi.Context(host_only=True).plan_info(d)
         assert capped.n_groups > 1 and capped.total_bytes <= abi.NOALLOC_SCRATCH_BYTES
-        assert host.encode_noalloc(0, d, *t) == HELIX_ERR_NO_DEVICE
+        assert c.encode_noalloc(0, d, *t) == HELIX_ERR_NO_DEVICE
+    assert 0 < host.scratch_size(mp((8192, 1, 64, 64, 256, 8), HELIX_BACKEND_SGMMA)) <= abi.NOALLOC_SCRATCH_BYTES
     huge = mp((64, 1, 4096, 64, 256, 1), HELIX_BACKEND_SGMMA)   # one chunk's state is 256 MiB
-    assert host.encode_noalloc(0, huge, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
-    assert "HELIX_NOALLOC_SCRATCH_BYTES" in host.last_error()
+    assert native.encode_noalloc(0, huge, *t) == HELIX_ERR_SCRATCH_TOO_SMALL
+    assert "HELIX_NOALLOC_SCRATCH_BYTES" in native.last_error()
+    native.close()
     fits = mp(CONFIG_SHAPES["cfg2"])
     assert 0 < host.scratch_size(fits) <= abi.NOALLOC_SCRATCH_BYTES
     assert host.encode_noalloc(0, fits, *t) == HELIX_ERR_NO_DEVICE
@@ -357,16 +385,22 @@ def test_backend_selection(host):
     assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
     assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
             == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+    # d_state 256: blocks of 128 by default, one launch sequence on the d_state
+    # 256 kernels with HELIX_STATE_BLOCKS=0.
+    native = tuned(HELIX_STATE_BLOCKS="0")
     assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+    assert (native.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
             == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
-    assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1)))
+    assert (native.backend_desc(mp((64, 1, 1, 64, 256, 1)))
             == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
     x3 = tuned(HELIX_PASSA_SPLIT="3")
     assert x3.backend_desc(mp(shape)) == ("mfma bf16 pass C, chunk walk, pass A bf16x3 (narrower state: opt-in) "
                                           "(d_state<=128)")
     assert x3.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x3agg_n128"
-    assert (host.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
+    assert (native.backend_desc(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
             == "mfma fp32, pass A bf16x6 (d_state<=256)")
+    native.close()
     # d_state 64 walks too, where the plan walks more than one chunk; one
     # chunk (a single-chunk sequence, or config 0's four chunks over eight
     # heads) keeps the chunk-parallel Pass C unless HELIX_F32_WALK=1.
@@ -431,7 +465,8 @@ def test_backend_selection(host):
     recs = S * (-(-L // 64)) * H * 64
     assert k.rec_bytes == 8 * recs
     assert host.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).rec_bytes == 16 * recs
-    assert host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
+    native = tuned(HELIX_STATE_BLOCKS="0")   # d_state 256 on its own kernels
+    assert native.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA)).rec_bytes == 0
     assert kc.total_bytes >= kc.s_seg_bytes + kc.bccopy_bytes and kc.total_bytes > k.total_bytes
     k0 = tuned(HELIX_WALK_BCCOPY="0").plan_info(mp(CONFIG_SHAPES["cfg4a"]))
     assert b"_bc_" not in k0.kernel_a and b"_bc_" not in k0.kernel_c and k0.bccopy_bytes == 0
@@ -439,8 +474,9 @@ def test_backend_selection(host):
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6agg_r64_n128", b"helix_scan_walk_x6_n128")
     k = tuned(HELIX_F32_WALK="0").plan_info(mp(shape, HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_hb_x6f32_n128", b"helix_chunk_out_x6_n128")
-    k = host.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
+    k = native.plan_info(mp((64, 1, 1, 64, 256, 1), HELIX_BACKEND_SGMMA))
     assert (k.kernel_a, k.kernel_c) == (b"helix_chunk_state_x6f32_n256", b"helix_chunk_out_f32_n256")
+    native.close()
     # multipass=false (the descriptor default) runs the fp32 single-pass
     # kernel under AUTO and SGMMA; an explicit MPP request is declined there
     # (reference caps.mm:66,145-147).
@@ -457,11 +493,13 @@ def test_backend_selection(host):
     # where every segment has the rows of a tile: 65 rows at d_state 64 and a
     # 64-channel slab, 129 at 128. 100 tokens leave only d_state 64 there; the
     # one-launch kernel stays named as the encoder's fallback.
-    for n, want, in_y in ((64, 64, 1), (40, 64, 1), (96, 128, 0), (256, 256, 0)):
+    # d_state 256 runs as two blocks of 128, each one launch.
+    for n, want, in_y in ((64, 64, 1), (40, 64, 1), (96, 128, 0), (256, 128, 0)):
         d = mp((100, 1, 2, 64, n, 1))
         d.multipass = False
         k = host.plan_info(d)
-        assert (k.np, k.launches, k.total_bytes, k.n_groups, k.state_in_y) == (want, 3 if in_y else 1, 0, 1, in_y)
+        launches = 3 if in_y else 2 if n > 128 else 1
+        assert (k.np, k.launches, k.total_bytes, k.n_groups, k.state_in_y) == (want, launches, 0, 1, in_y)
         assert k.kernel_1pass == b"helix_scan_1pass_f32_n%d" % want
         if in_y:
             assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
@@ -493,6 +531,7 @@ def test_backend_selection(host):
 # ---------------------------------------------------------------------------
 
 def test_bc_copy_condition(host):
+    native = tuned(HELIX_STATE_BLOCKS="0")   # d_state 256 on its own kernels
     # Up to d_state 128 the head-block Pass A writes the copies when more than
     # eight (head, P slab) items share a group's rows (K = heads_per_group *
     # n_pslab > 8). At d_state 256 the per-item Pass A needs the K workgroups
@@ -504,7 +543,7 @@ def test_bc_copy_condition(host):
                                ((8, 64, 256, 1), True), ((4, 64, 256, 1), False), ((2, 128, 256, 1), False),
                                ((4, 128, 256, 1), True)]:
         d = mp((4096, 1, H, P, N, G))
-        k = host.plan_info(d)
+        k = (native if N > 128 else host).plan_info(d)
         assert (k.bccopy_bytes > 0) == copy, (H, P, N, G)
         assert k.kernel_c.endswith(b"_n%d" % k.np)
         assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
