@@ -149,8 +149,11 @@ HELIX_DEV int tri_jb(int idx) {
 // part (per-phase cycle counts).
 // Two waves per SIMD hide each other's staging, preamble and load latencies.
 // NWV = 4 (diagonal A, d_state 256): every wave does all four parts.
-template <int NP, bool DIAG, typename IO = float, int NWV = 4>
+// YACC: a block of state indices after the first (fp32 storage, p.y_acc): each
+// y wave loads y of its rows at the top of the chunk and adds it at the store.
+template <int NP, bool DIAG, typename IO = float, int NWV = 4, bool YACC = false>
 __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
+    static_assert(!YACC || sizeof(IO) == 4, "y accumulates in fp32 storage only");
     static_assert(NWV == 4 || (NWV == 8 && !DIAG), "eight waves on the scalar-A path only");
     constexpr int NT  = NP / 16;           // 16-row state tiles
     constexpr int NTW = NT / 4;            // state tiles state wave sw advances: NTW sw .. NTW sw + NTW - 1
@@ -313,6 +316,19 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
     for (int c = 0; c < n_ch; ++c) {
         const int t0   = c * HELIX_CS;
         const int tlen = min(HELIX_CS, p.n_tok - t0);
+        f32x4 yprev = zero4();
+        if constexpr (YACC) {
+            if (ywave) {
+                const helix_rsrc ryp = make_rsrc(b.y + seq * p.seq_y + h * p.s_y[1] + (long long)t0 * p.s_y[0] +
+                                                     (long long)p0 * p.s_y[2],
+                                                 ((tlen - 1) * sy0 + (pw - 1) * sy2 + 1) * 4u);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tb + 4 * g4 + r;
+                    yprev[r] = buf_f32(ryp, store_off_if_lt((t * sy0 + l16 * sy2) * 4, t, tlen, l16, pw), 0);
+                }
+            }
+        }
 
         // ---- chunk preamble and staging ------------------------------------
         // dt = 0 past tlen, so Lcum stays at Lcum[tlen-1] there and dtX rows
@@ -657,14 +673,21 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
             const helix_rsrc ry = make_rsrc(reinterpret_cast<IO*>(b.y) + seq * p.seq_y + h * p.s_y[1] +
                                                 (long long)t0 * p.s_y[0] + (long long)p0 * p.s_y[2],
                                             bytes);
-            with_y_acc(p, [&](auto acc_on) {
+            auto put = [&](auto acc_on) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = 16 * tb + 4 * g4 + r;
                     y_store<IO, decltype(acc_on)::value>(
                         ry, ya[r], store_off_if_lt((t * sy0 + l16 * sy2) * ES, t, tlen, l16, pw), 0);
                 }
-            });
+            };
+            if constexpr (YACC) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ya[r] += yprev[r];
+                put(std::false_type{});
+            } else {
+                with_y_acc(p, put);
+            }
         }
         }
         // The next chunk's staging overwrites C, B/M and dtX. X6 needs no
@@ -712,9 +735,19 @@ __device__ __forceinline__ void scan_1pass_impl(const HelixScanParams& p, const 
         scan_1pass_impl<NP, true>(p, b);                                                        \
     }
 
+// The one-launch kernel of the second and later blocks of state indices
+// (at most HELIX_N_BLOCK = 128 wide).
+#define HELIX_SCAN_1PASS_ACC(NP)                                                                \
+    extern "C" __global__ __launch_bounds__(64 * HELIX_1PASS_WAVES(NP)) void helix_scan_1pass_f32_acc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                \
+        scan_1pass_impl<NP, false, float, HELIX_1PASS_WAVES(NP), true>(p, b);                   \
+    }
+
 HELIX_SCAN_1PASS(64)
 HELIX_SCAN_1PASS(128)
 HELIX_SCAN_1PASS(256)
+HELIX_SCAN_1PASS_ACC(64)
+HELIX_SCAN_1PASS_ACC(128)
 HELIX_SCAN_1PASS_IO(64)
 HELIX_SCAN_1PASS_IO(128)
 HELIX_SCAN_1PASS_IO(256)

@@ -105,6 +105,7 @@ struct TraitTable {
                                                                 : "v_mfma_f32_16x16x4_f32";
                 t.np = kNps[k];
                 t.k_single = kernel(std::string("helix_scan_1pass_") + (io == 0 ? "f32_" : kIoTag[io]) + "n" + np);
+                if (io == 0 && kNps[k] <= HELIX_N_BLOCK) t.k_single_acc = kernel("helix_scan_1pass_f32_acc_n" + np);
                 t.single_threads = 64 * HELIX_1PASS_WAVES(kNps[k]);
             }
             if (k < 2) {

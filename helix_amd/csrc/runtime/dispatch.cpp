@@ -144,7 +144,10 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
     // the one-launch path.
     helix::rt::MultipassPlan yplan;
     bool ytile = false;
-    if (trp->k_single && !inner) {   // inner: a block adds into y, or y overlaps an input; no tiles there
+    // Not for a block that adds into y (y holds the sum so far); the first
+    // block of a single pass may keep its tiles in y, which it then
+    // overwrites with its share.
+    if (trp->k_single && !y_acc) {
         const HelixMatmulTraits* ytr = nullptr;
         yplan = helix::rt::plan_ytile(ctx, *d, *trp, &ytr);
         ytile = ytr && (reinterpret_cast<uintptr_t>(dptr(y)) & 15) == 0 &&
@@ -154,7 +157,7 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
     }
     const HelixMatmulTraits& tr = *trp;
     if (tr.k_single) {
-        hipFunction_t f1 = fn(tr.k_single);
+        hipFunction_t f1 = fn(y_acc && tr.k_single_acc ? tr.k_single_acc : tr.k_single);
         if (!f1) {
             set_error(ctx, "kernel not resolved in code object");
             return HELIX_ERR_PIPELINE;
@@ -517,7 +520,7 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
     out->state_blocks = nb;
     const HelixMatmulTraits* ytr = nullptr;
     const helix::rt::MultipassPlan yplan =
-        tr.k_single && nb == 1 ? helix::rt::plan_ytile(ctx, pd, tr, &ytr) : helix::rt::MultipassPlan{};
+        tr.k_single ? helix::rt::plan_ytile(ctx, pd, tr, &ytr) : helix::rt::MultipassPlan{};
     if (tr.k_single && !ytr) {
         out->n_chunks = (d->n_tok + HELIX_CS - 1) / HELIX_CS;
         out->chunks_per_group = out->n_chunks;
@@ -559,7 +562,9 @@ extern "C" helix_status helix_scan_plan_info(helix_ctx* ctx, const helix_scan_de
         out->rec_bytes = pl.rec_elems * sizeof(float);
     }
     const bool fuse_b = helix::rt::fuse_b_on(ctx, tp, pl);   // as helix_scan_encode decides
-    out->launches = (fuse_b ? 2 : 3 * pl.n_groups) * nb;
+    // With blocks of state indices a single pass keeps tiles in y for its
+    // first block only; the others run kernel_1pass.
+    out->launches = ytr ? (fuse_b ? 2 : 3) + (nb - 1) : (fuse_b ? 2 : 3 * pl.n_groups) * nb;
     out->np = tp.np;
     out->kernel_a = tp.k_chunk_state;
     out->kernel_b = fuse_b ? nullptr : tp.k_state_scan;

@@ -73,6 +73,9 @@ struct HelixMatmulTraits {
     // caps.mm:18-25). Set only in the single-pass trait set, where the three
     // pass names are null.
     const char*   k_single;
+    // Its form for a block of state indices after the first, which adds into
+    // y with y loaded ahead (null: k_single adds through y_acc itself).
+    const char*   k_single_acc;
     int           single_threads;  // its workgroup size (64 x waves)
     // Heads per workgroup of a walking Pass C; 0 means HELIX_WALK_HPW(np).
     int           walk_hpw;

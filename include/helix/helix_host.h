@@ -57,12 +57,16 @@ typedef struct {
                                    tile); helix_scan_encode runs kernel_1pass
                                    alone instead when y is not 16-byte aligned
                                    or overlaps x, dt, A, B, C, s0, ids or s1    */
-    int32_t  state_blocks;      /* 1 up to d_state 256; above it, the number of
-                                   blocks of state indices (equal, multiples of
-                                   8, at most 128) the scan runs as, one after
-                                   another on the fp32 path, each adding its
-                                   share into y. The other fields describe one
-                                   block (the largest), launches all of them  */
+    int32_t  state_blocks;      /* the number of blocks of state indices (equal,
+                                   multiples of 8, at most 128) the scan runs
+                                   as, one after another, each adding its share
+                                   into y: 1 up to d_state 128; more above 256
+                                   (the fp32 path) and, with fp32 storage and
+                                   scalar A, from 129 (HELIX_STATE_BLOCKS=0:
+                                   1 up to 256). The other fields describe one
+                                   block (the largest); launches counts all of
+                                   them. A single pass keeps its tiles in y
+                                   (state_in_y) for the first block only     */
 } helix_plan_info;
 
 #define HELIX_PASS_B_LAUNCHED 0   /* kernel_b, between Pass A and Pass C         */
