@@ -200,6 +200,18 @@ struct TraitTable {
                         t.rec_kind = 1;
                     }
         }
+        // What helix_ctx_backend_desc reports for a descriptor run as blocks
+        // of state indices on these kernels.
+        auto blocks_name = [&](HelixMatmulTraits& t) {
+            if (t.name) t.name_blocks = keep(std::string(t.name) + ", in blocks of at most " +
+                                             std::to_string(HELIX_N_BLOCK) + " state indices");
+        };
+        for (auto& a : single) for (auto& t : a) blocks_name(t);
+        for (auto& t : f32) blocks_name(t);
+        for (auto& t : f32walk) blocks_name(t);
+        for (auto& t : ysingle) blocks_name(t);
+        for (auto& t : diag) blocks_name(t);
+        for (auto& a : bf16) for (auto& b2 : a) for (auto& c2 : b2) for (auto& t : c2) blocks_name(t);
     }
 };
 
@@ -822,5 +834,6 @@ extern "C" helix_backend helix_ctx_select_backend(helix_ctx* ctx, const helix_sc
 extern "C" const char* helix_ctx_backend_desc(helix_ctx* ctx, const helix_scan_desc* d) {
     if (!ctx || !d) return "unavailable (null context)";
     if (!helix_scan_supported(ctx, d)) return "declined (shape unsupported)";
-    return helix::rt::select_traits(ctx, *d).name;
+    const HelixMatmulTraits& tr = helix::rt::select_traits(ctx, *d);
+    return helix::rt::n_state_blocks(ctx, *d) > 1 && tr.name_blocks ? tr.name_blocks : tr.name;
 }

@@ -55,6 +55,7 @@ struct helix_ctx {
 struct HelixMatmulTraits {
     helix_backend backend;
     const char*   name;            // what helix_ctx_backend_desc reports
+    const char*   name_blocks;     // the same for blocks of state indices
     const char*   k_chunk_state;   // Pass A
     const char*   k_state_scan;    // Pass B
     const char*   k_chunk_out;     // Pass C

@@ -392,7 +392,7 @@ def test_backend_selection(host):
     # 256 kernels with HELIX_STATE_BLOCKS=0.
     native = tuned(HELIX_STATE_BLOCKS="0")
     assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128), in blocks of at most 128 state indices")
     assert (native.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
             == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
     assert (native.backend_desc(mp((64, 1, 1, 64, 256, 1)))
