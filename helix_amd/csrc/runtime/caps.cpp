@@ -224,8 +224,9 @@ const TraitTable& table() {
 // HELIX_WALK_BCCOPY=0 / 1 switches them off / on where the kernels can. At
 // d_state 256 the per-item Pass A copies when the K = heads_per_group *
 // n_pslab workgroups of a chunk cover its 64 rows with two quads of four state
-// indices per thread (pass_a_x6.hip, copy_map).
-bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d) {
+// indices per thread (pass_a_x6.hip, copy_map). block: d is one block of
+// state indices of a larger d_state.
+bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d, bool block) {
     if (tu.bccopy == 0) return false;
     const long K = (long)(d.n_head / d.n_group) * ((d.head_dim + HELIX_HD - 1) / HELIX_HD);
     // The head-block Pass A (d_state <= 128) can copy at every shape (one
@@ -233,7 +234,11 @@ bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d) {
     // pay off when many walk workgroups read a chunk's rows (measured at
     // configs 4a and 4b, 80 and 27 heads per group: 45 and 56 us faster);
     // at 8 (config 2) the walk reading the fp32 rows itself is 3 us faster.
-    if (d.d_state <= 128) return tu.bccopy == 1 || K > 8;
+    // Blocks of state indices: at config 2's shape with d_state 256 in two
+    // blocks of 128, the walks reading their columns of the caller's rows took
+    // 81 and 103 us, on the copies 66-68 and 76-78 us, for 11-13 us more per
+    // Pass A (294-296 against 275-283 us a scan, three processes).
+    if (d.d_state <= 128) return tu.bccopy == 1 || K > 8 || block;
     return (64 + K - 1) / K * (d.d_state / 4) <= 2 * 256;
 }
 
@@ -348,11 +353,11 @@ helix_scan_desc plan_desc(const helix_ctx* ctx, const helix_scan_desc& d) { retu
 
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d) {
     // Blocks of state indices: the kernels of their blocks.
-    if (n_state_blocks(ctx, d) > 1) return select_traits_unblocked(ctx, plan_desc(ctx, d));
+    if (n_state_blocks(ctx, d) > 1) return select_traits_unblocked(ctx, plan_desc(ctx, d), /*block=*/true);
     return select_traits_unblocked(ctx, d);
 }
 
-const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d) {
+const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d, bool block) {
     const helix_tuning& tu = tuning_of(ctx);
     const TraitTable& tt = table();
     const int k = np_index(d.d_state);
@@ -371,7 +376,7 @@ const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const hel
                                     (tu.f32_walk < 0 && choose_walk_len(d, (d.n_tok + HELIX_CS - 1) / HELIX_CS) > 1));
         return walk ? tt.f32walk[k] : tt.f32[k];
     }
-    const int bc = io == 0 && bccopy_on(tu, d) ? 1 : 0;
+    const int bc = io == 0 && bccopy_on(tu, d, block) ? 1 : 0;
     return tt.bf16[io][tu.passa_split == 3 ? 0 : 1][bc][k];
 }
 

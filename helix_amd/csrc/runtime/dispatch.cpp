@@ -83,8 +83,9 @@ bool y_overlaps_others(const helix_scan_desc& d, const void* y, const void* x, c
 
 // One launch sequence for d_state <= HELIX_N_MAX, or for one block of state
 // indices (inner: d is helix::rt::state_block's descriptor or the single-pass
-// form of the caller's, already gated as part of it; no state tiles in y;
-// y_acc: add into y; unblocked: d itself even where blocks would apply).
+// form of the caller's, already gated as part of it; y_acc: add into y).
+// sel: the kernels d runs on (helix::rt::select_traits for the caller's
+// descriptor, select_traits_unblocked for a block or the single-pass form).
 // scratch_sized: the scratch is the library's own fixed array, already known
 // to hold the plan (helix_scan_encode_noalloc), so its allocation is not
 // queried.
@@ -95,7 +96,7 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
                         helix_tensor s0, helix_tensor x, helix_tensor dt, helix_tensor A,
                         helix_tensor B, helix_tensor C, helix_tensor ids, helix_tensor y,
                         helix_tensor s1, helix_tensor scratch, bool scratch_sized, size_t budget_cap,
-                        bool inner, bool y_acc, bool dry, bool unblocked = false) {
+                        bool inner, bool y_acc, bool dry, const HelixMatmulTraits& sel) {
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
         return HELIX_ERR_INVALID_ARG;
@@ -127,9 +128,7 @@ helix_status encode_one(helix_ctx* ctx, hipStream_t stream, const helix_scan_des
         return HELIX_ERR_INVALID_ARG;
     }
 
-    // unblocked: d itself, where blocks of state indices would otherwise apply.
-    const HelixMatmulTraits* trp =
-        unblocked ? &helix::rt::select_traits_unblocked(ctx, *d) : &helix::rt::select_traits(ctx, *d);
+    const HelixMatmulTraits* trp = &sel;
     auto fn = [&](const char* name) -> hipFunction_t {
         if (!name) return nullptr;
         auto it = ctx->kernels.find(name);
@@ -388,7 +387,7 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
     const int nb = helix::rt::n_state_blocks(ctx, *d);
     if (nb == 1)
         return encode_one(ctx, stream, d, s0, x, dt, A, B, C, ids, y, s1, scratch, scratch_sized, budget_cap,
-                          /*inner=*/false, /*y_acc=*/false, /*dry=*/false);
+                          /*inner=*/false, /*y_acc=*/false, /*dry=*/false, helix::rt::select_traits(ctx, *d));
     // Up to HELIX_N_MAX blocks are a choice: where y overlaps an input (in
     // place over x, say) d runs as the one-launch single pass instead, which
     // reads each chunk of x before it writes that chunk's y and needs no
@@ -404,7 +403,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
         one.multipass = false;
         one.backend = HELIX_BACKEND_SGMMA;
         return encode_one(ctx, stream, &one, s0, x, dt, A, B, C, ids, y, s1, scratch, scratch_sized, budget_cap,
-                          /*inner=*/true, /*y_acc=*/false, /*dry=*/false, /*unblocked=*/true);
+                          /*inner=*/true, /*y_acc=*/false, /*dry=*/false,
+                          helix::rt::select_traits_unblocked(ctx, one));
     }
     if (!s0.buf || !x.buf || !dt.buf || !A.buf || !B.buf || !C.buf || !y.buf || !s1.buf) {
         set_error(ctx, "null tensor (s0, x, dt, A, B, C, y and s1 are required)");
@@ -429,7 +429,8 @@ helix_status encode_core(helix_ctx* ctx, hipStream_t stream, const helix_scan_de
             };
             const helix_status st = encode_one(ctx, stream, &sub, at_n0(s0), x, dt, A, at_n0(B), at_n0(C), ids, y,
                                                at_n0(s1), scratch, scratch_sized, budget_cap, /*inner=*/true,
-                                               /*y_acc=*/k > 0, /*dry=*/pass == 0);
+                                               /*y_acc=*/k > 0, /*dry=*/pass == 0,
+                                               helix::rt::select_traits_unblocked(ctx, sub, /*block=*/true));
             if (st != HELIX_OK) return st;
         }
     }

@@ -110,8 +110,10 @@ const char* const* all_kernel_names(size_t* count);
 // descriptor; ctx == nullptr plans with the default tuning.
 const HelixMatmulTraits& select_traits(const helix_ctx* ctx, const helix_scan_desc& d);
 // The same for d run in one launch sequence (d_state <= HELIX_N_MAX), whether
-// or not blocks of state indices would apply.
-const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d);
+// or not blocks of state indices would apply; block: d is one block of state
+// indices of a larger d_state (state_block).
+const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const helix_scan_desc& d,
+                                                 bool block = false);
 
 // How the multipass scan is tiled over the sequence (see helix_params.h):
 // super-chunk groups bound live scratch; segments of seg_len chunks are the

@@ -115,6 +115,9 @@ MID_SHAPES = [
     (600, 2, 4, 64, 256, 2, "N=256: two blocks of 128"),
     (700, 1, 4, 96, 192, 2, "N=192, P=96: two blocks of 96"),
     (333, 2, 2, 64, 160, 1, "N=160: two blocks of 80, ragged last chunk"),
+    # 20 heads per group: the bf16 path's Pass A writes bf16 copies of each
+    # block's B and C columns for the walks.
+    (400, 1, 20, 64, 256, 1, "N=256, 20 heads per group: copies of B and C"),
 ]
 MID_MODES = [("bf16", HELIX_BACKEND_MPP, True), ("fp32", HELIX_BACKEND_SGMMA, True),
              ("single", HELIX_BACKEND_AUTO, False)]

@@ -221,8 +221,11 @@ def test_state_blocks_from_129(host):
             # The caller's backend is kept up to 256.
             assert host.select_backend(d) == (HELIX_BACKEND_SGMMA if backend == HELIX_BACKEND_SGMMA
                                               else HELIX_BACKEND_MPP)
+    # Each block reads 128 of the 256 columns of B's and C's rows: Pass A
+    # writes bf16 copies of its columns for the walks.
     d = mp((300, 2, 4, 64, 256, 2))
-    assert host.plan_info(d).kernel_c == b"helix_scan_walk16_bf16_n128"
+    assert host.plan_info(d).kernel_c == b"helix_scan_walk16_bf16_bc_n128"
+    assert tuned(HELIX_WALK_BCCOPY="0").plan_info(d).kernel_c == b"helix_scan_walk16_bf16_n128"
     assert native.plan_info(d).kernel_c == b"helix_scan_walk16_bf16_n256"
     # 16-bit storage and diagonal A keep one launch sequence.
     e = mp((300, 2, 4, 64, 256, 2))
@@ -551,6 +554,19 @@ def test_bc_copy_condition(host):
         assert k.kernel_c.endswith(b"_n%d" % k.np)
         assert (b"_bc_" in k.kernel_a) == copy and (b"_bc_" in k.kernel_c) == copy
         assert (b"_hb_" in k.kernel_a) == (N <= 128)
+    # A block of state indices reads d_state of each row's columns: copies at
+    # any K. A caller's B and C inside wider rows are planned as usual.
+    for G in (8, 1):
+        H = 8 * G
+        d = mp((4096, 1, H, 64, 256, G))
+        k = host.plan_info(d)
+        assert k.state_blocks == 2 and k.bccopy_bytes > 0 and b"_bc_" in k.kernel_c, G
+        assert tuned(HELIX_WALK_BCCOPY="0").plan_info(d).bccopy_bytes == 0
+        d = mp((4096, 1, H, 64, 128, G))
+        for s in (d.s_b, d.s_c):
+            s[0], s[1] = G * 256, 256
+        d.seq_b = d.seq_c = 4096 * G * 256
+        assert host.plan_info(d).bccopy_bytes == 0
     # Not with 16-bit storage (Pass C reads the caller's 16-bit B and C).
     d = mp((4096, 1, 64, 64, 128, 8))
     d.io_dtype = HELIX_BF16
