@@ -43,6 +43,7 @@ REF_TOKS = 1315051.0
 CFG = dict(L=8192, S=1, H=64, P=64, N=128, G=8)
 ARENA_BYTES = 4 << 30   # the headline workload's inputs, outputs and scratch fit
 Y_PLACES, Y_STEP = 4, 1 << 20   # y placements timed for the headline (1 MiB apart)
+COLD_FLUSH_BYTES = 1 << 30      # a copy of this size evicts the 256 MB Infinity Cache
 
 # BASELINE.json's configurations (config 4 in its two head-dim variants): shape,
 # the paths each is quoted on, and the distributions that differ from the common
@@ -160,6 +161,24 @@ def time_placements(v: Variant, steps: int, stream, ys):
         v.y = y0
     ts = [a.elapsed_time(b) for a, b in evs]
     return ts, [ts[k::len(ys)] for k in range(len(ys))]
+
+
+def time_cold(v: Variant, steps: int, stream, flush_bytes: int):
+    """Per-step event times (ms) of `steps` whole scans, each preceded, outside
+    its events, by a device copy of `flush_bytes` that evicts the 256 MB
+    Infinity Cache: the scan then reads its inputs from HBM, as a first call
+    on them would."""
+    src = torch.empty(flush_bytes, dtype=torch.uint8, device=v.y.device)
+    dst = torch.empty_like(src)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        dst.copy_(src)
+        a.record(stream)
+        v.encode(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
 
 
 def time_passes(v: Variant, steps: int, stream):
@@ -455,6 +474,9 @@ def main():
     ap.add_argument("--only-config", default=None, metavar="NAME",
                     help="run only the per-config report of this BASELINE config (0 1 2 3 4a 4b) and "
                          "print it: a process of its own for profiling one configuration")
+    ap.add_argument("--cold-steps", type=int, default=0, metavar="K",
+                    help="also time K scans of the bf16 and fp32 paths, each after a 1 GiB copy "
+                         "that evicts the Infinity Cache (reported as cold_cache)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MiB",
                     help="also run a plain device copy of this size (a known-traffic kernel "
                          "that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -685,6 +707,18 @@ def main():
             if rv["passes"]:
                 e["passes_us"] = pass_us(rv["passes"])
             out["variants"][v.name] = e
+    if args.cold_steps > 0:
+        # Steps that repeat one input find much of it in the 256 MB Infinity
+        # Cache (x alone is 128 MiB); these scans start with it evicted.
+        cold = {}
+        for name in ("bf16", "fp32"):
+            v = next(vv for vv in variants if vv.name == name)
+            warm_up(v, 100.0)
+            tc = statistics.median(time_cold(v, args.cold_steps, stream, COLD_FLUSH_BYTES))
+            cold[name] = {"ms_per_step": tc, "tok_s": S * L / (tc * 1e-3), "vs_warm": tc / results[name]["ms"]}
+        cold["flush"] = f"a {COLD_FLUSH_BYTES >> 20} MiB device copy before each timed scan, outside its events"
+        cold["steps"] = args.cold_steps
+        out["cold_cache"] = cold
     if args.config_steps > 0:
         out["configs"] = config_report(ctx, stream, dev, args.config_steps,
                                        min(args.warmup_ms, 100.0))
