@@ -2,7 +2,9 @@
 most 128 state indices on the fp32 path, and from 129 to 256 (fp32 storage,
 scalar A) on whichever path the descriptor asks for; block k reads B, C and
 s0 and writes s1 at its first state index and adds its share of y into y
-(HelixScanParams::y_acc; the walks of the later blocks load y ahead).
+(HelixScanParams::y_acc; the walks of the later blocks load y ahead). On the
+bf16 path each block's Pass A writes bf16 copies of its columns of B and C for
+its walk.
 
 Parity against the fp64 oracle (pinned at these d_state against the
 reference's own ref::scan and for the block decomposition itself in
@@ -174,3 +176,45 @@ def test_blocks_match_one_launch_sequence(gpu):
     _, y_b, s_b = run(native, p, desc=d)
     assert po.allclose_ratio(y_a, y_b, F32_REL, F32_ABS) <= 1.0
     assert po.allclose_ratio(s_a, s_b, F32_REL, F32_ABS) <= 1.0
+
+
+@pytest.mark.parametrize("heads", [4, 20], ids=["4 heads per group", "20 heads per group"])
+def test_blocks_up_to_256_copies_ids_and_groups(gpu, heads):
+    # The bf16 path's blocks with copies of B and C: ids pick s0 rows in
+    # reverse, and a 1 MiB scratch budget cuts the plan into many super-chunk
+    # groups, each group's Pass A copying its chunks' columns of B and C for
+    # that group's walks, the state carried through s1's columns of the block.
+    G = 2 if heads == 4 else 1
+    shape = (900, 3, heads * G, 64, 256, G, "copies, ids, many groups")
+    p, d = _problem(shape, 5164)
+    d.backend = HELIX_BACKEND_MPP
+    p.ids = np.array([2, 0, 1], np.int32)
+    small = ctx_for(gpu, HELIX_SCRATCH_MB="1")
+    info = small.plan_info(d)
+    assert info.state_blocks == 2 and info.n_groups > 1 and info.bccopy_bytes > 0
+    y_ref, s_ref = po.scan(p, use_ids=True, threads=0)
+    _, y, s1 = run(small, p, desc=d, use_ids=True)
+    ry = po.allclose_ratio(y, y_ref, BF16_REL, BF16_ABS)
+    rs = po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS)
+    print(f"{heads} heads per group: y ratio {ry:.3f}  s1 ratio {rs:.3f}", flush=True)
+    assert ry <= 1.0 and rs <= 1.0, (ry, rs)
+
+
+def test_blocks_up_to_256_noalloc(gpu):
+    # The bf16 path's blocks, copies included, in the library's fixed scratch.
+    shape = (700, 2, 4, 64, 256, 2, "noalloc, N=256")
+    p, d = _problem(shape, 5165)
+    d.backend = HELIX_BACKEND_MPP
+    assert gpu.plan_info(d).bccopy_bytes > 0
+    y_ref, s_ref = po.scan(p, threads=0)
+    dev = {k: upload(getattr(p, k)) for k in ("s0", "x", "dt", "A", "B", "C")}
+    y = torch.full(p.y_shape(), float("nan"), device="cuda")
+    s1 = torch.full(p.s_shape(), float("nan"), device="cuda")
+    rc = gpu.encode_noalloc(torch.cuda.current_stream().cuda_stream, d, T(dev["s0"]), T(dev["x"]), T(dev["dt"]),
+                            T(dev["A"]), T(dev["B"]), T(dev["C"]), HELIX_TENSOR_NULL, T(y), T(s1))
+    assert rc == HELIX_OK, gpu.last_error()
+    torch.cuda.synchronize()
+    ry = po.allclose_ratio(y.cpu().numpy(), y_ref, BF16_REL, BF16_ABS)
+    rs = po.allclose_ratio(s1.cpu().numpy(), s_ref, F32_REL, F32_ABS)
+    print(f"noalloc N=256 bf16: y ratio {ry:.3f}  s1 ratio {rs:.3f}", flush=True)
+    assert ry <= 1.0 and rs <= 1.0, (ry, rs)
