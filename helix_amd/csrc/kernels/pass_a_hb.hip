@@ -37,6 +37,93 @@
 // run on one XCD.
 #include "helix_common.h"
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// fp16 planes (H16). The operands are scaled by powers of two into fp16's
+// range, then split into a high and a low fp16 plane: v = v0 + v1 + e with
+// |e| <= 2^-22 |v| wherever v1 is a normal number (|v| >= 2^-3 after scaling).
+// Three products a0 b1 + a1 b0 + a0 b0 leave out a1 b1 and the e terms: about
+// 3 * 2^-22 of |ab|, against fp32's 2^-24 per rounding.
+//
+// Scales. B's are per state index (a row of the aggregate), x's per channel
+// (a column), so a scale factors out of every product of the row or column.
+// Every scale starts at 2^127. A chunk whose max m (for x, a bound on it)
+// reaches 2^15 once scaled (fp16's largest finite value is 65504) replaces
+// it with 2^k, k = 12 - floor(log2 m), which puts m in [2^12, 2^13), and the
+// accumulated row or column is first multiplied by the exact power of two
+// between the two scales; while the row is still zero that is the first
+// nonzero chunk, which so sets the scale. A row's values then keep full
+// precision down to 2^-15 of the max that set its scale. Smaller later values
+// keep the scale: a term that then loses bits lies 2^-26 or more below the
+// largest term of its row and column so far, where fp32 accumulation loses it
+// as well. The aggregate is divided by both scales when stored.
+constexpr int HB_KINIT = 127;
+
+// The scale exponent after a chunk whose max is m (the bits of a value >= 0,
+// or of NaN, which takes the smallest scale); `changed`: the scale was
+// replaced.
+HELIX_DEV int hb_next_scale(int k, unsigned m, bool& changed) {
+    const int eb = (int)(m >> 23);   // biased exponent
+    changed = eb + k >= 127 + 15;
+    return changed ? 127 + 12 - eb : k;
+}
+
+// Round-to-nearest-even fp16 pair (element 0 in the low half).
+HELIX_DEV unsigned pk_f16(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, f16x2));
+}
+
+// Two-way fp16 split of the pair (a, b), 4 VALU operations: the residuals
+// a - v0 are exact in fp32, each one v_dot2_f32_f16 of the packed pair with
+// (-1, 0) or (0, -1), held in a scalar register (bf16_pair_reg).
+HELIX_DEV void split2h_pair(float a, float b, unsigned& w0, unsigned& w1) {
+    w0 = pk_f16(a, b);
+    const f16x2 h = __builtin_bit_cast(f16x2, w0);
+    const float ra = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(f16x2, bf16_pair_reg(0x0000bc00u)), a, false);
+    const float rb = __builtin_amdgcn_fdot2(h, __builtin_bit_cast(f16x2, bf16_pair_reg(0xbc000000u)), b, false);
+    w1 = pk_f16(ra, rb);
+}
+
+// The MFMA on operands that hold fp16 bits (the planes share the bf16 planes'
+// storage and layout).
+HELIX_DEV f32x16 mfma_f16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
+// Max of v over lanes l and l ^ 16, and over lanes l and l ^ 32: a swap of
+// 16- (32-) lane halves between two copies of v, then a max.
+HELIX_DEV unsigned xor16_max(unsigned v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return max((unsigned)r[0], (unsigned)r[1]);
+}
+HELIX_DEV unsigned xor32_max(unsigned v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((unsigned)r[0], (unsigned)r[1]);
+}
+
+// Max of v (the bits of a value >= 0) over the wave.
+HELIX_DEV unsigned wave_max_bits(unsigned v) {
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false));   // row_ror:1
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false));   // row_ror:2
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));   // row_ror:4
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));   // row_ror:8
+    return xor32_max(xor16_max(v));
+}
+
+// Max of v (the bits of a value >= 0) over the lanes that hold the same state
+// indices in the row-owner layout (hb_rows_at, OWN): lanes equal mod 4 (NP
+// 128) or mod 2 (NP 64). Every lane ends with the max.
+template <int NP>
+HELIX_DEV unsigned hb_row_max(unsigned v) {
+    if constexpr (NP == 64) v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false));
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));   // row_ror:4
+    v = max(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));   // row_ror:8
+    return xor32_max(xor16_max(v));
+}
+
 // x of the wave's P tile for one chunk, in storage form: channel 32 pt + lo,
 // tokens 16 s + 8 hi + e.
 template <typename IO>
@@ -65,9 +152,24 @@ struct HbRows {
 // dword 36 n + t / 2 of the plane) cover the 16 bank pairs 16 (q % 4) + 2 r:
 // no bank conflicts. NP 64: wave w owns tokens 8 w .. 8 w + 7, lane (q, r) =
 // (lane % 16, lane / 16) quad q of tokens 8 w + 2 r.
-template <int NP>
+//
+// OWN (the fp16 planes): wave w owns every token of state indices 16 w .. + 15
+// (NP 128) or 8 w .. + 7 (NP 64), so a state index's max over the chunk is a
+// reduction within the wave: lane bits (1:0) (bit 0 at NP 64) pick the quad,
+// the others the run of four (two) tokens. A load instruction reads 16 (32)
+// rows of 64 (32) contiguous bytes; the staging writes of 16 consecutive lanes
+// again cover distinct bank pairs.
+template <int NP, bool OWN = false>
 HELIX_DEV void hb_rows_at(int lane, int wave, int& n, int& t) {
-    if constexpr (NP == 128) {
+    if constexpr (OWN) {
+        if constexpr (NP == 128) {
+            n = 16 * wave + 4 * (lane & 3);
+            t = 4 * (lane >> 2);
+        } else {
+            n = 8 * wave + 4 * (lane & 1);
+            t = 2 * (lane >> 1);
+        }
+    } else if constexpr (NP == 128) {
         const int q = (lane & 3) | ((lane >> 4) << 2);
         n = 64 * (wave >> 2) + 4 * q;
         t = 16 * (wave & 3) + 4 * ((lane >> 2) & 3);
@@ -129,7 +231,7 @@ HELIX_DEV void vmem_fence() { __builtin_amdgcn_sched_barrier(0x0001 | 0x0002 | 0
 // that does not copy issues its C loads past the resource's range, which
 // returns zeros without touching memory (the loads stay on every path, so the
 // vmcnt waits are the same for every wave).
-template <int NP, typename IO, bool BCC>
+template <int NP, typename IO, bool BCC, bool OWN = false>
 __device__ __forceinline__ void hb_load_rows(HbRows<NP, IO>& st, const HelixScanParams& p,
                                              const IO* __restrict__ B_g, const float* __restrict__ C_g, int c,
                                              int lane, int wave, int N, bool copier) {
@@ -140,7 +242,7 @@ __device__ __forceinline__ void hb_load_rows(HbRows<NP, IO>& st, const HelixScan
     const int sb0 = sgpr_fresh((int)p.s_b[0]);
     const helix_rsrc rb = make_rsrc(B_g + (long long)t0 * p.s_b[0], ((tlen - 1) * sb0 + N) * (unsigned)ES);
     int nq, j0;
-    hb_rows_at<NP>(lane, wave, nq, j0);
+    hb_rows_at<NP, OWN>(lane, wave, nq, j0);
     const int n0 = min(nq, N - 4);
 #pragma unroll
     for (int i = 0; i < L; ++i) {
@@ -195,14 +297,17 @@ HELIX_DEV int hb_off(int k, int r, int c) {
 
 // Split the L consecutive tokens' values v[0..L-1] of state index n into NS
 // planes and store them at tokens t .. t + L - 1 of row n (hb_off layout).
-template <int NP, int NS, int L>
+// H16: two fp16 planes.
+template <int NP, int NS, int L, bool H16 = false>
 HELIX_DEV void hb_stage_run(__bf16* planes, int n, int t, const float* v) {
     static_assert(L == 2 || L == 4, "runs of two or four tokens");
     unsigned q[NS][L / 2];
 #pragma unroll
     for (int e = 0; e < L / 2; ++e) {
         unsigned w[3];
-        if constexpr (NS == 3)
+        if constexpr (H16)
+            split2h_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+        else if constexpr (NS == 3)
             split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
         else
             split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
@@ -257,12 +362,15 @@ __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtr
 // fp64 decay records of the fp32 path's Pass C; MODE 2: segment aggregates only,
 // and the walk's decay records. IO: the caller's storage type of x and B. BCC:
 // write the bf16 copies of B and C (fp32 storage). NS: split planes per operand.
-// R64: MODE 2 with the fp32 path's records, for its bf16x6 walk.
-template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3, bool R64 = false>
+// R64: MODE 2 with the fp32 path's records, for its bf16x6 walk. H16: two
+// fp16 planes with power-of-two scales (see hb_next_scale), aggregates of
+// fp32 storage only.
+template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3, bool R64 = false, bool H16 = false>
 __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     static_assert(NP == 64 || NP == 128, "the double-buffered B planes of d_state 256 exceed the LDS");
     static_assert(NS == 2 || NS == 3, "two or three split planes");
     static_assert(MODE == 0 || MODE == 2, "per-chunk fp32 prefixes or aggregates only");
+    static_assert(!H16 || (NS == 2 && MODE == 2 && !R64 && sizeof(IO) == 4), "fp16 planes: aggregates, fp32 storage");
     constexpr int HB = HELIX_HB;
     constexpr int NTN = NP / 32;        // 32-row n tiles per wave
     constexpr int PLANES = NS * NP * HB_RS;
@@ -270,6 +378,12 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // Per chunk parity and item: w_j of the chunk's 64 tokens, and L_end (fp64
     // bits) at [64], [65].
     __shared__ __attribute__((aligned(16))) float sW[2][HB][HELIX_CS + 4];
+    // H16: the scale exponent of every state index for the planes of chunk
+    // step it (buffer it % 3: a wave may read the previous step's while
+    // another already writes the next one's), and per step parity and wave
+    // whether a scale in use changed.
+    __shared__ __attribute__((aligned(16))) int sKb[H16 ? 3 : 1][H16 ? NP : 4];
+    __shared__ __attribute__((aligned(8))) unsigned char sFlag[H16 ? 2 : 1][8];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = wave_uniform(), lo = lane & 31, hi = lane >> 5;
@@ -338,14 +452,41 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // this thread's rows), and the bf16 copies of its B and C rows.
     constexpr int L = HbRows<NP, IO>::L;
     int q4, tr;   // this thread's first state index and token
-    hb_rows_at<NP>(lane, wave, q4, tr);
+    hb_rows_at<NP, H16>(lane, wave, q4, tr);
+    // H16: scale exponents of state indices q4 .. q4 + 3 (the same in every
+    // lane of the quad) and of this lane's channel.
+    int kb[4] = {HB_KINIT, HB_KINIT, HB_KINIT, HB_KINIT};
+    int kx = HB_KINIT;
     auto stage_planes = [&](const HbRows<NP, IO>& rows, __bf16* planes, int k0, int k1) {
 #pragma unroll
         for (int k = k0; k < k1; ++k) {
             float v[L];
 #pragma unroll
-            for (int i = 0; i < L; ++i) v[i] = hb_b<NP, IO>(rows, i, k);
-            hb_stage_run<NP, NS, L>(planes, q4 + k, tr, v);
+            for (int i = 0; i < L; ++i) {
+                v[i] = hb_b<NP, IO>(rows, i, k);
+                if constexpr (H16) v[i] = __builtin_ldexpf(v[i], kb[k]);
+            }
+            hb_stage_run<NP, NS, L, H16>(planes, q4 + k, tr, v);
+        }
+    };
+    // H16: the scales of the state indices of the chunk in `rows`, whose
+    // planes chunk step `st` reads, into sKb[st % 3], and whether a scale in
+    // use changed into sFlag[st & 1].
+    auto update_b_scales = [&](const HbRows<NP, IO>& rows, int st) {
+        if constexpr (H16) {
+            bool any = false;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float m = 0.0f;
+#pragma unroll
+                for (int i = 0; i < L; ++i) m = fmaxf(m, fabsf(hb_b<NP, IO>(rows, i, k)));
+                bool ch;
+                kb[k] = hb_next_scale(kb[k], hb_row_max<NP>(__builtin_bit_cast(unsigned, m)), ch);
+                any |= ch;
+            }
+            if (tr == 0) *reinterpret_cast<int4*>(&sKb[st % 3][q4]) = int4{kb[0], kb[1], kb[2], kb[3]};
+            const bool wany = __builtin_amdgcn_ballot_w64(any) != 0;
+            if (lane == 0) sFlag[st & 1][wave] = wany ? 1 : 0;
         }
     };
     auto copy_rows = [&](const HbRows<NP, IO>& rows, int c) {
@@ -388,10 +529,13 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     auto preamble = [&](int c, double shift, float lam_c, float (*wdst)[HELIX_CS + 4], bool live) {
         const HbPre pr = hb_preamble<MODE, R64>(p, dtraw, A_h, c, lane, shift);
         wdst[is][lane] = pr.w;
+        // H16: the chunk's largest weight (>= 0) at [66], for the x scales.
+        const float wmax = H16 ? __builtin_bit_cast(float, wave_max_bits(__builtin_bit_cast(unsigned, pr.w))) : 0.0f;
         if (lane == 0) {
             const unsigned long long u = __builtin_bit_cast(unsigned long long, pr.lend);
             wdst[is][HELIX_CS] = __builtin_bit_cast(float, (unsigned)u);
             wdst[is][HELIX_CS + 1] = __builtin_bit_cast(float, (unsigned)(u >> 32));
+            if constexpr (H16) wdst[is][HELIX_CS + 2] = wmax;
         }
         // The record's address is formed unconditionally (a select of two
         // pointers becomes a branch); without records its range is zero.
@@ -428,6 +572,15 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // Smallest terms first, the two accumulators interleaved so no MFMA
     // waits on the one before it.
     auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NS], const bf16x8 (&xp)[NS]) {
+        if constexpr (H16) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][1], xp[0], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][0], xp[1], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][0], xp[0], acc[i0 + i]);
+            return;
+        }
         if constexpr (NS == 3) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_bf16(bp[i][2], xp[0], acc[i0 + i]);
@@ -451,11 +604,17 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
             v[e] = mul_legacy(w0[e], io_widen<IO>(xs.v[s][e]));
             v[4 + e] = mul_legacy(w1[e], io_widen<IO>(xs.v[s][4 + e]));
         }
+        if constexpr (H16) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(v[e], kx);
+        }
         u32x4 xq[NS];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             unsigned w[3];
-            if constexpr (NS == 3)
+            if constexpr (H16)
+                split2h_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
+            else if constexpr (NS == 3)
                 split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
             else
                 split2_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
@@ -464,6 +623,44 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         }
 #pragma unroll
         for (int k = 0; k < NS; ++k) xp[k] = __builtin_bit_cast(bf16x8, xq[k]);
+    };
+
+    // H16, before a chunk's products: the accumulated rows whose state index
+    // took a new scale for this chunk (planes of step it, scales in buffer
+    // it % 3, the previous step's in (it + 2) % 3) are multiplied by the exact
+    // power of two between the two scales; then the columns, for the bound
+    // max |x| * max w of the chunk's weighted x in each channel (over its two
+    // lanes; the largest weight from the preamble, wrow[66]), which puts the
+    // largest |w x| at or below 2^13 once scaled.
+    auto chunk_scales = [&](int it, const float* __restrict__ wrow) {
+        if constexpr (H16) {
+            if (it > 0 && *reinterpret_cast<const unsigned long long*>(&sFlag[it & 1][0]) != 0ull) {
+                const int kn = it % 3, ko = (it + 2) % 3;
+#pragma unroll
+                for (int i = 0; i < NTN; ++i)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const int row = 32 * i + acc_row(j, hi);
+                        acc[i][j] = __builtin_ldexpf(acc[i][j], sKb[kn][row] - sKb[ko][row]);
+                    }
+            }
+            float mx = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(io_widen<IO>(xs.v[s][e])));
+            const float bound = __builtin_bit_cast(float, xor32_max(__builtin_bit_cast(unsigned, mx))) * wrow[HELIX_CS + 2];
+            bool ch;
+            const int kn = hb_next_scale(kx, __builtin_bit_cast(unsigned, bound), ch);
+            if (__builtin_amdgcn_ballot_w64(ch) != 0) {
+                const int d = ch ? kn - kx : 0;
+#pragma unroll
+                for (int i = 0; i < NTN; ++i)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[i][j] = __builtin_ldexpf(acc[i][j], d);
+            }
+            kx = kn;
+        }
     };
 
     // Chunk nth(it). Its B planes are in `cur` and its weights in `wcur` (both
@@ -496,6 +693,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                                           acc[i][4 * r4 + 3], lane, tile_unit(NTN, pt, i, r4, 0));
         }
         const float a_c = MODE == 0 ? expf(lendf) : 1.0f;
+        chunk_scales(it, wrow);
 
         // The B planes of the next group and the weights of the next K step
         // are read from LDS while the current group's MFMAs run, so no MFMA
@@ -532,6 +730,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 }
             }
             vmem_fence();
+            if (s == 2) update_b_scales(rows, it + 1);
             if (s >= 2) stage_planes(rows, nxt, 2 * (s - 2), 2 * (s - 2) + 2);
             if (s == 3) copy_rows(rows, cn);
             vmem_fence();
@@ -551,7 +750,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         // The rows and dt of the chunk after cn.
         vmem_fence();
         const int cnn = nth(it + 2);
-        hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, cnn, lane, wave, N, copier);
+        hb_load_rows<NP, IO, BCC, H16>(rows, p, B_g, C_g, cnn, lane, wave, N, copier);
         dtraw = hb_load_dt(p, dt_h, cnn, lane);
         __syncthreads();
     };
@@ -560,13 +759,14 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // flight, the second chunk's rows and dt in flight.
     const int c0 = nth(0), c1 = nth(1);
     dtraw = hb_load_dt(p, dt_h, c0, lane);
-    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c0, lane, wave, N, copier);
+    hb_load_rows<NP, IO, BCC, H16>(rows, p, B_g, C_g, c0, lane, wave, N, copier);
 #pragma unroll
     for (int s = 0; s < 4; ++s) hb_load_xs<IO>(xs.v[s], p, x_w, c0, s, lane, pt, pw);
     if (pt == 1) preamble(c0, 0.0, 0.0f, sW[0], true);
+    update_b_scales(rows, 0);
     stage_planes(rows, sB, 0, 4);
     copy_rows(rows, c0);
-    hb_load_rows<NP, IO, BCC>(rows, p, B_g, C_g, c1, lane, wave, N, copier);
+    hb_load_rows<NP, IO, BCC, H16>(rows, p, B_g, C_g, c1, lane, wave, N, copier);
     dtraw = hb_load_dt(p, dt_h, c1, lane);
     __syncthreads();
     // MODE 2 takes the segment's last chunk out of the loop (last_step).
@@ -581,6 +781,18 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // or in y for the single pass without scratch (p.ytile; ytile_* in
     // helix_common.h, the range covering the rows the tile and the log-decay
     // take).
+    // H16: accumulator tiles i0 .. i1 - 1 divided by the scales of their rows
+    // and column.
+    auto unscale_tiles = [&](int i0, int i1) {
+        if constexpr (H16) {
+            const int kbuf = n_loop % 3;
+#pragma unroll
+            for (int i = i0; i < i1; ++i)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc[i][j] = __builtin_ldexpf(acc[i][j], -(kx + sKb[kbuf][32 * i + acc_row(j, hi)]));
+        }
+    };
     auto store_tiles = [&](int i0, int i1) {
         if (MODE == 2 && p.ytile) {
             const int upr = pw >> 2;
@@ -622,6 +834,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         lend = __builtin_bit_cast(double, (unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS]) |
                                               ((unsigned long long)__builtin_bit_cast(unsigned, wrow[HELIX_CS + 1]) << 32));
         mu += lend;
+        chunk_scales(n_loop, wrow);
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
             bf16x8 bq[2][2][NS];
@@ -635,6 +848,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 if (s + 1 < 4) read_group(cur, s + 1, 2 * gi, bq[(s + 1) & 1]);
                 mfma_group(2 * gi, bq[s & 1], xp);
             }
+            unscale_tiles(2 * gi, 2 * gi + 2);
             store_tiles(2 * gi, 2 * gi + 2);
         }
         if (p.ytile) {
@@ -672,6 +886,14 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x6agg_f16io_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                      \
         chunk_state_hb_impl<NP, 2, _Float16>(p, b);                                                   \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_h3agg_n##NP(    \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, false, 2, false, true>(p, b);                               \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_h3agg_bc_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, float, true, 2, false, true>(p, b);                                \
     }                                                                                                 \
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_n##NP(    \
         HelixScanParams p, HelixScanBuffers b) {                                                      \

@@ -75,6 +75,9 @@ struct TraitTable {
     // path's walk (d_state <= 128); [io][split6][bccopy][k]: bf16 path (bccopy
     // only with fp32 storage).
     HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk[2], bf16[3][2][2][3], ysingle[2];
+    // [bccopy][k]: bf16 path with Pass A on scaled fp16 planes (fp32 storage,
+    // d_state <= 128).
+    HelixMatmulTraits h3[2][2];
     std::vector<std::string> names;   // every kernel name, deduplicated
     std::deque<std::string> store;    // backing storage of the strings above
 
@@ -200,6 +203,15 @@ struct TraitTable {
                         t.rec_kind = 1;
                     }
         }
+        for (int k = 0; k < 2; ++k)
+            for (int bc = 0; bc < 2; ++bc) {
+                HelixMatmulTraits& t = h3[bc][k];
+                t = bf16[0][1][bc][k];
+                const std::string np = std::to_string(kNps[k]);
+                t.name = keep("mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes) (d_state<=" + np + ")");
+                t.k_chunk_state = kernel(std::string("helix_chunk_state_hb_h3agg_") + (bc ? "bc_" : "") + "n" + np);
+                t.mfma_a = "v_mfma_f32_32x32x16_f16 (two scaled fp16 planes, three products)";
+            }
         // What helix_ctx_backend_desc reports for a descriptor run as blocks
         // of state indices on these kernels.
         auto blocks_name = [&](HelixMatmulTraits& t) {
@@ -212,6 +224,7 @@ struct TraitTable {
         for (auto& t : ysingle) blocks_name(t);
         for (auto& t : diag) blocks_name(t);
         for (auto& a : bf16) for (auto& b2 : a) for (auto& c2 : b2) for (auto& t : c2) blocks_name(t);
+        for (auto& a : h3) for (auto& t : a) blocks_name(t);
     }
 };
 
@@ -281,6 +294,8 @@ helix_tuning tuning_from_env() {
     if (const char* f = std::getenv("HELIX_FORCE_BACKEND")) t.force_fp32 = f[0] == 's' || f[0] == 'S';
     if (env_switch("HELIX_PASSA_SPLIT") == 3) t.passa_split = 3;
     t.fuse_b = env_switch("HELIX_FUSE_B");
+    const int f16 = env_switch("HELIX_PASSA_F16");
+    if (f16 >= 0) t.passa_f16 = f16 > 0 ? 1 : 0;
     if (t.fuse_b > 1) t.fuse_b = 1;
     const int bc = env_switch("HELIX_WALK_BCCOPY");
     t.bccopy = bc == 0 ? 0 : bc > 0 ? 1 : -1;
@@ -377,6 +392,11 @@ const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const hel
         return walk ? tt.f32walk[k] : tt.f32[k];
     }
     const int bc = io == 0 && bccopy_on(tu, d, block) ? 1 : 0;
+    // Pass A on two scaled fp16 planes (three products) by default with fp32
+    // storage up to d_state 128: config 2, 0.110 against 0.117 ms on six bf16
+    // split products, s1 at the same fp32 per-element bound;
+    // HELIX_PASSA_F16=0 keeps the six.
+    if (io == 0 && k < 2 && tu.passa_split != 3 && tu.passa_f16 != 0) return tt.h3[bc][k];
     return tt.bf16[io][tu.passa_split == 3 ? 0 : 1][bc][k];
 }
 

@@ -105,6 +105,11 @@ MODES = [
     ("fp32/n256/long", HELIX_BACKEND_SGMMA, None, "long", {"HELIX_STATE_BLOCKS": "0"}, True),
     ("bf16/n256/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_STATE_BLOCKS": "0"}, True),
     ("1pass/n256/long", HELIX_BACKEND_AUTO, None, "long", {"HELIX_STATE_BLOCKS": "0", "HELIX_1PASS_Y": "0"}, False),
+    # Pass A on two scaled fp16 planes (three products), s1 at the fp32 bound.
+    ("bf16/h3", HELIX_BACKEND_MPP, None, "short", {"HELIX_PASSA_F16": "1"}, True),
+    ("bf16/h3/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_PASSA_F16": "1"}, True),
+    ("bf16/h3/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA_F16": "1"}, True),
+    ("bf16/h3/copy/long", HELIX_BACKEND_MPP, None, "long", {"HELIX_PASSA_F16": "1", "HELIX_WALK_BCCOPY": "1"}, True),
     # Opt-in: Pass A on two split planes (three products), s1 at the wider bound.
     ("bf16/x3", HELIX_BACKEND_MPP, None, "short", {"HELIX_PASSA_SPLIT": "3"}, True),
     ("bf16/x3/sm/long", HELIX_BACKEND_MPP, 1, "long", {"HELIX_PASSA_SPLIT": "3"}, True),
@@ -164,6 +169,7 @@ def _baseline(name, memory):
 # quotes on the bf16 path.
 CASES = [(n, path, mem) for n in CONFIGS for mem in ("dist", "long") for path in ("fp32", "bf16", "1pass")]
 CASES += [(n, "bf16/x3", "dist") for n, c in CONFIGS.items() if "bf16" in c.paths]
+CASES += [(n, "bf16/h3", mem) for n, c in CONFIGS.items() if "bf16" in c.paths for mem in ("dist", "long")]
 
 
 @pytest.mark.parametrize("name,path,memory", CASES, ids=[f"{n}-{p}-{m}" for n, p, m in CASES])
@@ -173,7 +179,8 @@ def test_baseline_config(gpu, name, path, memory):
     d.multipass = path != "1pass"
     d.backend = (HELIX_BACKEND_MPP if path.startswith("bf16")
                  else HELIX_BACKEND_AUTO if path == "1pass" else HELIX_BACKEND_SGMMA)
-    ctx = ctx_for(gpu, HELIX_PASSA_SPLIT="3" if path == "bf16/x3" else None)
+    ctx = ctx_for(gpu, HELIX_PASSA_SPLIT="3" if path == "bf16/x3" else None,
+                  HELIX_PASSA_F16="1" if path == "bf16/h3" else None)
     assert ctx.supported(d)
     s_rel, s_abs = s1_tolerance(ctx, d)
     assert (ctx.select_backend(d) == HELIX_BACKEND_MPP) == path.startswith("bf16")

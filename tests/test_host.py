@@ -385,17 +385,24 @@ def test_backend_selection(host):
     assert (f0.backend_desc(mp(shape, HELIX_BACKEND_SGMMA))
             == "mfma fp32, passes A and C bf16x6 (d_state<=128)")
     assert f0.plan_info(mp(shape, HELIX_BACKEND_SGMMA)).kernel_c == b"helix_chunk_out_x6_n128"
-    # The bf16 path walks segments in Pass C at every d_state; its Pass A runs
-    # six split products (the carried state stays fp32-accurate, reference
-    # caps.mm:65-73) unless HELIX_PASSA_SPLIT=3 opts into three.
-    assert host.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
-    assert (host.backend_desc(mp((64, 1, 1, 64, 128, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)")
+    # The bf16 path walks segments in Pass C at every d_state. Its Pass A keeps
+    # the carried state fp32-accurate (reference caps.mm:65-73): on two scaled
+    # fp16 planes (three products) with fp32 storage up to d_state 128, on six
+    # bf16 split products otherwise or with HELIX_PASSA_F16=0;
+    # HELIX_PASSA_SPLIT=3 opts into three bf16 products.
+    h3 = "mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes) (d_state<=128)"
+    assert host.backend_desc(mp(shape)) == h3
+    assert host.backend_desc(mp((64, 1, 1, 64, 128, 1))) == h3
+    x6 = tuned(HELIX_PASSA_F16="0")
+    assert x6.backend_desc(mp(shape)) == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128)"
+    assert x6.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_x6agg_n128"
+    assert host.plan_info(mp(shape)).kernel_a == b"helix_chunk_state_hb_h3agg_n128"
+    assert host.plan_info(mp((64, 1, 1, 64, 64, 1))).kernel_a == b"helix_chunk_state_hb_h3agg_n64"
     # d_state 256: blocks of 128 by default, one launch sequence on the d_state
     # 256 kernels with HELIX_STATE_BLOCKS=0.
     native = tuned(HELIX_STATE_BLOCKS="0")
     assert (host.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
-            == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=128), in blocks of at most 128 state indices")
+            == h3 + ", in blocks of at most 128 state indices")
     assert (native.backend_desc(mp((4096, 1, 32, 64, 256, 1)))
             == "mfma bf16 pass C, chunk walk, pass A bf16x6 (d_state<=256)")
     assert (native.backend_desc(mp((64, 1, 1, 64, 256, 1)))
@@ -429,7 +436,7 @@ def test_backend_selection(host):
     # only walk segments that are Pass A's segments too (HELIX_FUSE_B=1 with
     # HELIX_SEG_LEN=16 runs it there).
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        b"helix_chunk_state_hb_x6agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
+        b"helix_chunk_state_hb_h3agg_n128", b"helix_state_scan_f32", b"helix_scan_walk16_bf16_n128")
     assert k.bccopy_bytes == 0 and k.pass_b == abi.PASS_B_LAUNCHED
     # Pass A (head blocks of four heads) runs 8-chunk segments, 16 per
     # sequence; the walk runs 16-chunk ones, each starting at every other
@@ -461,7 +468,7 @@ def test_backend_selection(host):
     L, S, H, P, N, G = shape
     # HELIX_WALK_BCCOPY=1: Pass A writes bf16 copies of B and C that the walk reads.
     kc = tuned(HELIX_WALK_BCCOPY="1").plan_info(mp(shape))
-    assert (kc.kernel_a, kc.kernel_c) == (b"helix_chunk_state_hb_x6agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
+    assert (kc.kernel_a, kc.kernel_c) == (b"helix_chunk_state_hb_h3agg_bc_n128", b"helix_scan_walk16_bf16_bc_n128")
     assert kc.bccopy_bytes == 2 * (S * L * G * N * 2)
     assert k4.bccopy_bytes > 0   # 80 heads per group: copies by default
     # Pass A writes one decay record per (seq, chunk, head, token) for the
