@@ -471,18 +471,28 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     };
     // H16: the scales of the state indices of the chunk in `rows`, whose
     // planes chunk step `st` reads, into sKb[st % 3], and whether a scale in
-    // use changed into sFlag[st & 1].
+    // use changed into sFlag[st & 1]. Each lane first checks its own tokens of
+    // its four rows against the scales in use; only where one of them would
+    // overflow does the wave reduce the rows' maxima and choose scales again.
     auto update_b_scales = [&](const HbRows<NP, IO>& rows, int st) {
         if constexpr (H16) {
-            bool any = false;
+            float m[4];
+            bool need = false;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                float m = 0.0f;
+                m[k] = 0.0f;
 #pragma unroll
-                for (int i = 0; i < L; ++i) m = fmaxf(m, fabsf(hb_b<NP, IO>(rows, i, k)));
-                bool ch;
-                kb[k] = hb_next_scale(kb[k], hb_row_max<NP>(__builtin_bit_cast(unsigned, m)), ch);
-                any |= ch;
+                for (int i = 0; i < L; ++i) m[k] = fmaxf(m[k], fabsf(hb_b<NP, IO>(rows, i, k)));
+                need |= (int)(__builtin_bit_cast(unsigned, m[k]) >> 23) + kb[k] >= 127 + 15;
+            }
+            bool any = false;
+            if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    bool ch;
+                    kb[k] = hb_next_scale(kb[k], hb_row_max<NP>(__builtin_bit_cast(unsigned, m[k])), ch);
+                    any |= ch;
+                }
             }
             if (tr == 0) *reinterpret_cast<int4*>(&sKb[st % 3][q4]) = int4{kb[0], kb[1], kb[2], kb[3]};
             const bool wany = __builtin_amdgcn_ballot_w64(any) != 0;
