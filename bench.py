@@ -540,8 +540,8 @@ def main():
         variants.append(Variant("bf16-storage", ctx, HELIX_BACKEND_MPP, as_storage(tensors, torch.bfloat16)))
         variants.append(Variant("bf16-passA-x3-optin", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_PASSA_SPLIT": "3"}))
-        variants.append(Variant("bf16-passA-f16", ctx, HELIX_BACKEND_MPP, tensors,
-                                env={"HELIX_PASSA_F16": "1"}))
+        variants.append(Variant("bf16-passA-x6", ctx, HELIX_BACKEND_MPP, tensors,
+                                env={"HELIX_PASSA_F16": "0"}))
         variants.append(Variant("bf16-copies", ctx, HELIX_BACKEND_MPP, tensors,
                                 env={"HELIX_WALK_BCCOPY": "1"}))
         # The fp32 path at d_state 64 (config 2's shape otherwise): the walk

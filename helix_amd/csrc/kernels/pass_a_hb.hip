@@ -363,14 +363,13 @@ __device__ __forceinline__ HbPre hb_preamble(const HelixScanParams& p, float dtr
 // and the walk's decay records. IO: the caller's storage type of x and B. BCC:
 // write the bf16 copies of B and C (fp32 storage). NS: split planes per operand.
 // R64: MODE 2 with the fp32 path's records, for its bf16x6 walk. H16: two
-// fp16 planes with power-of-two scales (see hb_next_scale), aggregates of
-// fp32 storage only.
+// fp16 planes with power-of-two scales (see hb_next_scale), aggregates only.
 template <int NP, int MODE, typename IO = float, bool BCC = false, int NS = 3, bool R64 = false, bool H16 = false>
 __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, const HelixScanBuffers& b) {
     static_assert(NP == 64 || NP == 128, "the double-buffered B planes of d_state 256 exceed the LDS");
     static_assert(NS == 2 || NS == 3, "two or three split planes");
     static_assert(MODE == 0 || MODE == 2, "per-chunk fp32 prefixes or aggregates only");
-    static_assert(!H16 || (NS == 2 && MODE == 2 && !R64 && sizeof(IO) == 4), "fp16 planes: aggregates, fp32 storage");
+    static_assert(!H16 || (NS == 2 && MODE == 2 && !R64), "fp16 planes: aggregates");
     constexpr int HB = HELIX_HB;
     constexpr int NTN = NP / 32;        // 32-row n tiles per wave
     constexpr int PLANES = NS * NP * HB_RS;
@@ -904,6 +903,14 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_h3agg_bc_n##NP( \
         HelixScanParams p, HelixScanBuffers b) {                                                      \
         chunk_state_hb_impl<NP, 2, float, true, 2, false, true>(p, b);                                \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_h3agg_bf16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, __bf16, false, 2, false, true>(p, b);                              \
+    }                                                                                                 \
+    extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_h3agg_f16io_n##NP( \
+        HelixScanParams p, HelixScanBuffers b) {                                                      \
+        chunk_state_hb_impl<NP, 2, _Float16, false, 2, false, true>(p, b);                            \
     }                                                                                                 \
     extern "C" __global__ __launch_bounds__(HELIX_HB_THREADS) void helix_chunk_state_hb_x3agg_n##NP(    \
         HelixScanParams p, HelixScanBuffers b) {                                                      \

@@ -75,9 +75,9 @@ struct TraitTable {
     // path's walk (d_state <= 128); [io][split6][bccopy][k]: bf16 path (bccopy
     // only with fp32 storage).
     HelixMatmulTraits single[3][3], diag[2], f32[3], f32walk[2], bf16[3][2][2][3], ysingle[2];
-    // [bccopy][k]: bf16 path with Pass A on scaled fp16 planes (fp32 storage,
-    // d_state <= 128).
-    HelixMatmulTraits h3[2][2];
+    // [io][bccopy][k]: bf16 path with Pass A on scaled fp16 planes (d_state
+    // <= 128; bccopy only with fp32 storage).
+    HelixMatmulTraits h3[3][2][2];
     std::vector<std::string> names;   // every kernel name, deduplicated
     std::deque<std::string> store;    // backing storage of the strings above
 
@@ -203,15 +203,18 @@ struct TraitTable {
                         t.rec_kind = 1;
                     }
         }
-        for (int k = 0; k < 2; ++k)
-            for (int bc = 0; bc < 2; ++bc) {
-                HelixMatmulTraits& t = h3[bc][k];
-                t = bf16[0][1][bc][k];
-                const std::string np = std::to_string(kNps[k]);
-                t.name = keep("mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes) (d_state<=" + np + ")");
-                t.k_chunk_state = kernel(std::string("helix_chunk_state_hb_h3agg_") + (bc ? "bc_" : "") + "n" + np);
-                t.mfma_a = "v_mfma_f32_32x32x16_f16 (two scaled fp16 planes, three products)";
-            }
+        for (int io = 0; io < 3; ++io)
+            for (int k = 0; k < 2; ++k)
+                for (int bc = 0; bc < 2; ++bc) {
+                    HelixMatmulTraits& t = h3[io][bc][k];
+                    t = bf16[io][1][bc][k];
+                    if (!t.name) continue;   // copies only from fp32 storage
+                    const std::string np = std::to_string(kNps[k]);
+                    t.name = keep(std::string("mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes)") +
+                                  (io == 1 ? ", bf16 storage" : io == 2 ? ", f16 storage" : "") + " (d_state<=" + np + ")");
+                    t.k_chunk_state = kernel(std::string("helix_chunk_state_hb_h3agg_") + (bc ? "bc_" : kIoTag[io]) + "n" + np);
+                    t.mfma_a = "v_mfma_f32_32x32x16_f16 (two scaled fp16 planes, three products)";
+                }
         // What helix_ctx_backend_desc reports for a descriptor run as blocks
         // of state indices on these kernels.
         auto blocks_name = [&](HelixMatmulTraits& t) {
@@ -224,7 +227,7 @@ struct TraitTable {
         for (auto& t : ysingle) blocks_name(t);
         for (auto& t : diag) blocks_name(t);
         for (auto& a : bf16) for (auto& b2 : a) for (auto& c2 : b2) for (auto& t : c2) blocks_name(t);
-        for (auto& a : h3) for (auto& t : a) blocks_name(t);
+        for (auto& a : h3) for (auto& b2 : a) for (auto& t : b2) blocks_name(t);
     }
 };
 
@@ -392,11 +395,11 @@ const HelixMatmulTraits& select_traits_unblocked(const helix_ctx* ctx, const hel
         return walk ? tt.f32walk[k] : tt.f32[k];
     }
     const int bc = io == 0 && bccopy_on(tu, d, block) ? 1 : 0;
-    // Pass A on two scaled fp16 planes (three products) by default with fp32
-    // storage up to d_state 128: config 2, 0.110 against 0.117 ms on six bf16
-    // split products, s1 at the same fp32 per-element bound;
-    // HELIX_PASSA_F16=0 keeps the six.
-    if (io == 0 && k < 2 && tu.passa_split != 3 && tu.passa_f16 != 0) return tt.h3[bc][k];
+    // Pass A on two scaled fp16 planes (three products) by default up to
+    // d_state 128: config 2, 0.110 against 0.117 ms on six bf16 split
+    // products, s1 at the same fp32 per-element bound; HELIX_PASSA_F16=0
+    // keeps the six.
+    if (k < 2 && tu.passa_split != 3 && tu.passa_f16 != 0) return tt.h3[io][bc][k];
     return tt.bf16[io][tu.passa_split == 3 ? 0 : 1][bc][k];
 }
 

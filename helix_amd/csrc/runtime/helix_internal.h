@@ -25,9 +25,9 @@ struct helix_tuning {
     int  passa_split = 6;      // HELIX_PASSA_SPLIT=3: bf16 path Pass A on two split
                                // planes (three products, state to about 2^-16;
                                // opt-in, narrower than the reference's fp32 Pass A)
-    int  passa_f16   = -1;     // HELIX_PASSA_F16=0: bf16 path Pass A (fp32 storage, d_state
-                               // <= 128) on six bf16 split products instead of two
-                               // scaled fp16 planes (three products)
+    int  passa_f16   = -1;     // HELIX_PASSA_F16=0: bf16 path Pass A (d_state <= 128) on six
+                               // bf16 split products instead of two scaled fp16 planes
+                               // (three products)
     int  fuse_b      = -1;     // HELIX_FUSE_B=0|1: Pass B in the walk's prologue
     int  bccopy      = -1;     // HELIX_WALK_BCCOPY=0: no bf16 copies of B and C
     int  seg_len     = 0;      // HELIX_SEG_LEN: chunks per Pass A segment

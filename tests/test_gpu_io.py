@@ -22,7 +22,7 @@ from oracle import pyoracle as po
 from helix_amd.desc import (HELIX_BACKEND_AUTO, HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_F16,
                             HELIX_OK, HELIX_TENSOR_NULL)
 from baseline_configs import CONFIGS
-from gpu_harness import BF16_ABS, BF16_GATE, BF16_REL, F32_ABS, F32_GATE, F32_REL, X3_ABS, X3_REL, T
+from gpu_harness import BF16_ABS, BF16_GATE, BF16_REL, F32_ABS, F32_GATE, F32_REL, X3_ABS, X3_REL, T, ctx_for
 
 pytestmark = pytest.mark.gpu
 
@@ -95,7 +95,7 @@ SHAPES = [
     (1100, 1, 4, 64, 128, 2, "L=1100 two segments"),
 ]
 PATHS = [("walk", HELIX_BACKEND_AUTO, True), ("1pass", HELIX_BACKEND_AUTO, False),
-         ("fp32", HELIX_BACKEND_SGMMA, True)]
+         ("fp32", HELIX_BACKEND_SGMMA, True), ("walk/x6", HELIX_BACKEND_AUTO, True)]
 IOS = [HELIX_BF16, HELIX_F16]
 
 
@@ -107,9 +107,11 @@ def test_storage_matrix(gpu, shape, path, io):
     p = rounded(po.problem_harness(*shape[:6], 4242, "long"), io)
     p.s0 = np.random.default_rng(3).standard_normal(p.s0.shape).astype(np.float32) * 0.2
     y_ref, s_ref = po.scan(p, use_ids=False)
-    desc, y, s1 = run_io(gpu, p, io, backend, multipass)
+    # walk/x6: Pass A on six bf16 split products instead of two fp16 planes.
+    ctx = ctx_for(gpu, HELIX_PASSA_F16="0") if label == "walk/x6" else gpu
+    desc, y, s1 = run_io(ctx, p, io, backend, multipass)
     assert f"{NAME[io]} storage" in desc
-    assert ("chunk walk" in desc) == (label == "walk")
+    assert ("chunk walk" in desc) == label.startswith("walk")
     ey, es = check(io, desc, y, s1, y_ref, s_ref)
     print(f"{NAME[io]} {label} {shape[-1]}: y {ey:.2e} s1 {es:.2e}  [{desc}]", flush=True)
 

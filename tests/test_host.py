@@ -273,11 +273,15 @@ def test_16bit_storage_selection(host, io, name):
     d = mp(shape)
     d.io_dtype = io
     assert host.supported(d)
-    assert host.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
+    assert host.backend_desc(d) == (f"mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes), {name} storage "
+                                    f"(d_state<=128)")
     k = host.plan_info(d)
     assert (k.kernel_a, k.kernel_b, k.kernel_c) == (
-        f"helix_chunk_state_hb_x6agg_{name}io_n128".encode(), b"helix_state_scan_f32",
+        f"helix_chunk_state_hb_h3agg_{name}io_n128".encode(), b"helix_state_scan_f32",
         f"helix_scan_walk16_bf16_{name}io_n128".encode())
+    x6 = tuned(HELIX_PASSA_F16="0")         # six bf16 split products
+    assert x6.plan_info(d).kernel_a == f"helix_chunk_state_hb_x6agg_{name}io_n128".encode()
+    assert x6.backend_desc(d) == f"mfma bf16 pass C, chunk walk, pass A bf16x6, {name} storage (d_state<=128)"
     assert k.pass_b == abi.PASS_B_LAUNCHED
     x3 = tuned(HELIX_PASSA_SPLIT="3")       # Pass A on three split products: opt-in
     assert x3.plan_info(d).kernel_a == f"helix_chunk_state_hb_x3agg_{name}io_n128".encode()
