@@ -8,7 +8,9 @@
 // planes (NS = 3: six products, fp32 accuracy; NS = 2: three products, the
 // opt-in narrower state), issued smallest term first. The operand values, the
 // K order and the product order are those of pass_a_x6.hip, so the two kernels
-// produce the same segment aggregates.
+// produce the same segment aggregates. H16 (the bf16 path's default): two
+// fp16 planes of operands scaled by powers of two, three products on
+// v_mfma_f32_32x32x16_f16 (see hb_next_scale).
 //
 // What differs is how the work is laid out:
 //   - One workgroup of 2 * HELIX_HB waves owns HELIX_HB items that share a B/C

@@ -43,9 +43,11 @@ namespace {
 //     Pass C helix_scan_walk_x6_n{64,128}
 //   bf16 path (AUTO or MPP, multipass): Pass C walks each segment's chunks on
 //   bf16 MFMA with the state in registers; Pass A computes the segment
-//   aggregates only, on six split products (fp32 accuracy, the reference's
-//   contract for the carried state) or, opted into with HELIX_PASSA_SPLIT=3,
-//   on three.
+//   aggregates only, fp32-accurate (the reference's contract for the carried
+//   state): up to d_state 128 on three products of scaled fp16 planes
+//   (helix_chunk_state_hb_h3agg_{,bc_,bf16io_,f16io_}n*; HELIX_PASSA_F16=0
+//   keeps six bf16 split products), otherwise on six bf16 split products, or,
+//   opted into with HELIX_PASSA_SPLIT=3, on three.
 //     Pass A helix_chunk_state{_hb}_x{6,3}agg_n*     fp32 storage
 //            helix_chunk_state{_hb}_x{6,3}agg_bc_n*  ... also writes bf16 copies
 //                                                    of B and C for the walk
