@@ -299,7 +299,7 @@ HELIX_DEV int hb_off(int k, int r, int c) {
 
 // Split the L consecutive tokens' values v[0..L-1] of state index n into NS
 // planes and store them at tokens t .. t + L - 1 of row n (hb_off layout).
-// H16: two fp16 planes.
+// H16: two fp16 planes, or one where the scaled values are exact in fp16.
 template <int NP, int NS, int L, bool H16 = false>
 HELIX_DEV void hb_stage_run(__bf16* planes, int n, int t, const float* v) {
     static_assert(L == 2 || L == 4, "runs of two or four tokens");
@@ -307,7 +307,9 @@ HELIX_DEV void hb_stage_run(__bf16* planes, int n, int t, const float* v) {
 #pragma unroll
     for (int e = 0; e < L / 2; ++e) {
         unsigned w[3];
-        if constexpr (H16)
+        if constexpr (H16 && NS == 1)
+            w[0] = pk_f16(v[2 * e], v[2 * e + 1]);
+        else if constexpr (H16)
             split2h_pair(v[2 * e], v[2 * e + 1], w[0], w[1]);
         else if constexpr (NS == 3)
             split3_pair(v[2 * e], v[2 * e + 1], w[0], w[1], w[2]);
@@ -374,7 +376,12 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     static_assert(!H16 || (NS == 2 && MODE == 2 && !R64), "fp16 planes: aggregates");
     constexpr int HB = HELIX_HB;
     constexpr int NTN = NP / 32;        // 32-row n tiles per wave
-    constexpr int PLANES = NS * NP * HB_RS;
+    // B's planes. With fp16 planes and 16-bit storage one: a bf16 or f16 value
+    // (8 or 11 significant bits) scaled by a power of two is exact in fp16
+    // wherever it stays a normal number, so B's low plane would be zero and
+    // the products are a1 b0 + a0 b0.
+    constexpr int NSB = (H16 && sizeof(IO) == 2) ? 1 : NS;
+    constexpr int PLANES = NSB * NP * HB_RS;
     __shared__ __attribute__((aligned(16))) __bf16 sB[2 * PLANES];   // two chunks' planes
     // Per chunk parity and item: w_j of the chunk's 64 tokens, and L_end (fp64
     // bits) at [64], [65].
@@ -467,7 +474,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
                 v[i] = hb_b<NP, IO>(rows, i, k);
                 if constexpr (H16) v[i] = __builtin_ldexpf(v[i], kb[k]);
             }
-            hb_stage_run<NP, NS, L, H16>(planes, q4 + k, tr, v);
+            hb_stage_run<NP, NSB, L, H16>(planes, q4 + k, tr, v);
         }
     };
     // H16: the scales of the state indices of the chunk in `rows`, whose
@@ -569,11 +576,11 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     // R[n][p] += sum_j B^T[n][j] (w_j x[j][p]) over four K steps of 16 tokens,
     // in groups of two n tiles.
     constexpr int NG = NTN / 2;                 // groups of two n tiles per K step
-    auto read_group = [&](const __bf16* planes, int s, int i0, bf16x8 (&bp)[2][NS]) {
+    auto read_group = [&](const __bf16* planes, int s, int i0, bf16x8 (&bp)[2][NSB]) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int k = 0; k < NS; ++k)
+            for (int k = 0; k < NSB; ++k)
                 bp[i][k] = *reinterpret_cast<const bf16x8*>(&planes[hb_off<NP>(k, 32 * (i0 + i) + lo, 2 * s + hi)]);
     };
     auto read_w = [&](const float* __restrict__ wrow, int s, f32x4& w0, f32x4& w1) {
@@ -582,8 +589,14 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
     };
     // Smallest terms first, the two accumulators interleaved so no MFMA
     // waits on the one before it.
-    auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NS], const bf16x8 (&xp)[NS]) {
-        if constexpr (H16) {
+    auto mfma_group = [&](int i0, const bf16x8 (&bp)[2][NSB], const bf16x8 (&xp)[NS]) {
+        if constexpr (H16 && NSB == 1) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][0], xp[1], acc[i0 + i]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][0], xp[0], acc[i0 + i]);
+            return;
+        } else if constexpr (H16) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) acc[i0 + i] = mfma_f16(bp[i][1], xp[0], acc[i0 + i]);
 #pragma unroll
@@ -709,7 +722,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         // The B planes of the next group and the weights of the next K step
         // are read from LDS while the current group's MFMAs run, so no MFMA
         // waits on the LDS.
-        bf16x8 bq[2][2][NS];        // the B planes of two groups, in turn
+        bf16x8 bq[2][2][NSB];       // the B planes of two groups, in turn
         f32x4 w0, w1;
         read_group(cur, 0, 0, bq[0]);
         read_w(wrow, 0, w0, w1);
@@ -848,7 +861,7 @@ __device__ __forceinline__ void chunk_state_hb_impl(const HelixScanParams& p, co
         chunk_scales(n_loop, wrow);
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-            bf16x8 bq[2][2][NS];
+            bf16x8 bq[2][2][NSB];
             read_group(cur, 0, 2 * gi, bq[0]);
 #pragma unroll
             for (int s = 0; s < 4; ++s) {

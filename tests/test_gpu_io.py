@@ -128,6 +128,38 @@ def test_storage_ids(gpu, path, io):
     check(io, desc, y, s1, y_ref, s_ref)
 
 
+RANGES = ["rows spread", "channels spread", "spikes"]
+
+
+@pytest.mark.parametrize("kind", RANGES)
+@pytest.mark.parametrize("io", IOS, ids=["bf16", "f16"])
+def test_storage_ranges(gpu, io, kind):
+    """16-bit storage on the bf16 path, where Pass A keeps one fp16 plane of B
+    (the scaled bf16 or f16 value is exact in it): B's state indices spread
+    over eight decades, x's channels over six, or single-token spikes late in
+    a segment, within the storage type's range; s1 at the fp32 bound (its
+    absolute term scaled with the largest reference value)."""
+    p = po.problem_harness(1100, 2, 8, 64, 128, 2, 91, "long")
+    rng = np.random.default_rng(91)
+    if kind == "rows spread":
+        p.B *= (10.0 ** rng.uniform(-4, 4, p.B.shape[-1])).astype(np.float32)
+    elif kind == "channels spread":
+        p.x *= (10.0 ** rng.uniform(-3, 3, p.x.shape[-1])).astype(np.float32)
+    else:
+        p.x[:, 300, :, 5] *= np.float32(2e3)
+        p.B[:, 200, :, 11] *= np.float32(2e3)
+    p = rounded(p, io)
+    p.s0 = (rng.standard_normal(p.s0.shape) * 0.3).astype(np.float32)
+    y_ref, s_ref = po.scan(p, use_ids=False)
+    desc, y, s1 = run_io(gpu, p, io, HELIX_BACKEND_AUTO, True)
+    assert "fp16x3" in desc
+    assert np.all(np.isfinite(y)) and np.all(np.isfinite(s1))
+    ry = po.allclose_ratio(y, y_ref, BF16_REL, BF16_ABS * max(1.0, float(np.max(np.abs(y_ref)))))
+    rs = po.allclose_ratio(s1, s_ref, F32_REL, F32_ABS * max(1.0, float(np.max(np.abs(s_ref)))))
+    print(f"{NAME[io]} {kind}: y ratio {ry:.3f} s1 ratio {rs:.3f}", flush=True)
+    assert ry <= 1.0 and rs <= 1.0, (ry, rs)
+
+
 @pytest.mark.parametrize("io", IOS, ids=["bf16", "f16"])
 @pytest.mark.parametrize("name", ["cfg2", "cfg4a"])
 def test_storage_baseline_config(gpu, name, io):
