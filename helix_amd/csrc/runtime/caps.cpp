@@ -215,7 +215,8 @@ struct TraitTable {
                     t.name = keep(std::string("mfma bf16 pass C, chunk walk, pass A fp16x3 (scaled planes)") +
                                   (io == 1 ? ", bf16 storage" : io == 2 ? ", f16 storage" : "") + " (d_state<=" + np + ")");
                     t.k_chunk_state = kernel(std::string("helix_chunk_state_hb_h3agg_") + (bc ? "bc_" : kIoTag[io]) + "n" + np);
-                    t.mfma_a = "v_mfma_f32_32x32x16_f16 (two scaled fp16 planes, three products)";
+                    t.mfma_a = io ? "v_mfma_f32_32x32x16_f16 (one scaled fp16 plane of B, two of x: two products)"
+                                  : "v_mfma_f32_32x32x16_f16 (two scaled fp16 planes, three products)";
                 }
         // What helix_ctx_backend_desc reports for a descriptor run as blocks
         // of state indices on these kernels.
@@ -254,8 +255,9 @@ bool bccopy_on(const helix_tuning& tu, const helix_scan_desc& d, bool block) {
     // at 8 (config 2) the walk reading the fp32 rows itself is 3 us faster.
     // Blocks of state indices: at config 2's shape with d_state 256 in two
     // blocks of 128, the walks reading their columns of the caller's rows took
-    // 81 and 103 us, on the copies 66-68 and 76-78 us, for 11-13 us more per
-    // Pass A (294-296 against 275-283 us a scan, three processes).
+    // 81 and 103 us, on the copies 69 and 79 us, for 15 us more per Pass A
+    // (0.279 against 0.273 ms a scan; 9 us and 0.297 against 0.280 ms with
+    // the six-product Pass A).
     if (d.d_state <= 128) return tu.bccopy == 1 || K > 8 || block;
     return (64 + K - 1) / K * (d.d_state / 4) <= 2 * 256;
 }
