@@ -7,7 +7,10 @@ as blocks of state indices), SHORT or LONG memory and a nonzero s0; shapes
 whose oracle would take more than about a second are drawn again. The bf16
 path (Pass A on scaled fp16 planes by default), the fp32 path and the single
 pass are held to the reference's per-element bounds (y at the bf16 bound on the
-bf16 path, s1 at the fp32 bound everywhere).
+bf16 path, s1 at the fp32 bound everywhere). Every other shape also runs with
+x, B, C and y in bf16 and f16 storage on the walk, the fp32 path and the single
+pass, against the oracle fed the same inputs rounded to the storage type, to the
+bounds of the storage tests (test_gpu_io.check).
 """
 from __future__ import annotations
 
@@ -15,8 +18,9 @@ import numpy as np
 import pytest
 
 from oracle import pyoracle as po
-from helix_amd.desc import HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA
+from helix_amd.desc import HELIX_BACKEND_AUTO, HELIX_BACKEND_MPP, HELIX_BACKEND_SGMMA, HELIX_BF16, HELIX_F16
 from gpu_harness import BF16_ABS, BF16_REL, F32_ABS, F32_REL, run
+from test_gpu_io import NAME, check, rounded, run_io
 
 pytestmark = pytest.mark.gpu
 
@@ -63,3 +67,32 @@ def test_random_shape(gpu, case, path):
           f"[{gpu.backend_desc(d)}]", flush=True)
     assert np.all(np.isfinite(y)) and np.all(np.isfinite(s1))
     assert ry <= 1.0 and rs <= 1.0, (ry, rs)
+
+
+IO_CASES = CASES[::2]
+IO_PATHS = [("walk", HELIX_BACKEND_AUTO, True), ("fp32", HELIX_BACKEND_SGMMA, True), ("1pass", HELIX_BACKEND_AUTO, False)]
+_io_refs = {}
+
+
+def _io_problem(case, io):
+    """The case's inputs rounded to the storage type and the oracle's result on them (kept per case)."""
+    key = (case, io)
+    if key not in _io_refs:
+        L, S, H, P, N, G, memory, seed = case
+        p = rounded(po.problem_harness(L, S, H, P, N, G, seed % 100000, memory), io)
+        p.s0 = (np.random.default_rng(seed).standard_normal(p.s0.shape) * 0.3).astype(np.float32)
+        _io_refs.clear()
+        _io_refs[key] = (p, *po.scan(p, threads=0))
+    return _io_refs[key]
+
+
+@pytest.mark.parametrize("path", IO_PATHS, ids=[p[0] for p in IO_PATHS])
+@pytest.mark.parametrize("io", [HELIX_BF16, HELIX_F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("case", IO_CASES, ids=[f"L{c[0]}-S{c[1]}-H{c[2]}-P{c[3]}-N{c[4]}-G{c[5]}-{c[6]}" for c in IO_CASES])
+def test_random_shape_storage(gpu, case, io, path):
+    label, backend, multipass = path
+    p, y_ref, s_ref = _io_problem(case, io)
+    desc, y, s1 = run_io(gpu, p, io, backend, multipass)
+    assert f"{NAME[io]} storage" in desc
+    ey, es = check(io, desc, y, s1, y_ref, s_ref)
+    print(f"{NAME[io]} {label} {case[:7]}: y {ey:.2e} s1 {es:.2e}  [{desc}]", flush=True)
